@@ -1,0 +1,315 @@
+"""Encode and apply updates on an MI355X (gfx950) through the native library.
+
+Mirrors the reference's codec module (src/crukx_sync/codec.py): `encode`, `apply`, `checksum`,
+`bits16`, `exponents`, `huffman_lengths`, `canonical_codes` and the `_SLAB` knob keep their names
+and meaning. The work runs in hand-written HIP kernels (crukx-sync_amd/csrc); this module only
+checks arguments, resolves names to tensors, manages checksum caches and device memory.
+
+Tensors may live on a HIP device or on the CPU; CPU tensors are staged through the current HIP
+device (there is no CPU implementation in the product, and without a HIP device the calls fail).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Mapping
+
+import torch
+
+from . import _native
+from .wire import (BLOCK, MAX_CODE_LEN, MAX_RICE, MAX_SYMBOL, CorruptUpdate, Group, ParsedUpdate,  # noqa: F401
+                   Table, TensorHeader, Update, new_bytes, parse, serialize)
+
+_MASK64 = (1 << 64) - 1
+# Elements ranked by one wavefront (a multiple of 128, at most 2^17).  The reference's _SLAB bounds
+# the size of one stable sort (codec.py:30); here it cuts tensors into slabs whose exponent
+# histograms are scanned afterwards.  Either way it changes how work is split, never the bytes.
+_SLAB = 1 << 16
+
+
+# ---------------------------------------------------------------- shared helpers
+
+def bits16(name: str, t: torch.Tensor) -> torch.Tensor:
+    """Flat int16 view of a bf16 (or int16 bit-pattern) tensor (codec.py:35-41)."""
+    if not isinstance(t, torch.Tensor) or t.dtype not in (torch.bfloat16, torch.int16):
+        raise ValueError(f"{name}: expected a bfloat16 or int16 torch tensor, got {getattr(t, 'dtype', type(t))}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: tensor must be contiguous")
+    return t.view(torch.int16).view(-1)
+
+
+def exponents(a: torch.Tensor) -> torch.Tensor:
+    return ((a >> 7) & 0xFF).long()
+
+
+def _hip_device(dev: torch.device) -> torch.device:
+    if dev.type == "cuda":
+        return dev
+    if not torch.cuda.is_available():
+        raise RuntimeError("crukx_sync needs a HIP (ROCm) device: the codec runs only in its gfx950 kernels")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def checksum(a: torch.Tensor) -> int:
+    """sum(u_i * w_i) mod 2^64 over the uint16 bits u_i, w_i = splitmix64(i) | 1 (codec.py:61-68)."""
+    a = bits16("tensor", a)
+    dev = _hip_device(a.device)
+    if a.device != dev:
+        a = a.to(dev)
+    L = _native.lib()
+    ws = _native.Workspace(dev)
+    out = ctypes.c_uint64()
+    err = _native.errbuf()
+    with torch.cuda.device(dev):
+        rc = L.crx_checksum(a.data_ptr(), a.numel(), _native.stream_of(dev), ws.fn, None, ctypes.byref(out), err, 512)
+    ws.check()
+    _native.raise_for(rc, err)
+    return out.value
+
+
+def huffman_lengths(counts: list[int]) -> list[int]:
+    """Huffman code lengths limited to MAX_CODE_LEN (codec.py:71-78), computed natively."""
+    n = len(counts)
+    c = (ctypes.c_uint64 * n)(*counts)
+    out = (ctypes.c_int32 * n)()
+    _native.raise_for(_native.lib().crx_huffman_lengths(c, n, out), None)
+    return list(out)
+
+
+def canonical_codes(lengths: list[int]) -> list[int]:
+    """Canonical codes, assigned in order of (length, position in the table) (codec.py:101-111)."""
+    n = len(lengths)
+    L = (ctypes.c_int32 * n)(*lengths)
+    out = (ctypes.c_uint32 * n)()
+    _native.raise_for(_native.lib().crx_canonical_codes(L, n, out), None)
+    return list(out)
+
+
+def rice_parameter(count: int, gap_sum: int, shifted_sums) -> int:
+    """The Rice parameter of one group from its sums (codec.py:268-275): `shifted_sums(r)` must
+    return sum(gap >> r) over the group's gaps."""
+    L = _native.lib()
+    cand = (ctypes.c_int32 * 3)()
+    L.crx_rice_candidates(count, gap_sum, cand)
+    sh = (ctypes.c_uint64 * 3)(*[shifted_sums(c) for c in cand])
+    return L.crx_rice_choose(count, cand, sh)
+
+
+# ---------------------------------------------------------------- encoder
+
+class EncodedUpdate(Update):
+    """An update encoded on the device: header on the host, block table and payload in HBM."""
+
+    def __init__(self, handle, names: list[str], device, workspace):
+        self._h = handle
+        self._free = _native.lib().crx_encoded_free
+        self._names = [n.encode() for n in names]
+        self._device = device
+        self._ws = workspace  # keeps the device buffers alive
+        self._tensors = None
+
+    def __del__(self):
+        h, self._h = getattr(self, "_h", None), None
+        if h:
+            self._free(h)
+
+    def _name_args(self):
+        arr = (ctypes.c_char_p * max(len(self._names), 1))(*self._names)
+        lens = _native.u64_array([len(n) for n in self._names])
+        return arr, lens
+
+    def nbytes(self) -> int:
+        arr, lens = self._name_args()
+        return _native.lib().crx_encoded_size(self._h, arr, lens)
+
+    def _serialize_native(self) -> bytes:
+        n = self.nbytes()
+        data, addr = new_bytes(n)
+        self._write(addr, False)
+        return data
+
+    def to_device(self) -> torch.Tensor:
+        """The serialized update as a uint8 tensor on the encoding device."""
+        out = torch.empty(self.nbytes(), dtype=torch.uint8, device=self._device)
+        self._write(out.data_ptr(), True)
+        return out
+
+    def _write(self, addr: int, on_device: bool) -> None:
+        arr, lens = self._name_args()
+        err = _native.errbuf()
+        with torch.cuda.device(self._device):
+            rc = _native.lib().crx_encoded_write(self._h, arr, lens, addr, 1 if on_device else 0,
+                                                 _native.stream_of(self._device), err, 512)
+        _native.raise_for(rc, err)
+
+    @property
+    def tensors(self) -> list[TensorHeader]:
+        if self._tensors is None:
+            L = _native.lib()
+            e, cnt, r = ctypes.c_int32(), ctypes.c_uint64(), ctypes.c_int32()
+            out = []
+            for t, name in enumerate(self._names):
+                if not L.crx_encoded_present(self._h, t):
+                    continue
+                groups = []
+                for g in range(L.crx_encoded_n_groups(self._h, t)):
+                    L.crx_encoded_group(self._h, t, g, ctypes.byref(e), ctypes.byref(cnt), ctypes.byref(r))
+                    groups.append(Group(e.value, cnt.value, r.value))
+                out.append(TensorHeader(name.decode(), self._numels[t], L.crx_encoded_checksum(self._h, t), groups))
+            self._tensors = out
+        return self._tensors
+
+    @tensors.setter
+    def tensors(self, v):
+        self._tensors = v
+
+    @property
+    def tables(self) -> list[Table]:
+        L = _native.lib()
+        e, n = ctypes.c_int32(), ctypes.c_int64()
+        out = []
+        for i in range(L.crx_encoded_n_tables(self._h)):
+            L.crx_encoded_table(self._h, i, ctypes.byref(e), ctypes.byref(n), None, None)
+            syms, lens = (ctypes.c_uint32 * n.value)(), (ctypes.c_uint8 * n.value)()
+            L.crx_encoded_table(self._h, i, ctypes.byref(e), ctypes.byref(n), syms, lens)
+            out.append(Table(e.value, list(syms), list(lens)))
+        return out
+
+    @tables.setter
+    def tables(self, v):
+        pass
+
+    @property
+    def block_bits(self) -> list[int]:
+        L = _native.lib()
+        n = L.crx_encoded_n_blocks(self._h)
+        arr = (ctypes.c_uint32 * max(n, 1))()
+        with torch.cuda.device(self._device):
+            _native.raise_for(L.crx_encoded_block_bits(self._h, arr, _native.stream_of(self._device)), None)
+        return list(arr[:n])
+
+    @block_bits.setter
+    def block_bits(self, v):
+        pass
+
+    @property
+    def payload(self) -> bytes:
+        L = _native.lib()
+        n = L.crx_encoded_payload_len(self._h)
+        data, addr = new_bytes(n)
+        with torch.cuda.device(self._device):
+            _native.raise_for(L.crx_encoded_payload(self._h, addr, _native.stream_of(self._device)), None)
+        return data
+
+    @payload.setter
+    def payload(self, v):
+        pass
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """32-bit aligned storage: the kernels read pairs of bf16 as one word."""
+    return t if t.data_ptr() % 4 == 0 else t.clone()
+
+
+def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
+           checksums: dict[str, int] | None = None) -> tuple[Update, dict[str, int]]:
+    """The update, and the new checksums for the caller to commit once the update is serialized
+    (codec.py:278-420)."""
+    pairs = {}
+    for name in old:
+        a, b = bits16(name, old[name]), bits16(name, new[name])
+        if a.shape != b.shape:
+            raise ValueError(f"{name}: old and new differ in shape")
+        pairs[name] = (a, b)
+    if not pairs:
+        return Update([], []), {}
+    if len({t.device for ab in pairs.values() for t in ab}) != 1:
+        raise ValueError("all tensors must be on one device")
+    src = next(iter(pairs.values()))[0].device
+    dev = _hip_device(src)
+    names = list(pairs)
+    A, B = [], []
+    for a, b in pairs.values():
+        if a.device != dev:
+            a, b = a.to(dev), b.to(dev)
+        A.append(_aligned(a))
+        B.append(_aligned(b))
+    has = [1 if checksums is not None and n in checksums else 0 for n in names]
+    vals = [(checksums[n] & _MASK64) if h else 0 for n, h in zip(names, has)]
+    L = _native.lib()
+    ws = _native.Workspace(dev)
+    err = _native.errbuf()
+    h = ctypes.c_void_p()
+    with torch.cuda.device(dev):
+        rc = L.crx_encode(len(names), _native.ptr_array([a.data_ptr() for a in A]),
+                          _native.ptr_array([b.data_ptr() for b in B]), _native.u64_array([a.numel() for a in A]),
+                          _native.i32_array(has), _native.u64_array(vals), int(_SLAB),
+                          _native.stream_of(dev), ws.fn, None, ctypes.byref(h), err, 512)
+    ws.check()
+    _native.raise_for(rc, err)
+    upd = EncodedUpdate(h.value, names, dev, ws)
+    upd._numels = [a.numel() for a in A]
+    new_checksums = {n: L.crx_encoded_checksum(h.value, t) for t, n in enumerate(names)
+                     if L.crx_encoded_present(h.value, t)}
+    return upd, new_checksums
+
+
+# ---------------------------------------------------------------- apply
+
+def _cache_get(checksums, name, t):
+    """A cached checksum, trusted only if the tensor was not modified since it was recorded
+    (codec.py:457-460)."""
+    hit = checksums.get(name) if checksums is not None else None
+    return hit[0] if isinstance(hit, tuple) and hit[1] == t._version else None
+
+
+def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None = None) -> int:
+    """Verify `u` against `weights`, then write the new values in place. Returns elements changed
+    (codec.py:578-717)."""
+    if not isinstance(u, ParsedUpdate):
+        u = parse(serialize(u))
+    headers = u.tensors
+    if not headers:
+        return 0
+    targets = []
+    for h in headers:
+        if h.name not in weights:
+            raise ValueError(f"update has tensor {h.name!r} that the receiver does not have")
+        a = bits16(h.name, weights[h.name])
+        if a.numel() != h.numel:
+            raise ValueError(f"{h.name}: update is for {h.numel} elements, receiver has {a.numel()}")
+        targets.append(a)
+    src = targets[0].device
+    if any(a.device != src for a in targets):
+        raise ValueError("all updated tensors must be on one device")
+    dev = _hip_device(src)
+    staged = [a.to(dev) for a in targets] if src != dev else targets
+    cache = [_cache_get(checksums, h.name, weights[h.name]) for h in headers]
+    has = [0 if c is None else 1 for c in cache]
+    vals = [0 if c is None else c & _MASK64 for c in cache]
+    payload_dev = 0
+    if u._payload_dev is not None:
+        pd = u._payload_dev
+        if pd.device != dev:
+            pd = pd.to(dev)
+        payload_dev = pd.data_ptr()
+    L = _native.lib()
+    ws = _native.Workspace(dev)
+    err = _native.errbuf()
+    changed = ctypes.c_uint64()
+    with torch.cuda.device(dev):
+        rc = L.crx_apply(u.handle, payload_dev or None, _native.ptr_array([a.data_ptr() for a in staged]),
+                         _native.u64_array([a.numel() for a in staged]), _native.i32_array(has),
+                         _native.u64_array(vals), int(_SLAB), _native.stream_of(dev), ws.fn, None,
+                         ctypes.byref(changed), err, 512)
+    ws.check()
+    ws.release()
+    _native.raise_for(rc, err)
+    for h, a, s in zip(headers, targets, staged):
+        if s is not a:
+            a.copy_(s)  # an in-place op: bumps the tensor's version like index_put_ does
+        else:
+            torch.autograd.graph.increment_version(weights[h.name])
+    if checksums is not None:  # record the version after our own write
+        checksums.update({h.name: (h.checksum, weights[h.name]._version) for h in headers})
+    return changed.value

@@ -1,0 +1,884 @@
+// Host orchestration of the gfx950 update codec and the C ABI (include/crukx.h).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/crukx.h"
+#include "format.h"
+#include "kernels.h"
+
+namespace crx {
+
+#define HIP_OK(call)                                                                              \
+    do {                                                                                          \
+        hipError_t e_ = (call);                                                                   \
+        if (e_ != hipSuccess)                                                                     \
+            throw DeviceError(std::string(#call) + ": " + hipGetErrorString(e_));                 \
+    } while (0)
+
+// ------------------------------------------------------------------ timing
+namespace {
+struct Pending {
+    std::string name;
+    hipEvent_t a, b;
+};
+struct Stat {
+    int64_t calls = 0;
+    double ms = 0;
+};
+std::mutex g_tmu;
+bool g_timing = false;
+hipEvent_t g_open = nullptr;
+std::vector<Pending> g_pending;
+std::map<std::string, Stat> g_stats;
+
+void timing_collect() {
+    std::lock_guard<std::mutex> lk(g_tmu);
+    for (Pending &p : g_pending) {
+        float ms = 0;
+        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            g_stats[p.name].calls++;
+            g_stats[p.name].ms += ms;
+        }
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    g_pending.clear();
+}
+}  // namespace
+
+void timing_begin(hipStream_t s) {
+    if (!g_timing) return;
+    std::lock_guard<std::mutex> lk(g_tmu);
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return;
+    (void)hipEventRecord(e, s);
+    g_open = e;
+}
+
+void timing_end(const char *name, hipStream_t s) {
+    if (!g_timing) return;
+    std::lock_guard<std::mutex> lk(g_tmu);
+    if (!g_open) return;
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return;
+    (void)hipEventRecord(e, s);
+    g_pending.push_back(Pending{name, g_open, e});
+    g_open = nullptr;
+}
+
+// ------------------------------------------------------------------ workspace
+struct Arena {
+    crx_alloc_fn fn;
+    void *ctx;
+    template <typename T>
+    T *get(uint64_t count) {
+        uint64_t bytes = std::max<uint64_t>(count * sizeof(T), 16);
+        bytes = (bytes + 255) & ~uint64_t(255);
+        void *p = fn(ctx, bytes);
+        if (!p) throw std::bad_alloc();
+        return static_cast<T *>(p);
+    }
+};
+
+template <typename T>
+void h2d(T *dst, const T *src, uint64_t n, hipStream_t s) {
+    if (n) HIP_OK(hipMemcpyAsync(dst, src, n * sizeof(T), hipMemcpyHostToDevice, s));
+}
+template <typename T>
+void d2h(T *dst, const T *src, uint64_t n, hipStream_t s) {
+    if (n) HIP_OK(hipMemcpyAsync(dst, src, n * sizeof(T), hipMemcpyDeviceToHost, s));
+}
+template <typename T>
+void zero(T *dst, uint64_t n, hipStream_t s) {
+    if (n) HIP_OK(hipMemsetAsync(dst, 0, n * sizeof(T), s));
+}
+void sync(hipStream_t s) { HIP_OK(hipStreamSynchronize(s)); }
+
+uint32_t slab_size(int32_t slab) {
+    if (slab <= 0) return 65536;
+    uint32_t s = (uint32_t)slab;
+    s = std::max<uint32_t>(kRow, std::min<uint32_t>(s, 1u << 17));
+    return s / kRow * kRow;
+}
+
+// Slab layout and the chunking of the per-tensor histogram scan.
+struct Layout {
+    std::vector<TensorDesc> descs;
+    std::vector<int32_t> call_index;  // descriptor -> caller's tensor index
+    uint32_t tiles = 0;
+    std::vector<ScanChunk> chunks;
+    std::vector<uint32_t> tensor_chunk_begin;
+};
+
+void finish_layout(Layout &L, uint32_t slab) {
+    L.tiles = 0;
+    L.chunks.clear();
+    L.tensor_chunk_begin.assign(1, 0);
+    for (uint32_t t = 0; t < L.descs.size(); ++t) {
+        TensorDesc &d = L.descs[t];
+        uint64_t nt = (d.numel + slab - 1) / slab;
+        if ((uint64_t)L.tiles + nt >= (1ULL << 31)) throw Invalid("too many slabs; raise the slab size");
+        d.tile_begin = L.tiles;
+        d.n_tiles = (uint32_t)nt;
+        L.tiles += (uint32_t)nt;
+        for (uint32_t c = 0; c < nt; c += kScanTiles)
+            L.chunks.push_back(
+                ScanChunk{d.tile_begin + c, d.tile_begin + std::min<uint32_t>(c + kScanTiles, (uint32_t)nt), t, 0});
+        L.tensor_chunk_begin.push_back((uint32_t)L.chunks.size());
+    }
+}
+
+TensorDesc make_desc(const uint16_t *p, uint64_t numel) {
+    if (((uintptr_t)p) & 1) throw Invalid("tensor data must be 2-byte aligned");
+    if (numel >= (1ULL << 32)) throw Invalid("tensors of 2^32 or more elements are not supported");
+    TensorDesc d{};
+    d.frame = reinterpret_cast<const uint32_t *>((uintptr_t)p & ~uintptr_t(3));
+    d.lead = (uint32_t)(((uintptr_t)p & 3) >> 1);
+    d.base = const_cast<uint16_t *>(p);
+    d.numel = numel;
+    return d;
+}
+
+// Device copies of the scan chunking.
+struct ScanDev {
+    ScanChunk *chunks;
+    uint32_t *tcb, *csum;
+    uint32_t n_chunks;
+};
+
+ScanDev upload_scan(Arena &ar, const Layout &L, hipStream_t s) {
+    ScanDev sd;
+    sd.n_chunks = (uint32_t)L.chunks.size();
+    sd.chunks = ar.get<ScanChunk>(sd.n_chunks);
+    sd.tcb = ar.get<uint32_t>(L.tensor_chunk_begin.size());
+    sd.csum = ar.get<uint32_t>((uint64_t)sd.n_chunks * 256);
+    h2d(sd.chunks, L.chunks.data(), sd.n_chunks, s);
+    h2d(sd.tcb, L.tensor_chunk_begin.data(), L.tensor_chunk_begin.size(), s);
+    return sd;
+}
+
+}  // namespace crx
+
+using namespace crx;
+
+// ------------------------------------------------------------------ handles
+struct crx_update {
+    Update u;
+    std::vector<uint8_t> owned;  // empty: payload read from the caller's buffer
+};
+
+struct crx_encoded {
+    int32_t n = 0;
+    std::vector<int32_t> present;
+    std::vector<uint64_t> checksum;
+    std::vector<uint64_t> numel;
+    std::vector<Table> tables;
+    std::vector<std::vector<Group>> groups;  // per caller tensor
+    uint64_t n_blocks = 0;
+    const uint32_t *d_block_bits = nullptr;
+    uint64_t payload_len = 0;
+    const uint8_t *d_payload = nullptr;
+    uint64_t total_changes = 0;
+};
+
+namespace crx {
+namespace {
+
+void write_header(const crx_encoded &e, const char *const *names, const uint64_t *name_lens, std::vector<uint8_t> &out) {
+    out.clear();
+    out.insert(out.end(), {'C', 'R', 'X', 'S', kVersion});
+    put_varint(out, e.tables.size());
+    for (const Table &t : e.tables) {
+        out.push_back((uint8_t)t.exponent);
+        put_varint(out, t.symbols.size());
+        for (size_t k = 0; k < t.symbols.size(); ++k) {
+            put_varint(out, t.symbols[k]);
+            out.push_back(t.lengths[k]);
+        }
+    }
+    uint64_t n_present = 0;
+    for (int32_t t = 0; t < e.n; ++t) n_present += e.present[t] ? 1 : 0;
+    put_varint(out, n_present);
+    for (int32_t t = 0; t < e.n; ++t) {
+        if (!e.present[t]) continue;
+        put_varint(out, name_lens[t]);
+        out.insert(out.end(), names[t], names[t] + name_lens[t]);
+        put_varint(out, e.numel[t]);
+        for (int k = 0; k < 8; ++k) out.push_back((uint8_t)(e.checksum[t] >> (8 * k)));
+        put_varint(out, e.groups[t].size());
+        for (const Group &g : e.groups[t]) {
+            out.push_back((uint8_t)g.exponent);
+            put_varint(out, g.count);
+            out.push_back((uint8_t)g.rice);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ encode
+// codec.encode (codec.py:278-420) on the device.
+void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news, const uint64_t *numels,
+            const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab_req, hipStream_t s, Arena &ar,
+            crx_encoded &E) {
+    const uint32_t slab = slab_size(slab_req);
+    E.n = n;
+    E.present.assign(n, 0);
+    E.checksum.assign(n, 0);
+    E.numel.assign(numels, numels + n);
+    E.groups.assign(n, {});
+    Layout L;
+    uint64_t total_elems = 0;
+    for (int32_t t = 0; t < n; ++t) {
+        if (!numels[t]) continue;
+        TensorDesc d = make_desc(olds[t], numels[t]);
+        TensorDesc dn = make_desc(news[t], numels[t]);
+        if (dn.lead != d.lead) throw Invalid("old and new must have the same 4-byte alignment");
+        d.frame_new = dn.frame;
+        d.cold = (has_cache && has_cache[t]) ? 0u : 1u;
+        L.descs.push_back(d);
+        L.call_index.push_back(t);
+        total_elems += numels[t];
+    }
+    if (L.descs.empty()) return;
+    finish_layout(L, slab);
+    const uint32_t T = (uint32_t)L.descs.size(), tiles = L.tiles;
+
+    TensorDesc *d_descs = ar.get<TensorDesc>(T);
+    h2d(d_descs, L.descs.data(), T, s);
+    uint32_t *hall = ar.get<uint32_t>((uint64_t)tiles * 256), *hchg = ar.get<uint32_t>((uint64_t)tiles * 256);
+    uint64_t *delta = ar.get<uint64_t>(tiles), *full = ar.get<uint64_t>(tiles);
+    unsigned long long *cnt = ar.get<unsigned long long>(8);
+    ScanDev sd = upload_scan(ar, L, s);
+    uint32_t *tot_all = ar.get<uint32_t>((uint64_t)T * 256), *tot_chg = ar.get<uint32_t>((uint64_t)T * 256);
+    GroupDev *d_groups = ar.get<GroupDev>((uint64_t)T * 256);
+    uint32_t *gbase = ar.get<uint32_t>((uint64_t)T * 256);
+    unsigned long long *gcnt = ar.get<unsigned long long>(2);
+
+    uint64_t rec_cap = total_elems / 24 + 65536;
+    uint64_t *rec = nullptr;
+    Chunk *chunks = nullptr;
+    unsigned long long h[8];
+    for (int attempt = 0;; ++attempt) {
+        const uint64_t chunk_cap = tiles + rec_cap / (kRecCap - kRow) + 16;
+        rec = ar.get<uint64_t>(rec_cap);
+        chunks = ar.get<Chunk>(chunk_cap);
+        zero(cnt, 8, s);
+        EncRankArgs a{d_descs, T, slab, hall, hchg, rec, rec_cap, chunks, chunk_cap, cnt, delta, full};
+        launch_enc_rank(a, tiles, s);
+        d2h(h, cnt, 3, s);
+        sync(s);
+        if (!h[2]) break;
+        if (attempt) throw DeviceError("change records overflowed twice");
+        rec_cap = h[0] + 1;  // exact count of the first attempt
+    }
+    launch_scan_tables(hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_all, s);
+    launch_scan_tables(hchg, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_chg, s);
+    launch_enc_groups(tot_chg, T, d_groups, gbase, gcnt, s);
+    unsigned long long gc[2];
+    d2h(gc, gcnt, 2, s);
+    sync(s);
+    const uint64_t G = gc[0], C = gc[1];
+    E.total_changes = C;
+    if (C == 0) return;
+    if (C >= (1ULL << 32)) throw Invalid("2^32 or more changes in one update are not supported");
+
+    uint64_t *sorted = ar.get<uint64_t>(C);
+    launch_place(chunks, (uint32_t)h[1], rec, d_descs, T, hall, hchg, gbase, sorted, C, s);
+    launch_r0(d_groups, (uint32_t)G, sorted, s);
+    uint32_t *dense = ar.get<uint32_t>(256 * kDense);
+    uint32_t *rare = ar.get<uint32_t>(C);
+    unsigned long long *scnt = ar.get<unsigned long long>(2);
+    unsigned long long *cost = ar.get<unsigned long long>(G * 3);
+    uint64_t *t_delta = ar.get<uint64_t>(T), *t_full = ar.get<uint64_t>(T);
+    zero(dense, 256 * kDense, s);
+    zero(scnt, 2, s);
+    zero(cost, G * 3, s);
+    StatsArgs st{sorted, C, d_groups, (uint32_t)G, dense, rare, C, scnt, cost};
+    launch_stats(st, s);
+    launch_tensor_sums(d_descs, T, delta, t_delta, s);
+    launch_tensor_sums(d_descs, T, full, t_full, s);
+
+    std::vector<GroupDev> groups(G);
+    std::vector<unsigned long long> hcost(G * 3);
+    std::vector<uint32_t> hdense(256 * kDense);
+    std::vector<uint64_t> hdelta(T), hfull(T);
+    unsigned long long hs[2];
+    d2h(groups.data(), d_groups, G, s);
+    d2h(hcost.data(), cost, G * 3, s);
+    d2h(hdense.data(), dense, 256 * kDense, s);
+    d2h(hdelta.data(), t_delta, T, s);
+    d2h(hfull.data(), t_full, T, s);
+    d2h(hs, scnt, 2, s);
+    sync(s);
+    if (hs[1]) throw DeviceError("rare symbol list overflowed");
+    std::vector<uint32_t> hrare(hs[0]);
+    d2h(hrare.data(), rare, hs[0], s);
+    sync(s);
+    std::sort(hrare.begin(), hrare.end());
+
+    // checksums (codec.py:344-352) and groups / Rice parameters (codec.py:354-360)
+    for (uint32_t d = 0; d < T; ++d) {
+        const int32_t t = L.call_index[d];
+        E.checksum[t] = (has_cache && has_cache[t]) ? cache_vals[t] + hdelta[d] : hfull[d];
+    }
+    uint64_t blk = 0;
+    for (uint64_t g = 0; g < G; ++g) {
+        GroupDev &gr = groups[g];
+        const int c[3] = {(int)(gr.r0 ? gr.r0 - 1 : 0), (int)gr.r0, (int)std::min<uint32_t>(gr.r0 + 1, kMaxRice)};
+        const uint64_t sh[3] = {hcost[g * 3], hcost[g * 3 + 1], hcost[g * 3 + 2]};
+        gr.rice = (uint32_t)rice_choose(gr.count, c, sh);
+        gr.blk_base = (uint32_t)blk;
+        blk += n_blocks(gr.count);
+        const int32_t t = L.call_index[gr.tensor];
+        E.present[t] = 1;
+        E.groups[t].push_back(Group{(int)gr.exponent, gr.count, (int)gr.rice});
+    }
+    const uint64_t B = blk;
+    E.n_blocks = B;
+
+    // one canonical Huffman table per exponent, symbols ascending (codec.py:369-392)
+    std::vector<uint32_t> lut(256 * kDense, 0), rkeys, rvals;
+    size_t ri = 0;
+    for (int e = 0; e < 256; ++e) {
+        std::vector<uint32_t> syms;
+        std::vector<uint64_t> counts;
+        for (int z = 0; z < kDense; ++z)
+            if (hdense[e * kDense + z]) {
+                syms.push_back(z);
+                counts.push_back(hdense[e * kDense + z]);
+            }
+        while (ri < hrare.size() && (int)(hrare[ri] >> 17) == e) {
+            const uint32_t z = hrare[ri] & 0x1FFFF;
+            uint64_t c = 0;
+            while (ri < hrare.size() && hrare[ri] == (((uint32_t)e << 17) | z)) {
+                ++c;
+                ++ri;
+            }
+            syms.push_back(z);
+            counts.push_back(c);
+        }
+        if (syms.empty()) continue;
+        std::vector<int> len = huffman_lengths(counts);
+        std::vector<uint32_t> code = canonical_codes(len);
+        Table tb;
+        tb.exponent = e;
+        tb.symbols = syms;
+        for (size_t k = 0; k < syms.size(); ++k) {
+            tb.lengths.push_back((uint8_t)len[k]);
+            const uint32_t v = (code[k] << 5) | (uint32_t)len[k];
+            if (syms[k] < (uint32_t)kDense) lut[e * kDense + syms[k]] = v;
+            else {
+                rkeys.push_back(((uint32_t)e << 17) | syms[k]);
+                rvals.push_back(v);
+            }
+        }
+        E.tables.push_back(std::move(tb));
+    }
+
+    GroupDev *d_groups2 = ar.get<GroupDev>(G);
+    uint32_t *d_lut = ar.get<uint32_t>(256 * kDense);
+    uint32_t *d_rk = ar.get<uint32_t>(rkeys.size()), *d_rv = ar.get<uint32_t>(rvals.size());
+    h2d(d_groups2, groups.data(), G, s);
+    h2d(d_lut, lut.data(), lut.size(), s);
+    h2d(d_rk, rkeys.data(), rkeys.size(), s);
+    h2d(d_rv, rvals.data(), rvals.size(), s);
+    const uint64_t n_wg = (C + kElemsPerWG - 1) / kElemsPerWG;
+    unsigned long long *wsum = ar.get<unsigned long long>(n_wg), *woff = ar.get<unsigned long long>(n_wg + 1);
+    CodeArgs ca{sorted, C, d_groups2, (uint32_t)G, d_lut, d_rk, d_rv, (uint32_t)rkeys.size(), wsum, woff, nullptr, nullptr};
+    launch_code_lengths(ca, s);
+    launch_scan_u64(wsum, n_wg, woff, s);
+    unsigned long long total_bits = 0;
+    d2h(&total_bits, woff + n_wg, 1, s);
+    sync(s);
+
+    const uint64_t n_words = (total_bits + 31) / 32 + 4;
+    uint32_t *words = ar.get<uint32_t>(n_words);
+    unsigned long long *bstart = ar.get<unsigned long long>(B + 1);
+    uint32_t *bb = ar.get<uint32_t>(B);
+    unsigned int *ovf = ar.get<unsigned int>(1);
+    zero(words, n_words, s);
+    zero(ovf, 1, s);
+    HIP_OK(hipMemcpyAsync(bstart + B, woff + n_wg, sizeof(unsigned long long), hipMemcpyDeviceToDevice, s));
+    ca.words = words;
+    ca.bstart = bstart;
+    launch_pack(ca, s);
+    launch_block_bits(bstart, B, bb, ovf, s);
+    unsigned int hovf = 0;
+    d2h(&hovf, ovf, 1, s);
+    sync(s);
+    if (hovf) throw Invalid("a block exceeds 2^32 bits; the update cannot be represented");
+    E.d_block_bits = bb;
+    E.payload_len = (total_bits + 7) / 8;
+    E.d_payload = reinterpret_cast<const uint8_t *>(words);
+}
+
+// ------------------------------------------------------------------ apply
+// codec.apply (codec.py:578-717) on the device: decode, locate, verify, then write.
+void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets, const uint64_t *numels,
+           const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab_req, hipStream_t s, Arena &ar,
+           uint64_t *changed) {
+    *changed = 0;
+    const uint32_t T = (uint32_t)u.tensors.size();
+    if (!T) return;
+    const uint32_t slab = slab_size(slab_req);
+    const uint64_t C = u.total_changes;
+    if (C >= (1ULL << 32)) throw Invalid("2^32 or more changes in one update are not supported");
+    Layout L;
+    for (uint32_t t = 0; t < T; ++t) {
+        if (numels[t] != u.tensors[t].numel) throw Invalid(u.tensors[t].name + ": numel mismatch");
+        TensorDesc d = make_desc(targets[t], numels[t]);
+        d.cold = (has_cache && has_cache[t]) ? 0u : 1u;
+        L.descs.push_back(d);
+        L.call_index.push_back((int32_t)t);
+    }
+    finish_layout(L, slab);
+    const uint32_t tiles = L.tiles;
+
+    // groups, decoding tables and the group lookup (codec.py:594-625)
+    int table_of[256];
+    std::fill(table_of, table_of + 256, -1);
+    std::vector<uint32_t> tab(u.tables.size() * 54, 0), syms;
+    for (size_t ti = 0; ti < u.tables.size(); ++ti) {
+        const Table &tb = u.tables[ti];
+        table_of[tb.exponent] = (int)ti;
+        uint32_t per_len[kMaxCodeLen + 1] = {};
+        for (uint8_t l : tb.lengths) per_len[l]++;
+        std::vector<uint32_t> order(tb.symbols.size());
+        for (size_t k = 0; k < order.size(); ++k) order[k] = (uint32_t)k;
+        std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return tb.lengths[a] < tb.lengths[b]; });
+        uint32_t code = 0, idx = (uint32_t)syms.size();
+        for (int l = 1; l <= kMaxCodeLen; ++l) {
+            tab[ti * 54 + l] = code;
+            tab[ti * 54 + 18 + l] = per_len[l];
+            tab[ti * 54 + 36 + l] = idx;
+            code = (code + per_len[l]) << 1;
+            idx += per_len[l];
+        }
+        for (uint32_t k : order) syms.push_back(tb.symbols[k]);
+    }
+    std::vector<GroupDev> groups;
+    std::vector<int32_t> group_of((uint64_t)T * 256, -1);
+    uint64_t elem = 0, blk = 0;
+    for (uint32_t t = 0; t < T; ++t)
+        for (const Group &g : u.tensors[t].groups) {
+            GroupDev gd{};
+            gd.tensor = t;
+            gd.exponent = (uint32_t)g.exponent;
+            gd.count = (uint32_t)g.count;
+            gd.elem_base = (uint32_t)elem;
+            gd.blk_base = (uint32_t)blk;
+            gd.rice = (uint32_t)g.rice;
+            gd.table = (uint32_t)table_of[g.exponent];
+            group_of[(uint64_t)t * 256 + g.exponent] = (int32_t)groups.size();
+            groups.push_back(gd);
+            elem += g.count;
+            blk += n_blocks(g.count);
+        }
+    const uint64_t G = groups.size(), B = blk;
+
+    TensorDesc *d_descs = ar.get<TensorDesc>(T);
+    h2d(d_descs, L.descs.data(), T, s);
+    uint32_t *hall = ar.get<uint32_t>((uint64_t)tiles * 256);
+    uint64_t *full = ar.get<uint64_t>(tiles), *t_full = ar.get<uint64_t>(T);
+    ScanDev sd = upload_scan(ar, L, s);
+    uint32_t *sizes = ar.get<uint32_t>((uint64_t)T * 256);
+    GroupDev *d_groups = ar.get<GroupDev>(G);
+    int32_t *d_gof = ar.get<int32_t>((uint64_t)T * 256);
+    uint32_t *d_tab = ar.get<uint32_t>(tab.size()), *d_syms = ar.get<uint32_t>(syms.size());
+    uint32_t *d_bb = ar.get<uint32_t>(B);
+    unsigned long long *boff = ar.get<unsigned long long>(B + 1);
+    const uint64_t pay_words = (u.payload_len + 7) / 8 + 2;
+    uint64_t *pay = ar.get<uint64_t>(pay_words);
+    h2d(d_groups, groups.data(), G, s);
+    h2d(d_gof, group_of.data(), group_of.size(), s);
+    h2d(d_tab, tab.data(), tab.size(), s);
+    h2d(d_syms, syms.data(), syms.size(), s);
+    h2d(d_bb, u.block_bits.data(), B, s);
+    zero(pay, pay_words, s);
+    if (u.payload_len) {
+        if (payload_dev)
+            HIP_OK(hipMemcpyAsync(pay, payload_dev, u.payload_len, hipMemcpyDeviceToDevice, s));
+        else
+            HIP_OK(hipMemcpyAsync(pay, u.payload_host, u.payload_len, hipMemcpyHostToDevice, s));
+    }
+
+    // pass A: receiver exponent histograms (+ full old checksums on a cache miss)
+    HistArgs ha{d_descs, T, slab, hall, full};
+    launch_hist(ha, tiles, s);
+    launch_scan_tables(hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, sizes, s);
+    launch_tensor_sums(d_descs, T, full, t_full, s);
+    launch_scan_u32(d_bb, B, boff, s);
+
+    uint32_t *zz = ar.get<uint32_t>(C), *local = ar.get<uint32_t>(C), *pos = ar.get<uint32_t>(C);
+    uint16_t *val = ar.get<uint16_t>(C);
+    unsigned long long *blk_sum = ar.get<unsigned long long>(B), *blk_prefix = ar.get<unsigned long long>(B + 1);
+    unsigned long long *tdelta = ar.get<unsigned long long>(T);
+    unsigned int *bad = ar.get<unsigned int>(1);
+    uint32_t *lb = ar.get<uint32_t>((uint64_t)tiles * 256);
+    zero(bad, 1, s);
+    zero(tdelta, T, s);
+    DecodeArgs da{pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, sizes, d_tab, d_syms, (uint32_t)syms.size(),
+                  zz, local, blk_sum, bad};
+    launch_decode(da, s);
+    launch_scan_u64(blk_sum, B, blk_prefix, s);
+    BlockArgs ba{d_groups, (uint32_t)G, d_descs, sizes, blk_prefix, local, zz, pos, val, tdelta, bad};
+    launch_local_fix(ba, B, s);
+    SelectArgs sa{d_descs, T, slab, hall, lb, d_gof, d_groups, local, pos, val, bad};
+    launch_locate(sa, tiles, s);
+    launch_select(sa, tiles, s);
+    launch_verify(ba, B, s);
+
+    unsigned int hbad = 0;
+    std::vector<unsigned long long> hdelta(T);
+    std::vector<uint64_t> hfull(T);
+    d2h(&hbad, bad, 1, s);
+    d2h(hdelta.data(), tdelta, T, s);
+    d2h(hfull.data(), t_full, T, s);
+    sync(s);
+    if (hbad & kBadDecode) throw Corrupt("payload does not decode to its block table");
+    if (hbad) throw Corrupt("payload positions outside their exponent groups");
+    std::vector<std::string> wrong;
+    for (uint32_t t = 0; t < T; ++t) {
+        const uint64_t old = (has_cache && has_cache[t]) ? cache_vals[t] : hfull[t];
+        if (old + hdelta[t] != u.tensors[t].checksum) wrong.push_back(u.tensors[t].name);
+    }
+    if (!wrong.empty()) {
+        std::string m = "update does not verify (checksum mismatch: ";
+        for (size_t i = 0; i < std::min<size_t>(3, wrong.size()); ++i) m += (i ? ", '" : "'") + wrong[i] + "'";
+        throw Corrupt(m + ")");
+    }
+    launch_scatter(ba, B, s);
+    sync(s);
+    *changed = C;
+}
+
+void full_checksum(const uint16_t *p, uint64_t n, hipStream_t s, Arena &ar, uint64_t *out) {
+    *out = 0;
+    if (!n) return;
+    TensorDesc d = make_desc(p, n);
+    const uint64_t words = (n + d.lead + 1) >> 1;
+    const uint32_t parts = (uint32_t)std::min<uint64_t>(2048, (words + 65535) / 65536);
+    uint64_t *partial = ar.get<uint64_t>(parts);
+    launch_checksum(d.frame, d.lead, n, partial, parts, s);
+    std::vector<uint64_t> h(parts);
+    d2h(h.data(), partial, parts, s);
+    sync(s);
+    for (uint64_t v : h) *out += v;
+}
+
+template <typename F>
+int32_t guarded(char *err, uint64_t errlen, F &&f) {
+    auto put = [&](const char *m) {
+        if (err && errlen) std::snprintf(err, (size_t)errlen, "%s", m);
+    };
+    try {
+        f();
+        if (g_timing) timing_collect();
+        return CRX_OK;
+    } catch (const Corrupt &e) {
+        put(e.what());
+        if (g_timing) timing_collect();
+        return CRX_CORRUPT;
+    } catch (const Invalid &e) {
+        put(e.what());
+        return CRX_INVALID;
+    } catch (const DeviceError &e) {
+        put(e.what());
+        return CRX_DEVICE;
+    } catch (const NeedMore &) {
+        put("need more bytes");
+        return CRX_INVALID;
+    } catch (const std::bad_alloc &) {
+        put("out of memory");
+        return CRX_NOMEM;
+    } catch (const std::exception &e) {
+        put(e.what());
+        return CRX_DEVICE;
+    }
+}
+
+}  // namespace
+}  // namespace crx
+
+// ------------------------------------------------------------------ C ABI
+extern "C" {
+
+int32_t crx_abi_version(void) { return CRX_ABI_VERSION; }
+
+int32_t crx_parse(const uint8_t *data, uint64_t len, crx_update **out, char *err, uint64_t errlen) {
+    *out = nullptr;
+    return guarded(err, errlen, [&] {
+        auto *h = new crx_update();
+        try {
+            parse(data, len, len, len ? data[len - 1] : 0, h->u);
+        } catch (...) {
+            delete h;
+            throw;
+        }
+        h->u.payload_host = data + h->u.payload_offset;
+        *out = h;
+    });
+}
+
+int32_t crx_parse_prefix(const uint8_t *prefix, uint64_t prefix_len, uint64_t total_len, uint8_t last_byte,
+                         crx_update **out, uint64_t *need, char *err, uint64_t errlen) {
+    *out = nullptr;
+    *need = 0;
+    try {
+        auto *h = new crx_update();
+        try {
+            parse(prefix, prefix_len, total_len, last_byte, h->u);
+        } catch (...) {
+            delete h;
+            throw;
+        }
+        h->u.payload_host = nullptr;
+        *out = h;
+        return CRX_OK;
+    } catch (const NeedMore &m) {
+        *need = m.need;
+        if (err && errlen) std::snprintf(err, (size_t)errlen, "need %llu bytes", (unsigned long long)m.need);
+        return CRX_INVALID;
+    } catch (const Corrupt &e) {
+        if (err && errlen) std::snprintf(err, (size_t)errlen, "%s", e.what());
+        return CRX_CORRUPT;
+    } catch (const std::bad_alloc &) {
+        return CRX_NOMEM;
+    } catch (const std::exception &e) {
+        if (err && errlen) std::snprintf(err, (size_t)errlen, "%s", e.what());
+        return CRX_INVALID;
+    }
+}
+
+void crx_update_free(crx_update *u) { delete u; }
+int64_t crx_update_n_tables(const crx_update *u) { return (int64_t)u->u.tables.size(); }
+
+int32_t crx_update_table(const crx_update *u, int64_t i, int32_t *exponent, int64_t *n_sym, uint32_t *symbols,
+                         uint8_t *lengths) {
+    if (i < 0 || (size_t)i >= u->u.tables.size()) return CRX_INVALID;
+    const Table &t = u->u.tables[i];
+    *exponent = t.exponent;
+    *n_sym = (int64_t)t.symbols.size();
+    if (symbols) std::copy(t.symbols.begin(), t.symbols.end(), symbols);
+    if (lengths) std::copy(t.lengths.begin(), t.lengths.end(), lengths);
+    return CRX_OK;
+}
+
+int64_t crx_update_n_tensors(const crx_update *u) { return (int64_t)u->u.tensors.size(); }
+
+int32_t crx_update_tensor(const crx_update *u, int64_t i, const uint8_t **name, uint64_t *name_len, uint64_t *numel,
+                          uint64_t *checksum, int32_t *n_groups) {
+    if (i < 0 || (size_t)i >= u->u.tensors.size()) return CRX_INVALID;
+    const TensorHeader &t = u->u.tensors[i];
+    *name = reinterpret_cast<const uint8_t *>(t.name.data());
+    *name_len = t.name.size();
+    *numel = t.numel;
+    *checksum = t.checksum;
+    *n_groups = (int32_t)t.groups.size();
+    return CRX_OK;
+}
+
+int32_t crx_update_group(const crx_update *u, int64_t i, int32_t g, int32_t *exponent, uint64_t *count, int32_t *rice) {
+    if (i < 0 || (size_t)i >= u->u.tensors.size()) return CRX_INVALID;
+    const TensorHeader &t = u->u.tensors[i];
+    if (g < 0 || (size_t)g >= t.groups.size()) return CRX_INVALID;
+    *exponent = t.groups[g].exponent;
+    *count = t.groups[g].count;
+    *rice = t.groups[g].rice;
+    return CRX_OK;
+}
+
+uint64_t crx_update_n_blocks(const crx_update *u) { return u->u.block_bits.size(); }
+
+int32_t crx_update_block_bits(const crx_update *u, uint32_t *out) {
+    std::copy(u->u.block_bits.begin(), u->u.block_bits.end(), out);
+    return CRX_OK;
+}
+
+uint64_t crx_update_payload_offset(const crx_update *u) { return u->u.payload_offset; }
+uint64_t crx_update_payload_len(const crx_update *u) { return u->u.payload_len; }
+uint64_t crx_update_total_changes(const crx_update *u) { return u->u.total_changes; }
+
+int32_t crx_apply(const crx_update *u, const uint8_t *payload_dev, uint16_t *const *targets, const uint64_t *numels,
+                  const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab, void *stream, crx_alloc_fn alloc,
+                  void *alloc_ctx, uint64_t *changed, char *err, uint64_t errlen) {
+    *changed = 0;
+    return guarded(err, errlen, [&] {
+        if (!payload_dev && u->u.payload_len && !u->u.payload_host) throw Invalid("payload is not on the host");
+        Arena ar{alloc, alloc_ctx};
+        apply(u->u, payload_dev, targets, numels, has_cache, cache_vals, slab, (hipStream_t)stream, ar, changed);
+    });
+}
+
+int32_t crx_encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news, const uint64_t *numels,
+                   const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab, void *stream, crx_alloc_fn alloc,
+                   void *alloc_ctx, crx_encoded **out, char *err, uint64_t errlen) {
+    *out = nullptr;
+    return guarded(err, errlen, [&] {
+        auto *e = new crx_encoded();
+        try {
+            Arena ar{alloc, alloc_ctx};
+            encode(n, olds, news, numels, has_cache, cache_vals, slab, (hipStream_t)stream, ar, *e);
+        } catch (...) {
+            delete e;
+            throw;
+        }
+        *out = e;
+    });
+}
+
+int32_t crx_encoded_present(const crx_encoded *e, int32_t t) { return (t >= 0 && t < e->n) ? e->present[t] : 0; }
+uint64_t crx_encoded_checksum(const crx_encoded *e, int32_t t) { return (t >= 0 && t < e->n) ? e->checksum[t] : 0; }
+uint64_t crx_encoded_total_changes(const crx_encoded *e) { return e->total_changes; }
+
+uint64_t crx_encoded_size(const crx_encoded *e, const char *const *names, const uint64_t *name_lens) {
+    std::vector<uint8_t> hdr;
+    write_header(*e, names, name_lens, hdr);
+    std::vector<uint8_t> pl;
+    put_varint(pl, e->payload_len);
+    return hdr.size() + 4 * e->n_blocks + pl.size() + e->payload_len;
+}
+
+int32_t crx_encoded_write(const crx_encoded *e, const char *const *names, const uint64_t *name_lens, uint8_t *dst,
+                          int32_t dst_on_device, void *stream, char *err, uint64_t errlen) {
+    return guarded(err, errlen, [&] {
+        hipStream_t s = (hipStream_t)stream;
+        std::vector<uint8_t> hdr, pl;
+        write_header(*e, names, name_lens, hdr);
+        put_varint(pl, e->payload_len);
+        const hipMemcpyKind from_dev = dst_on_device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
+        uint64_t off = 0;
+        if (dst_on_device) {
+            HIP_OK(hipMemcpyAsync(dst, hdr.data(), hdr.size(), hipMemcpyHostToDevice, s));
+        } else {
+            std::memcpy(dst, hdr.data(), hdr.size());
+        }
+        off += hdr.size();
+        if (e->n_blocks) HIP_OK(hipMemcpyAsync(dst + off, e->d_block_bits, 4 * e->n_blocks, from_dev, s));
+        off += 4 * e->n_blocks;
+        if (dst_on_device) HIP_OK(hipMemcpyAsync(dst + off, pl.data(), pl.size(), hipMemcpyHostToDevice, s));
+        else std::memcpy(dst + off, pl.data(), pl.size());
+        off += pl.size();
+        if (e->payload_len) HIP_OK(hipMemcpyAsync(dst + off, e->d_payload, e->payload_len, from_dev, s));
+        HIP_OK(hipStreamSynchronize(s));
+    });
+}
+
+int64_t crx_encoded_n_tables(const crx_encoded *e) { return (int64_t)e->tables.size(); }
+
+int32_t crx_encoded_table(const crx_encoded *e, int64_t i, int32_t *exponent, int64_t *n_sym, uint32_t *symbols,
+                          uint8_t *lengths) {
+    if (i < 0 || (size_t)i >= e->tables.size()) return CRX_INVALID;
+    const Table &t = e->tables[i];
+    *exponent = t.exponent;
+    *n_sym = (int64_t)t.symbols.size();
+    if (symbols) std::copy(t.symbols.begin(), t.symbols.end(), symbols);
+    if (lengths) std::copy(t.lengths.begin(), t.lengths.end(), lengths);
+    return CRX_OK;
+}
+
+int32_t crx_encoded_n_groups(const crx_encoded *e, int32_t t) {
+    return (t >= 0 && t < e->n) ? (int32_t)e->groups[t].size() : 0;
+}
+
+int32_t crx_encoded_group(const crx_encoded *e, int32_t t, int32_t g, int32_t *exponent, uint64_t *count, int32_t *rice) {
+    if (t < 0 || t >= e->n || g < 0 || (size_t)g >= e->groups[t].size()) return CRX_INVALID;
+    *exponent = e->groups[t][g].exponent;
+    *count = e->groups[t][g].count;
+    *rice = e->groups[t][g].rice;
+    return CRX_OK;
+}
+
+uint64_t crx_encoded_n_blocks(const crx_encoded *e) { return e->n_blocks; }
+
+int32_t crx_encoded_block_bits(const crx_encoded *e, uint32_t *out, void *stream) {
+    return guarded(nullptr, 0, [&] {
+        if (e->n_blocks)
+            HIP_OK(hipMemcpyAsync(out, e->d_block_bits, 4 * e->n_blocks, hipMemcpyDeviceToHost, (hipStream_t)stream));
+        HIP_OK(hipStreamSynchronize((hipStream_t)stream));
+    });
+}
+
+uint64_t crx_encoded_payload_len(const crx_encoded *e) { return e->payload_len; }
+
+int32_t crx_encoded_payload(const crx_encoded *e, uint8_t *out, void *stream) {
+    return guarded(nullptr, 0, [&] {
+        if (e->payload_len)
+            HIP_OK(hipMemcpyAsync(out, e->d_payload, e->payload_len, hipMemcpyDeviceToHost, (hipStream_t)stream));
+        HIP_OK(hipStreamSynchronize((hipStream_t)stream));
+    });
+}
+
+void crx_encoded_free(crx_encoded *e) { delete e; }
+
+int32_t crx_checksum(const uint16_t *data, uint64_t n, void *stream, crx_alloc_fn alloc, void *alloc_ctx, uint64_t *out,
+                     char *err, uint64_t errlen) {
+    *out = 0;
+    return guarded(err, errlen, [&] {
+        Arena ar{alloc, alloc_ctx};
+        full_checksum(data, n, (hipStream_t)stream, ar, out);
+    });
+}
+
+int32_t crx_huffman_lengths(const uint64_t *counts, int64_t n, int32_t *lengths) {
+    if (n <= 0) return CRX_INVALID;
+    try {
+        std::vector<int> L = huffman_lengths(std::vector<uint64_t>(counts, counts + n));
+        std::copy(L.begin(), L.end(), lengths);
+        return CRX_OK;
+    } catch (const std::bad_alloc &) {
+        return CRX_NOMEM;
+    }
+}
+
+int32_t crx_canonical_codes(const int32_t *lengths, int64_t n, uint32_t *codes) {
+    if (n <= 0) return CRX_INVALID;
+    try {
+        std::vector<uint32_t> c = canonical_codes(std::vector<int>(lengths, lengths + n));
+        std::copy(c.begin(), c.end(), codes);
+        return CRX_OK;
+    } catch (const std::bad_alloc &) {
+        return CRX_NOMEM;
+    }
+}
+
+void crx_rice_candidates(uint64_t count, uint64_t gap_sum, int32_t cand[3]) {
+    int c[3];
+    rice_candidates(count, gap_sum, c);
+    for (int k = 0; k < 3; ++k) cand[k] = c[k];
+}
+
+int32_t crx_rice_choose(uint64_t count, const int32_t cand[3], const uint64_t shifted[3]) {
+    const int c[3] = {cand[0], cand[1], cand[2]};
+    return rice_choose(count, c, shifted);
+}
+
+void crx_timing_enable(int32_t on) { g_timing = on != 0; }
+
+void crx_timing_reset(void) {
+    timing_collect();
+    std::lock_guard<std::mutex> lk(g_tmu);
+    g_stats.clear();
+}
+
+int32_t crx_timing_read(char *buf, uint64_t len) {
+    timing_collect();
+    std::lock_guard<std::mutex> lk(g_tmu);
+    std::string out;
+    char line[256];
+    for (const auto &kv : g_stats) {
+        std::snprintf(line, sizeof line, "%s %lld %.6f\n", kv.first.c_str(), (long long)kv.second.calls, kv.second.ms);
+        out += line;
+    }
+    if (buf && len) std::snprintf(buf, (size_t)len, "%s", out.c_str());
+    return (int32_t)out.size();
+}
+
+}  // extern "C"

@@ -1,0 +1,184 @@
+// Device data layouts and kernel launchers of the gfx950 update codec.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace crx {
+
+constexpr int kRow = 128;             // elements per wavefront row: 64 lanes x one 32-bit word
+constexpr int kRecCap = 512;          // change records a wavefront buffers in LDS before a flush
+constexpr int kDense = 32;            // residual symbols below this are counted in a dense table
+constexpr int kLocalGroups = 64;      // groups a statistics workgroup accumulates in LDS
+constexpr uint32_t kScanTiles = 32;   // slabs per chunk of the per-tensor histogram scan
+constexpr int kElemsPerThread = 16;   // change-order kernels: contiguous elements per thread
+constexpr int kElemsPerWG = 256 * kElemsPerThread;
+constexpr uint32_t kNone = 0xFFFFFFFFu;
+constexpr int32_t kFar = 0x40000000;  // "no target in this slab" for the select pass
+// bits of the apply verdict flag
+constexpr unsigned int kBadDecode = 1;    // a block does not decode exactly to its length
+constexpr unsigned int kBadLocal = 2;     // a change lies beyond its exponent group
+constexpr unsigned int kBadUnplaced = 4;  // a change was not found in the receiver's weights
+
+// One tensor of a call.  Elements are read as 32-bit words from `frame`, the 4-byte aligned address
+// at or below the first element: tensor element i is 16-bit frame element i + lead.
+struct TensorDesc {
+    const uint32_t *frame;      // old weights (encode) / receiver weights (apply)
+    const uint32_t *frame_new;  // encode: new weights, same lead as `frame`
+    uint16_t *base;             // apply: receiver tensor, written by the scatter
+    uint64_t numel;
+    uint32_t lead;
+    uint32_t tile_begin;        // first slab (global index)
+    uint32_t n_tiles;
+    uint32_t cold;              // 1: a full checksum is needed (new for encode, old for apply)
+};
+
+// A run of change records one wavefront flushed: records [base, base + count) of slab `tile`.
+struct Chunk {
+    uint32_t tile;
+    uint32_t count;
+    uint64_t base;
+};
+
+// One (tensor, exponent) group.  Encode fills r0/rice/blk_base after the statistics pass;
+// apply fills everything from the parsed header.
+struct GroupDev {
+    uint32_t tensor;
+    uint32_t exponent;
+    uint32_t count;
+    uint32_t elem_base;  // first change of the group in update order
+    uint32_t blk_base;   // first block of the group
+    uint32_t rice;
+    uint32_t r0;         // encode: floor(log2(mean gap)) clamped
+    uint32_t table;      // apply: decoding table index
+};
+
+struct EncRankArgs {
+    const TensorDesc *descs;
+    uint32_t n_tensors, slab;
+    uint32_t *hall, *hchg;          // [tiles][256]
+    uint64_t *rec;
+    uint64_t rec_cap;
+    Chunk *chunks;
+    uint64_t chunk_cap;
+    unsigned long long *counters;   // [0] records, [1] chunks, [2] overflow bits
+    uint64_t *delta, *full;         // [tiles]
+};
+
+struct HistArgs {
+    const TensorDesc *descs;
+    uint32_t n_tensors, slab;
+    uint32_t *hall;                 // [tiles][256]
+    uint64_t *full;                 // [tiles]
+};
+
+struct ScanChunk {                  // SCAN_TILES consecutive slabs of one tensor
+    uint32_t tile_begin, tile_end, tensor, pad;
+};
+
+struct StatsArgs {
+    const uint64_t *sorted;         // (zz << 32) | group-local index, in update order
+    uint64_t n;
+    const GroupDev *groups;
+    uint32_t n_groups;
+    uint32_t *dense;                // [256][kDense]
+    uint32_t *rare;                 // (exponent << 17) | zz for zz >= kDense
+    uint64_t rare_cap;
+    unsigned long long *counters;   // [0] rare count, [1] rare overflow
+    unsigned long long *cost;       // [groups][3]
+};
+
+struct CodeArgs {
+    const uint64_t *sorted;
+    uint64_t n;
+    const GroupDev *groups;
+    uint32_t n_groups;
+    const uint32_t *lut;            // [256][kDense]: (code << 5) | length, 0 if absent
+    const uint32_t *rare_keys;      // sorted (exponent << 17) | zz
+    const uint32_t *rare_vals;
+    uint32_t n_rare;
+    unsigned long long *wsum;       // [workgroups] bits per workgroup
+    const unsigned long long *woff; // [workgroups] exclusive bit offsets
+    uint32_t *words;                // payload as big-endian bytes in 32-bit words
+    unsigned long long *bstart;     // [blocks + 1] bit offset of each block
+};
+
+struct DecodeArgs {
+    const uint64_t *payload;        // big-endian byte stream, 8-byte aligned, zero padded
+    uint64_t n_words;
+    const uint32_t *block_bits;
+    const unsigned long long *block_off;
+    uint64_t n_blocks;
+    const GroupDev *groups;
+    uint32_t n_groups;
+    const uint32_t *sizes;          // [tensor][256] group sizes of the receiver
+    const uint32_t *tab;            // [tables][3][18]: first, count, base per code length
+    const uint32_t *syms;
+    uint32_t n_syms;
+    uint32_t *zz;                   // [changes]
+    uint32_t *local;                // [changes] block-relative, then group-local index
+    unsigned long long *blk_sum;    // [blocks] sum of (gap + 1) per block
+    unsigned int *bad;
+};
+
+struct SelectArgs {
+    const TensorDesc *descs;
+    uint32_t n_tensors, slab;
+    const uint32_t *pre;            // [tiles][256] exponent counts before the slab (in its tensor)
+    const uint32_t *lb;             // [tiles][256] first change of the group at or after the slab
+    const int32_t *group_of;        // [tensor][256] group index or -1
+    const GroupDev *groups;
+    const uint32_t *local;          // group-local index of every change
+    uint32_t *pos;                  // [changes] element index
+    uint16_t *val;                  // [changes] old, then new bits
+    const unsigned int *bad;
+};
+
+struct BlockArgs {                  // per-block kernels over the change list (one workgroup per block)
+    const GroupDev *groups;
+    uint32_t n_groups;
+    const TensorDesc *descs;
+    const uint32_t *sizes;
+    const unsigned long long *blk_prefix;
+    uint32_t *local;
+    const uint32_t *zz;
+    uint32_t *pos;
+    uint16_t *val;
+    unsigned long long *tdelta;     // [tensors]
+    unsigned int *bad;
+};
+
+void launch_enc_rank(const EncRankArgs &a, uint32_t tiles, hipStream_t s);
+void launch_hist(const HistArgs &a, uint32_t tiles, hipStream_t s);
+void launch_scan_tables(uint32_t *h, const ScanChunk *chunks, uint32_t n_chunks, const uint32_t *tensor_chunk_begin,
+                        uint32_t n_tensors, uint32_t *csum, uint32_t *totals, hipStream_t s);
+void launch_enc_groups(const uint32_t *totals_chg, uint32_t n_tensors, GroupDev *groups, uint32_t *gbase,
+                       unsigned long long *counters, hipStream_t s);
+void launch_place(const Chunk *chunks, uint32_t n_chunks, const uint64_t *rec, const TensorDesc *descs,
+                  uint32_t n_tensors, const uint32_t *hall_pre, const uint32_t *hchg_pre, const uint32_t *gbase,
+                  uint64_t *sorted, uint64_t n_sorted, hipStream_t s);
+void launch_r0(GroupDev *groups, uint32_t n_groups, const uint64_t *sorted, hipStream_t s);
+void launch_stats(const StatsArgs &a, hipStream_t s);
+void launch_code_lengths(const CodeArgs &a, hipStream_t s);
+void launch_pack(const CodeArgs &a, hipStream_t s);
+void launch_block_bits(const unsigned long long *bstart, uint64_t n_blocks, uint32_t *out, unsigned int *overflow,
+                       hipStream_t s);
+void launch_scan_u64(const unsigned long long *in, uint64_t n, unsigned long long *out, hipStream_t s);
+void launch_scan_u32(const uint32_t *in, uint64_t n, unsigned long long *out, hipStream_t s);
+void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint64_t *per_tile, uint64_t *out,
+                        hipStream_t s);
+void launch_decode(const DecodeArgs &a, hipStream_t s);
+void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
+void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s);
+void launch_select(const SelectArgs &a, uint32_t tiles, hipStream_t s);
+void launch_verify(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
+void launch_scatter(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
+void launch_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial, uint32_t n_parts,
+                     hipStream_t s);
+
+// Host-side timing of launches (events on the launch stream), enabled by crx_timing_enable.
+void timing_begin(hipStream_t s);
+void timing_end(const char *name, hipStream_t s);
+
+}  // namespace crx

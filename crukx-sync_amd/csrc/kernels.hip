@@ -1,0 +1,1042 @@
+// gfx950 kernels of the update codec (wave64, LDS, HBM-streaming; no MFMA: nothing here is a
+// contraction).
+//
+// Ranking (encode) and selection (apply) work on slabs: one wavefront owns `slab` consecutive
+// elements of one tensor and streams them as rows of 64 lanes x one 32-bit word (two bf16).  A
+// running per-exponent histogram in LDS gives, for any element, the number of same-exponent
+// elements before its row; the stable in-row rank comes from ballots and mbcnt.  Per-slab
+// histograms are scanned per tensor afterwards, so a slab's ranks become tensor-wide ranks.
+#include "kernels.h"
+
+namespace crx {
+namespace {
+
+constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ULL;
+constexpr uint64_t kMix1 = 0xBF58476D1CE4E5B9ULL;
+constexpr uint64_t kMix2 = 0x94D049BB133111EBULL;
+constexpr int kUnroll = 8;            // rows loaded ahead per wavefront
+
+// splitmix64(i) | 1: the per-position checksum weight (docs/FORMAT.md:61-64).
+__device__ __forceinline__ uint64_t weight(uint64_t i) {
+    uint64_t z = (i + 1) * kGolden;
+    z = (z ^ (z >> 30)) * kMix1;
+    z = (z ^ (z >> 27)) * kMix2;
+    return (z ^ (z >> 31)) | 1ULL;
+}
+
+__device__ __forceinline__ uint32_t lane() { return __lane_id(); }
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+// number of set bits of m below this lane
+__device__ __forceinline__ uint32_t mbcnt(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+__device__ __forceinline__ uint32_t rdlane(uint32_t v, uint32_t l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ uint64_t wave_sum(uint64_t v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t zigzag(uint32_t o16, uint32_t n16) {
+    int32_t res = (int32_t)(int16_t)n16 - (int32_t)(int16_t)o16;
+    return res >= 0 ? (uint32_t)(2 * res) : (uint32_t)(-2 * res - 1);
+}
+
+__device__ uint32_t tensor_of_tile(const TensorDesc *d, uint32_t n, uint32_t tau) {
+    uint32_t lo = 0, hi = n;  // last tensor whose first slab is <= tau
+    while (hi - lo > 1) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (d[mid].tile_begin <= tau) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// last group whose first change is <= i
+__device__ uint32_t group_of_elem(const GroupDev *g, uint32_t n, uint64_t i) {
+    uint32_t lo = 0, hi = n;
+    while (hi - lo > 1) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (g[mid].elem_base <= i) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// last group whose first block is <= b
+__device__ uint32_t group_of_block(const GroupDev *g, uint32_t n, uint64_t b) {
+    uint32_t lo = 0, hi = n;
+    while (hi - lo > 1) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (g[mid].blk_base <= b) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+struct Slab {
+    uint64_t lo, hi;          // tensor elements [lo, hi)
+    uint64_t d_begin, d_end;  // 32-bit frame words covering them
+    uint32_t nrows;
+};
+
+__device__ __forceinline__ Slab slab_of(const TensorDesc &td, uint32_t local, uint32_t slab) {
+    Slab s;
+    s.lo = (uint64_t)local * slab;
+    s.hi = min(s.lo + slab, td.numel);
+    s.d_begin = (s.lo + td.lead) >> 1;
+    s.d_end = (s.hi + td.lead + 1) >> 1;
+    s.nrows = (uint32_t)((s.d_end - s.d_begin + 63) / 64);
+    return s;
+}
+
+// ================================================================== encode: rank pass
+// One wavefront per slab.  Reads old and new once.  For every changed element it records its rank
+// among same-exponent elements of the slab (`rank`), its rank among same-exponent *changes* of the
+// slab (`rc`), the old exponent and the zigzag residual; per slab it writes both histograms, the
+// checksum delta of the changes and (cold) the full checksum of new.
+__device__ void flush_records(const EncRankArgs &a, uint32_t tau, const uint64_t *rbuf, uint32_t cnt) {
+    __syncthreads();
+    unsigned long long base = 0;
+    if (lane() == 0) base = atomicAdd(&a.counters[0], (unsigned long long)cnt);
+    base = __shfl(base, 0, 64);
+    if (base + cnt <= a.rec_cap) {
+        for (uint32_t j = lane(); j < cnt; j += 64) a.rec[base + j] = rbuf[j];
+        if (lane() == 0) {
+            unsigned long long ci = atomicAdd(&a.counters[1], 1ULL);
+            if (ci < a.chunk_cap) a.chunks[ci] = Chunk{tau, cnt, base};
+            else atomicOr(&a.counters[2], 2ULL);
+        }
+    } else if (lane() == 0) {
+        atomicOr(&a.counters[2], 1ULL);
+    }
+    __syncthreads();
+}
+
+template <bool COLD>
+__device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32_t tau, const Slab &sl,
+                              uint32_t *hall, uint32_t *hchg, uint64_t *rbuf) {
+    const uint32_t ln = lane();
+    const uint32_t rep = ln & 3;
+    uint32_t cnt = 0;
+    uint64_t dacc = 0, facc = 0;
+    const uint32_t *po = td.frame, *pn = td.frame_new;
+    for (uint32_t r = 0; r < sl.nrows; r += kUnroll) {
+        uint32_t ov[kUnroll], nv[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            uint64_t d = sl.d_begin + (uint64_t)(r + u) * 64 + ln;
+            bool in = d < sl.d_end;
+            ov[u] = in ? po[d] : 0u;
+            nv[u] = in ? pn[d] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            if (r + u >= sl.nrows) break;
+            const uint64_t d = sl.d_begin + (uint64_t)(r + u) * 64 + ln;
+            const int64_t i0 = (int64_t)(2 * d) - (int64_t)td.lead;
+            const bool v0 = i0 >= (int64_t)sl.lo && i0 < (int64_t)sl.hi;
+            const bool v1 = i0 + 1 >= (int64_t)sl.lo && i0 + 1 < (int64_t)sl.hi;
+            const uint32_t o = ov[u], n = nv[u];
+            const uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF;
+            const uint32_t x = o ^ n;
+            const bool c0 = v0 && (x & 0xFFFF), c1 = v1 && (x >> 16);
+            const uint64_t C0 = ballot(c0), C1 = ballot(c1);
+            if (C0 | C1) {
+                uint32_t rk0 = 0, rc0 = 0, rk1 = 0, rc1 = 0;
+                uint64_t P0 = C0, P1 = C1;
+                while (P0 | P1) {  // once per distinct exponent among this row's changes
+                    const uint32_t k = P0 ? rdlane(k0, (uint32_t)__builtin_ctzll(P0))
+                                          : rdlane(k1, (uint32_t)__builtin_ctzll(P1));
+                    const bool m0 = v0 && k0 == k, m1 = v1 && k1 == k;
+                    const uint64_t M0 = ballot(m0), M1 = ballot(m1);
+                    const uint32_t R = hall[4 * k] + hall[4 * k + 1] + hall[4 * k + 2] + hall[4 * k + 3];
+                    const uint32_t Rc = hchg[k];
+                    const uint32_t before = mbcnt(M0) + mbcnt(M1);
+                    const uint32_t beforec = mbcnt(M0 & C0) + mbcnt(M1 & C1);
+                    if (c0 && m0) {
+                        rk0 = R + before;
+                        rc0 = Rc + beforec;
+                    }
+                    if (c1 && m1) {
+                        rk1 = R + before + (m0 ? 1u : 0u);
+                        rc1 = Rc + beforec + ((c0 && m0) ? 1u : 0u);
+                    }
+                    __syncthreads();
+                    if (ln == 0) hchg[k] = Rc + (uint32_t)__popcll(M0 & C0) + (uint32_t)__popcll(M1 & C1);
+                    P0 &= ~M0;
+                    P1 &= ~M1;
+                }
+                const uint32_t cb = mbcnt(C0) + mbcnt(C1);  // changes in lower lanes of this row
+                if (c0) {
+                    rbuf[cnt + cb] = (uint64_t)rk0 | ((uint64_t)rc0 << 17) | ((uint64_t)k0 << 34) |
+                                     ((uint64_t)zigzag(o & 0xFFFF, n & 0xFFFF) << 42);
+                    dacc += (uint64_t)((int64_t)(n & 0xFFFF) - (int64_t)(o & 0xFFFF)) * weight((uint64_t)i0);
+                }
+                if (c1) {
+                    rbuf[cnt + cb + (c0 ? 1u : 0u)] = (uint64_t)rk1 | ((uint64_t)rc1 << 17) | ((uint64_t)k1 << 34) |
+                                                      ((uint64_t)zigzag(o >> 16, n >> 16) << 42);
+                    dacc += (uint64_t)((int64_t)(n >> 16) - (int64_t)(o >> 16)) * weight((uint64_t)i0 + 1);
+                }
+                cnt += (uint32_t)(__popcll(C0) + __popcll(C1));
+                __syncthreads();
+            }
+            if (v0) atomicAdd(&hall[4 * k0 + rep], 1u);
+            if (v1) atomicAdd(&hall[4 * k1 + rep], 1u);
+            if (COLD) {
+                if (v0) facc += (uint64_t)(n & 0xFFFF) * weight((uint64_t)i0);
+                if (v1) facc += (uint64_t)(n >> 16) * weight((uint64_t)i0 + 1);
+            }
+            if (cnt > kRecCap - kRow) {
+                flush_records(a, tau, rbuf, cnt);
+                cnt = 0;
+            }
+        }
+    }
+    if (cnt) flush_records(a, tau, rbuf, cnt);
+    __syncthreads();
+    for (uint32_t k = ln; k < 256; k += 64) {
+        a.hall[(uint64_t)tau * 256 + k] = hall[4 * k] + hall[4 * k + 1] + hall[4 * k + 2] + hall[4 * k + 3];
+        a.hchg[(uint64_t)tau * 256 + k] = hchg[k];
+    }
+    dacc = wave_sum(dacc);
+    facc = wave_sum(facc);
+    if (ln == 0) {
+        a.delta[tau] = dacc;
+        a.full[tau] = facc;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_enc_rank(EncRankArgs a) {
+    __shared__ uint32_t hall[256 * 4];  // 4 copies per exponent: fewer same-address LDS atomics
+    __shared__ uint32_t hchg[256];
+    __shared__ uint64_t rbuf[kRecCap];
+    const uint32_t tau = blockIdx.x;
+    const TensorDesc td = a.descs[tensor_of_tile(a.descs, a.n_tensors, tau)];
+    const Slab sl = slab_of(td, tau - td.tile_begin, a.slab);
+    for (uint32_t i = lane(); i < 1024; i += 64) hall[i] = 0;
+    for (uint32_t i = lane(); i < 256; i += 64) hchg[i] = 0;
+    __syncthreads();
+    if (td.cold) enc_rank_slab<true>(a, td, tau, sl, hall, hchg, rbuf);
+    else enc_rank_slab<false>(a, td, tau, sl, hall, hchg, rbuf);
+}
+
+// ================================================================== apply: histogram pass
+template <bool COLD>
+__device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau, const Slab &sl, uint32_t *hall) {
+    const uint32_t ln = lane(), rep = ln & 3;
+    uint64_t facc = 0;
+    const uint32_t *po = td.frame;
+    for (uint32_t r = 0; r < sl.nrows; r += kUnroll) {
+        uint32_t ov[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            uint64_t d = sl.d_begin + (uint64_t)(r + u) * 64 + ln;
+            ov[u] = d < sl.d_end ? po[d] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            if (r + u >= sl.nrows) break;
+            const uint64_t d = sl.d_begin + (uint64_t)(r + u) * 64 + ln;
+            const int64_t i0 = (int64_t)(2 * d) - (int64_t)td.lead;
+            const bool v0 = i0 >= (int64_t)sl.lo && i0 < (int64_t)sl.hi;
+            const bool v1 = i0 + 1 >= (int64_t)sl.lo && i0 + 1 < (int64_t)sl.hi;
+            const uint32_t o = ov[u];
+            if (v0) atomicAdd(&hall[4 * ((o >> 7) & 0xFF) + rep], 1u);
+            if (v1) atomicAdd(&hall[4 * ((o >> 23) & 0xFF) + rep], 1u);
+            if (COLD) {
+                if (v0) facc += (uint64_t)(o & 0xFFFF) * weight((uint64_t)i0);
+                if (v1) facc += (uint64_t)(o >> 16) * weight((uint64_t)i0 + 1);
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t k = ln; k < 256; k += 64)
+        a.hall[(uint64_t)tau * 256 + k] = hall[4 * k] + hall[4 * k + 1] + hall[4 * k + 2] + hall[4 * k + 3];
+    facc = wave_sum(facc);
+    if (ln == 0) a.full[tau] = facc;
+}
+
+__global__ __launch_bounds__(64) void k_hist(HistArgs a) {
+    __shared__ uint32_t hall[256 * 4];
+    const uint32_t tau = blockIdx.x;
+    const TensorDesc td = a.descs[tensor_of_tile(a.descs, a.n_tensors, tau)];
+    const Slab sl = slab_of(td, tau - td.tile_begin, a.slab);
+    for (uint32_t i = lane(); i < 1024; i += 64) hall[i] = 0;
+    __syncthreads();
+    if (td.cold) hist_slab<true>(a, td, tau, sl, hall);
+    else hist_slab<false>(a, td, tau, sl, hall);
+}
+
+// ================================================================== per-tensor histogram scan
+// h[tile][256] -> exclusive prefix over the tensor's slabs, in place; totals[tensor][256].
+__global__ __launch_bounds__(256) void k_scan_sum(const uint32_t *h, const ScanChunk *ch, uint32_t *csum) {
+    const ScanChunk c = ch[blockIdx.x];
+    const uint32_t k = threadIdx.x;
+    uint32_t s = 0;
+    for (uint32_t t = c.tile_begin; t < c.tile_end; ++t) s += h[(uint64_t)t * 256 + k];
+    csum[(uint64_t)blockIdx.x * 256 + k] = s;
+}
+
+__global__ __launch_bounds__(256) void k_scan_mid(uint32_t *csum, const uint32_t *tcb, uint32_t *totals) {
+    const uint32_t t = blockIdx.x, k = threadIdx.x;
+    uint32_t run = 0;
+    for (uint32_t c = tcb[t]; c < tcb[t + 1]; ++c) {
+        uint32_t v = csum[(uint64_t)c * 256 + k];
+        csum[(uint64_t)c * 256 + k] = run;
+        run += v;
+    }
+    totals[(uint64_t)t * 256 + k] = run;
+}
+
+__global__ __launch_bounds__(256) void k_scan_fin(uint32_t *h, const ScanChunk *ch, const uint32_t *csum) {
+    const ScanChunk c = ch[blockIdx.x];
+    const uint32_t k = threadIdx.x;
+    uint32_t run = csum[(uint64_t)blockIdx.x * 256 + k];
+    for (uint32_t t = c.tile_begin; t < c.tile_end; ++t) {
+        uint32_t v = h[(uint64_t)t * 256 + k];
+        h[(uint64_t)t * 256 + k] = run;
+        run += v;
+    }
+}
+
+// ================================================================== encode: groups and placement
+// Groups are the non-empty (tensor, exponent) pairs in (tensor, exponent) order (codec.py:317-333).
+__global__ __launch_bounds__(1024) void k_enc_groups(const uint32_t *tot, uint32_t n_tensors, GroupDev *groups,
+                                                     uint32_t *gbase, unsigned long long *counters) {
+    __shared__ uint32_t sv[1024], sz[1024];
+    __shared__ uint32_t carry_v, carry_z;
+    const uint32_t tid = threadIdx.x;
+    const uint64_t n = (uint64_t)n_tensors * 256;
+    if (tid == 0) carry_v = carry_z = 0;
+    __syncthreads();
+    for (uint64_t base = 0; base < n; base += 1024) {
+        const uint64_t idx = base + tid;
+        const uint32_t v = idx < n ? tot[idx] : 0u;
+        const uint32_t z = v ? 1u : 0u;
+        sv[tid] = v;
+        sz[tid] = z;
+        __syncthreads();
+        for (uint32_t off = 1; off < 1024; off <<= 1) {
+            uint32_t av = tid >= off ? sv[tid - off] : 0u, az = tid >= off ? sz[tid - off] : 0u;
+            __syncthreads();
+            sv[tid] += av;
+            sz[tid] += az;
+            __syncthreads();
+        }
+        const uint32_t ev = carry_v + sv[tid] - v, ez = carry_z + sz[tid] - z;
+        if (idx < n) {
+            gbase[idx] = ev;
+            if (v) {
+                GroupDev g{};
+                g.tensor = (uint32_t)(idx >> 8);
+                g.exponent = (uint32_t)(idx & 255);
+                g.count = v;
+                g.elem_base = ev;
+                groups[ez] = g;
+            }
+        }
+        __syncthreads();
+        if (tid == 1023) {
+            carry_v = ev + v;
+            carry_z = ez + z;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        counters[0] = carry_z;  // groups
+        counters[1] = carry_v;  // changes
+    }
+}
+
+// Records -> update order: position = group start + changes of the group in earlier slabs + rank
+// among the slab's changes of that exponent; value = zz and the group-local index.
+__global__ __launch_bounds__(64) void k_place(const Chunk *chunks, const uint64_t *rec, const TensorDesc *descs,
+                                              uint32_t n_tensors, const uint32_t *hall_pre, const uint32_t *hchg_pre,
+                                              const uint32_t *gbase, uint64_t *sorted, uint64_t n_sorted) {
+    const Chunk c = chunks[blockIdx.x];
+    const uint32_t t = tensor_of_tile(descs, n_tensors, c.tile);
+    for (uint32_t j = lane(); j < c.count; j += 64) {
+        const uint64_t r = rec[c.base + j];
+        const uint32_t rank = (uint32_t)(r & 0x1FFFF), rc = (uint32_t)((r >> 17) & 0x1FFFF);
+        const uint32_t k = (uint32_t)((r >> 34) & 0xFF), zz = (uint32_t)(r >> 42);
+        const uint32_t gidx = hall_pre[(uint64_t)c.tile * 256 + k] + rank;
+        const uint32_t dest = gbase[(uint64_t)t * 256 + k] + hchg_pre[(uint64_t)c.tile * 256 + k] + rc;
+        if (dest < n_sorted) sorted[dest] = ((uint64_t)zz << 32) | gidx;
+    }
+}
+
+// r0 = floor(log2(max(mean gap, 1))) clamped to 30; the gaps of a group sum to last index + 1 - count.
+__global__ __launch_bounds__(256) void k_r0(GroupDev *groups, uint32_t n_groups, const uint64_t *sorted) {
+    const uint32_t g = blockIdx.x * 256 + threadIdx.x;
+    if (g >= n_groups) return;
+    const GroupDev gr = groups[g];
+    const uint64_t last = (uint32_t)sorted[(uint64_t)gr.elem_base + gr.count - 1];
+    const uint64_t s = last + 1 - gr.count;
+    uint32_t r0 = 0;
+    while (r0 < 30 && ((uint64_t)gr.count << (r0 + 1)) <= s) ++r0;
+    groups[g].r0 = r0;
+}
+
+__device__ __forceinline__ void rice_cands(uint32_t r0, uint32_t c[3]) {
+    c[0] = r0 ? r0 - 1 : 0;
+    c[1] = r0;
+    c[2] = r0 < 30 ? r0 + 1 : 30;
+}
+
+// Per workgroup: 4096 consecutive changes, 16 contiguous per thread.  Sums of gap >> r for the
+// three Rice candidates of each group, residual symbol counts per exponent (dense below kDense,
+// the rest appended to a list the host sorts).
+__global__ __launch_bounds__(256) void k_stats(StatsArgs a) {
+    __shared__ uint32_t lhist[kLocalGroups * kDense];
+    __shared__ unsigned long long lcost[kLocalGroups * 3];
+    __shared__ uint32_t s_gfirst;
+    const uint32_t tid = threadIdx.x;
+    const uint64_t wbase = (uint64_t)blockIdx.x * kElemsPerWG;
+    for (uint32_t x = tid; x < kLocalGroups * kDense; x += 256) lhist[x] = 0;
+    for (uint32_t x = tid; x < kLocalGroups * 3; x += 256) lcost[x] = 0;
+    if (tid == 0) s_gfirst = group_of_elem(a.groups, a.n_groups, wbase);
+    __syncthreads();
+    const uint32_t gf = s_gfirst;
+    const uint64_t ib = wbase + (uint64_t)tid * kElemsPerThread;
+    const bool any = ib < a.n;
+    uint32_t g = any ? group_of_elem(a.groups, a.n_groups, ib) : 0;
+    GroupDev gr = a.groups[g];
+    uint32_t c[3];
+    rice_cands(gr.r0, c);
+    uint64_t prev = (any && ib > gr.elem_base) ? (uint32_t)a.sorted[ib - 1] : 0;
+    unsigned long long s0 = 0, s1 = 0, s2 = 0;
+    auto flush_cost = [&](uint32_t gg) {
+        if (!(s0 | s1 | s2)) return;
+        const uint32_t lg = gg - gf;
+        if (lg < kLocalGroups) {
+            atomicAdd(&lcost[lg * 3 + 0], s0);
+            atomicAdd(&lcost[lg * 3 + 1], s1);
+            atomicAdd(&lcost[lg * 3 + 2], s2);
+        } else {
+            atomicAdd(&a.cost[(uint64_t)gg * 3 + 0], s0);
+            atomicAdd(&a.cost[(uint64_t)gg * 3 + 1], s1);
+            atomicAdd(&a.cost[(uint64_t)gg * 3 + 2], s2);
+        }
+        s0 = s1 = s2 = 0;
+    };
+    for (int k = 0; k < kElemsPerThread; ++k) {
+        const uint64_t i = ib + k;
+        const bool valid = i < a.n;
+        uint32_t zz = 0, e = 0;
+        if (valid) {
+            while (i >= (uint64_t)gr.elem_base + gr.count) {
+                flush_cost(g);
+                gr = a.groups[++g];
+                rice_cands(gr.r0, c);
+            }
+            const uint64_t v = a.sorted[i];
+            const uint64_t gidx = (uint32_t)v;
+            zz = (uint32_t)(v >> 32);
+            e = gr.exponent;
+            const uint64_t gap = i == gr.elem_base ? gidx : gidx - prev - 1;
+            prev = gidx;
+            s0 += gap >> c[0];
+            s1 += gap >> c[1];
+            s2 += gap >> c[2];
+            if (zz < kDense) {
+                const uint32_t lg = g - gf;
+                if (lg < kLocalGroups) atomicAdd(&lhist[lg * kDense + zz], 1u);
+                else atomicAdd(&a.dense[e * kDense + zz], 1u);
+            }
+        }
+        const bool rare = valid && zz >= kDense;
+        const uint64_t m = ballot(rare);
+        if (m) {
+            const uint32_t leader = (uint32_t)__builtin_ctzll(m);
+            unsigned long long base = 0;
+            if (lane() == leader) base = atomicAdd(&a.counters[0], (unsigned long long)__popcll(m));
+            base = __shfl(base, leader, 64);
+            if (rare) {
+                const unsigned long long idx = base + mbcnt(m);
+                if (idx < a.rare_cap) a.rare[idx] = (e << 17) | zz;
+                else atomicOr(&a.counters[1], 1ULL);
+            }
+        }
+    }
+    if (any) flush_cost(g);
+    __syncthreads();
+    for (uint32_t x = tid; x < kLocalGroups * kDense; x += 256) {
+        const uint32_t v = lhist[x];
+        if (v) atomicAdd(&a.dense[a.groups[gf + x / kDense].exponent * kDense + x % kDense], v);
+    }
+    for (uint32_t x = tid; x < kLocalGroups * 3; x += 256) {
+        const unsigned long long v = lcost[x];
+        if (v) atomicAdd(&a.cost[(uint64_t)(gf + x / 3) * 3 + x % 3], v);
+    }
+}
+
+// ================================================================== encode: code lengths and packing
+struct Code {
+    uint64_t len;   // total bits
+    uint64_t q;     // unary run
+    uint32_t rice, hl, hc;
+    uint64_t gap;
+};
+
+__device__ __forceinline__ Code code_of(const CodeArgs &a, uint64_t gap, uint32_t zz, uint32_t e, uint32_t rice) {
+    uint32_t v;
+    if (zz < kDense) {
+        v = a.lut[e * kDense + zz];
+    } else {
+        const uint32_t key = (e << 17) | zz;
+        uint32_t lo = 0, hi = a.n_rare;
+        while (lo < hi) {
+            uint32_t mid = (lo + hi) >> 1;
+            if (a.rare_keys[mid] < key) lo = mid + 1;
+            else hi = mid;
+        }
+        v = lo < a.n_rare ? a.rare_vals[lo] : 0u;
+    }
+    Code c;
+    c.gap = gap;
+    c.rice = rice;
+    c.q = gap >> rice;
+    c.hl = v & 31;
+    c.hc = v >> 5;
+    c.len = c.q + 1 + rice + c.hl;
+    return c;
+}
+
+// Walks a thread's contiguous changes in update order, tracking the group and the previous index.
+struct Walk {
+    uint32_t g;
+    GroupDev gr;
+    uint64_t prev;
+};
+
+__device__ __forceinline__ Walk walk_start(const CodeArgs &a, uint64_t ib) {
+    Walk w;
+    w.g = group_of_elem(a.groups, a.n_groups, ib);
+    w.gr = a.groups[w.g];
+    w.prev = ib > w.gr.elem_base ? (uint32_t)a.sorted[ib - 1] : 0;
+    return w;
+}
+
+__device__ __forceinline__ Code walk_next(const CodeArgs &a, Walk &w, uint64_t i) {
+    while (i >= (uint64_t)w.gr.elem_base + w.gr.count) w.gr = a.groups[++w.g];
+    const uint64_t v = a.sorted[i];
+    const uint64_t gidx = (uint32_t)v;
+    const uint64_t gap = i == w.gr.elem_base ? gidx : gidx - w.prev - 1;
+    w.prev = gidx;
+    return code_of(a, gap, (uint32_t)(v >> 32), w.gr.exponent, w.gr.rice);
+}
+
+__device__ unsigned long long block_exclusive_sum(unsigned long long v, unsigned long long *sh, unsigned long long *total) {
+    const uint32_t tid = threadIdx.x;
+    sh[tid] = v;
+    __syncthreads();
+    for (uint32_t off = 1; off < 256; off <<= 1) {
+        unsigned long long x = tid >= off ? sh[tid - off] : 0ULL;
+        __syncthreads();
+        sh[tid] += x;
+        __syncthreads();
+    }
+    const unsigned long long incl = sh[tid];
+    *total = sh[255];
+    __syncthreads();
+    return incl - v;
+}
+
+__global__ __launch_bounds__(256) void k_code_lengths(CodeArgs a) {
+    __shared__ unsigned long long sh[256];
+    const uint64_t ib = (uint64_t)blockIdx.x * kElemsPerWG + (uint64_t)threadIdx.x * kElemsPerThread;
+    unsigned long long sum = 0;
+    if (ib < a.n) {
+        Walk w = walk_start(a, ib);
+        for (int k = 0; k < kElemsPerThread && ib + k < a.n; ++k) sum += walk_next(a, w, ib + k).len;
+    }
+    unsigned long long total;
+    block_exclusive_sum(sum, sh, &total);
+    if (threadIdx.x == 0) a.wsum[blockIdx.x] = total;
+}
+
+// OR `len` (<= 64) bits of `val` (right-aligned) into the big-endian bit stream at bit `off`.
+__device__ __forceinline__ void put_bits(uint32_t *words, uint64_t off, uint64_t val, uint32_t len) {
+    if (!len) return;
+    const uint32_t sh = (uint32_t)(off & 31);
+    const uint64_t w = off >> 5;
+    const unsigned __int128 X = (unsigned __int128)val << (96 - sh - len);
+    const uint32_t w0 = (uint32_t)(X >> 64), w1 = (uint32_t)(X >> 32), w2 = (uint32_t)X;
+    if (w0) atomicOr(&words[w], __builtin_bswap32(w0));
+    if (w1) atomicOr(&words[w + 1], __builtin_bswap32(w1));
+    if (w2) atomicOr(&words[w + 2], __builtin_bswap32(w2));
+}
+
+// q one-bits at bit `off`; whole 32-bit words inside the run belong to this code alone.
+__device__ void put_ones(uint32_t *words, uint64_t off, uint64_t q) {
+    const uint64_t end = off + q;
+    const uint32_t head = (uint32_t)min<uint64_t>((32 - (off & 31)) & 31, q);  // up to the next word
+    if (head) put_bits(words, off, (1ULL << head) - 1, head);
+    uint64_t w = (off + head) >> 5;
+    const uint64_t wend = end >> 5;  // whole words
+    for (; w < wend; ++w) words[w] = 0xFFFFFFFFu;
+    const uint32_t tail = (uint32_t)(end & 31);
+    if (w == wend && tail && (w << 5) >= off + head) put_bits(words, w << 5, (1ULL << tail) - 1, tail);
+}
+
+__device__ __forceinline__ void put_code(uint32_t *words, uint64_t off, const Code &c) {
+    const uint64_t tail = ((c.gap & ((1ULL << c.rice) - 1)) << c.hl) | c.hc;  // 0, r bits, Huffman code
+    const uint32_t tail_len = 1 + c.rice + c.hl;
+    if (c.len <= 64) {
+        const uint64_t ones = c.q ? (((1ULL << c.q) - 1) << tail_len) : 0ULL;
+        put_bits(words, off, ones | tail, (uint32_t)c.len);
+    } else {
+        put_ones(words, off, c.q);
+        put_bits(words, off + c.q, tail, tail_len);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_pack(CodeArgs a) {
+    __shared__ unsigned long long sh[256];
+    const uint64_t ib = (uint64_t)blockIdx.x * kElemsPerWG + (uint64_t)threadIdx.x * kElemsPerThread;
+    unsigned long long sum = 0;
+    if (ib < a.n) {
+        Walk w = walk_start(a, ib);
+        for (int k = 0; k < kElemsPerThread && ib + k < a.n; ++k) sum += walk_next(a, w, ib + k).len;
+    }
+    unsigned long long total;
+    unsigned long long off = a.woff[blockIdx.x] + block_exclusive_sum(sum, sh, &total);
+    if (ib < a.n) {
+        Walk w = walk_start(a, ib);
+        for (int k = 0; k < kElemsPerThread && ib + k < a.n; ++k) {
+            const uint64_t i = ib + k;
+            const Code c = walk_next(a, w, i);
+            const uint64_t rel = i - w.gr.elem_base;
+            if ((rel & 255) == 0) a.bstart[w.gr.blk_base + (rel >> 8)] = off;
+            put_code(a.words, off, c);
+            off += c.len;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_block_bits(const unsigned long long *bstart, uint64_t n_blocks, uint32_t *out,
+                                                    unsigned int *overflow) {
+    const uint64_t b = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= n_blocks) return;
+    const unsigned long long len = bstart[b + 1] - bstart[b];
+    if (len >= (1ULL << 32)) atomicOr(overflow, 1u);
+    out[b] = (uint32_t)len;
+}
+
+// ================================================================== generic scans and sums
+// Exclusive prefix sums of n values with one workgroup; out[n] = total.
+template <typename T>
+__global__ __launch_bounds__(1024) void k_scan1(const T *in, uint64_t n, unsigned long long *out) {
+    __shared__ unsigned long long part[1024];
+    const uint32_t tid = threadIdx.x;
+    const uint64_t per = (n + 1023) / 1024;
+    const uint64_t b = min((uint64_t)tid * per, n), e = min(b + per, n);
+    unsigned long long s = 0;
+    for (uint64_t i = b; i < e; ++i) s += in[i];
+    part[tid] = s;
+    __syncthreads();
+    for (uint32_t off = 1; off < 1024; off <<= 1) {
+        unsigned long long v = tid >= off ? part[tid - off] : 0ULL;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    unsigned long long run = part[tid] - s;
+    for (uint64_t i = b; i < e; ++i) {
+        const unsigned long long v = in[i];
+        out[i] = run;
+        run += v;
+    }
+    if (tid == 1023) out[n] = part[1023];
+}
+
+__global__ __launch_bounds__(256) void k_tensor_sums(const TensorDesc *descs, const uint64_t *per_tile, uint64_t *out) {
+    __shared__ unsigned long long sh[256];
+    const TensorDesc td = descs[blockIdx.x];
+    unsigned long long s = 0;
+    for (uint32_t t = threadIdx.x; t < td.n_tiles; t += 256) s += per_tile[td.tile_begin + t];
+    unsigned long long total;
+    block_exclusive_sum(s, sh, &total);
+    if (threadIdx.x == 0) out[blockIdx.x] = total;
+}
+
+// Full checksum of one tensor: each workgroup sums a contiguous range.
+__global__ __launch_bounds__(256) void k_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial,
+                                                  uint32_t n_parts) {
+    __shared__ unsigned long long sh[256];
+    const uint64_t words = (n + lead + 1) >> 1;
+    const uint64_t per = (words + n_parts - 1) / n_parts;
+    const uint64_t wb = (uint64_t)blockIdx.x * per, we = min(wb + per, words);
+    unsigned long long s = 0;
+    for (uint64_t d = wb + threadIdx.x; d < we; d += 256) {
+        const uint32_t o = frame[d];
+        const int64_t i0 = (int64_t)(2 * d) - (int64_t)lead;
+        if (i0 >= 0 && i0 < (int64_t)n) s += (uint64_t)(o & 0xFFFF) * weight((uint64_t)i0);
+        if (i0 + 1 >= 0 && i0 + 1 < (int64_t)n) s += (uint64_t)(o >> 16) * weight((uint64_t)i0 + 1);
+    }
+    unsigned long long total;
+    block_exclusive_sum(s, sh, &total);
+    if (threadIdx.x == 0) partial[blockIdx.x] = total;
+}
+
+// ================================================================== apply: block decode
+// One lane per block of up to 256 changes (blocks are independent: docs/FORMAT.md:41-44).  Per
+// change: unary run (count of leading ones, continued across 64-bit windows but never past the
+// block end or the group's bound q_max), a zero, `rice` remainder bits, then the canonical Huffman
+// code found by length with the first/count/base tables (codec.py:434-454).  Bits past the payload
+// read as zero.  Any violation raises the shared `bad` flag; nothing here can read out of bounds.
+__device__ __forceinline__ uint64_t read64(const uint64_t *p, uint64_t nw, uint64_t pos) {
+    const uint64_t w = pos >> 6;
+    const uint32_t s = (uint32_t)(pos & 63);
+    const uint64_t hi = w < nw ? __builtin_bswap64(p[w]) : 0ULL;
+    const uint64_t lo = w + 1 < nw ? __builtin_bswap64(p[w + 1]) : 0ULL;
+    return s ? (hi << s) | (lo >> (64 - s)) : hi;
+}
+
+__global__ __launch_bounds__(64) void k_decode(DecodeArgs a) {
+    const uint64_t b = (uint64_t)blockIdx.x * 64 + threadIdx.x;
+    if (b >= a.n_blocks) return;
+    const uint32_t g = group_of_block(a.groups, a.n_groups, b);
+    const GroupDev gr = a.groups[g];
+    const uint64_t kb = b - gr.blk_base;
+    const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
+    const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
+    const uint64_t size = a.sizes[(uint64_t)gr.tensor * 256 + gr.exponent];
+    const uint32_t rice = gr.rice;
+    const uint64_t qmax = size >> rice;
+    const uint32_t *first = a.tab + (uint64_t)gr.table * 54, *count = first + 18, *base = first + 36;
+    uint64_t cur = a.block_off[b];
+    const uint64_t end = cur + a.block_bits[b];
+    bool bad = kb == 0 && gr.count > size;  // a group with more changes than elements
+    uint64_t rel = 0;                         // sum of (gap + 1) so far in this block
+    for (uint32_t s = 0; s < cnt && !bad; ++s) {
+        if (cur >= end) {
+            bad = true;
+            break;
+        }
+        uint64_t q = 0;
+        for (;;) {
+            const uint64_t y = ~read64(a.payload, a.n_words, cur + q);
+            if (y) {
+                q += (uint64_t)__builtin_clzll(y);
+                break;
+            }
+            q += 64;
+            if (q > qmax || cur + q >= end) break;
+        }
+        if (q > qmax || cur + q >= end) {
+            bad = true;
+            break;
+        }
+        const uint64_t c = cur + q + 1;
+        const uint64_t x = read64(a.payload, a.n_words, c);
+        const uint64_t rem = rice ? x >> (64 - rice) : 0ULL;
+        const uint32_t peek = (uint32_t)((x << rice) >> (64 - 17));
+        uint32_t L = 0, idx = 0;
+        for (uint32_t l = 1; l <= 17; ++l) {
+            const uint32_t code = peek >> (17 - l);
+            const uint32_t d = code - first[l];
+            if (d < count[l]) {
+                L = l;
+                idx = base[l] + d;
+                break;
+            }
+        }
+        if (!L) {
+            bad = true;
+            break;
+        }
+        const uint64_t gap = (q << rice) | rem;
+        if (gap >= size) {
+            bad = true;
+            break;
+        }
+        rel += gap + 1;
+        a.zz[eb + s] = a.syms[min(idx, a.n_syms - 1)];
+        a.local[eb + s] = (uint32_t)min<uint64_t>(rel - 1, 0xFFFFFFFFULL);
+        cur = c + rice + L;
+    }
+    if (!bad && cur != end) bad = true;
+    a.blk_sum[b] = rel;
+    if (bad) atomicOr(a.bad, kBadDecode);
+}
+
+// local = (sum of (gap + 1) over earlier blocks of the group) + block-relative local; must stay
+// below the group size (codec.py:640-642,696-697).
+__global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
+    if (*a.bad) return;
+    const uint64_t b = blockIdx.x;
+    const uint32_t g = group_of_block(a.groups, a.n_groups, b);
+    const GroupDev gr = a.groups[g];
+    const uint64_t kb = b - gr.blk_base;
+    const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
+    const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
+    const uint64_t size = a.sizes[(uint64_t)gr.tensor * 256 + gr.exponent];
+    const unsigned long long base = a.blk_prefix[b] - a.blk_prefix[gr.blk_base];
+    const uint32_t s = threadIdx.x;
+    if (s < cnt) {
+        const unsigned long long local = base + a.local[eb + s];
+        if (local >= size) atomicOr(a.bad, kBadLocal);
+        a.local[eb + s] = (uint32_t)min<unsigned long long>(local, 0xFFFFFFFFULL);
+        a.pos[eb + s] = kNone;
+    }
+}
+
+// For every (slab, exponent): the first change of the group whose local index is at or after the
+// number of same-exponent elements before the slab.
+__global__ __launch_bounds__(256) void k_locate(SelectArgs a) {
+    if (*a.bad) return;
+    const uint32_t tau = blockIdx.x, k = threadIdx.x;
+    const uint32_t t = tensor_of_tile(a.descs, a.n_tensors, tau);
+    const int32_t g = a.group_of[(uint64_t)t * 256 + k];
+    uint32_t lb = kNone;
+    if (g >= 0) {
+        const GroupDev gr = a.groups[g];
+        const uint32_t target = a.pre[(uint64_t)tau * 256 + k];
+        uint32_t lo = gr.elem_base, hi = gr.elem_base + gr.count;
+        while (lo < hi) {
+            uint32_t mid = lo + ((hi - lo) >> 1);
+            if (a.local[mid] < target) lo = mid + 1;
+            else hi = mid;
+        }
+        lb = lo;
+    }
+    ((uint32_t *)a.lb)[(uint64_t)tau * 256 + k] = lb;
+}
+
+// ================================================================== apply: select pass
+// One wavefront per slab.  rem[e] = (slab rank of the next target of exponent e) - (elements of
+// exponent e seen so far).  Every element decrements its exponent's counter; the lane that takes it
+// from 0 shows that a target lies in this row, whose position then follows from the stable in-row
+// ranks (ballot + mbcnt).  The order in which same-address LDS atomics return does not matter: only
+// whether some lane saw 0 is used.
+__global__ __launch_bounds__(64) void k_select(SelectArgs a) {
+    __shared__ int32_t rem[256];
+    __shared__ uint32_t nxt[256], endj[256], tcur[256], pre[256];
+    if (*a.bad) return;
+    const uint32_t tau = blockIdx.x, ln = lane();
+    const uint32_t t = tensor_of_tile(a.descs, a.n_tensors, tau);
+    const TensorDesc td = a.descs[t];
+    const uint32_t local_tile = tau - td.tile_begin;
+    const Slab sl = slab_of(td, local_tile, a.slab);
+    for (uint32_t k = ln; k < 256; k += 64) {
+        const int32_t g = a.group_of[(uint64_t)t * 256 + k];
+        int32_t r = kFar;
+        uint32_t p = a.pre[(uint64_t)tau * 256 + k];
+        if (g >= 0) {
+            const GroupDev gr = a.groups[g];
+            const uint32_t j0 = a.lb[(uint64_t)tau * 256 + k];
+            const uint32_t je = local_tile + 1 < td.n_tiles ? a.lb[(uint64_t)(tau + 1) * 256 + k] : gr.elem_base + gr.count;
+            if (j0 < je) {
+                const uint32_t tc = a.local[j0] - p;
+                r = (int32_t)min<uint32_t>(tc, (uint32_t)kFar);
+                nxt[k] = j0;
+                endj[k] = je;
+                tcur[k] = tc;
+            }
+        }
+        rem[k] = r;
+        pre[k] = p;
+    }
+    __syncthreads();
+    const uint32_t *po = td.frame;
+    for (uint32_t r = 0; r < sl.nrows; r += kUnroll) {
+        uint32_t ov[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            uint64_t d = sl.d_begin + (uint64_t)(r + u) * 64 + ln;
+            ov[u] = d < sl.d_end ? po[d] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            if (r + u >= sl.nrows) break;
+            const uint64_t d = sl.d_begin + (uint64_t)(r + u) * 64 + ln;
+            const int64_t i0 = (int64_t)(2 * d) - (int64_t)td.lead;
+            const bool v0 = i0 >= (int64_t)sl.lo && i0 < (int64_t)sl.hi;
+            const bool v1 = i0 + 1 >= (int64_t)sl.lo && i0 + 1 < (int64_t)sl.hi;
+            const uint32_t o = ov[u];
+            const uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF;
+            const int32_t r0 = v0 ? atomicSub(&rem[k0], 1) : -1;
+            const int32_t r1 = v1 ? atomicSub(&rem[k1], 1) : -1;
+            uint64_t H0 = ballot(r0 == 0), H1 = ballot(r1 == 0);
+            if (H0 | H1) {
+                __syncthreads();
+                while (H0 | H1) {
+                    const uint32_t k = H0 ? rdlane(k0, (uint32_t)__builtin_ctzll(H0))
+                                          : rdlane(k1, (uint32_t)__builtin_ctzll(H1));
+                    const bool m0 = v0 && k0 == k, m1 = v1 && k1 == k;
+                    const uint64_t M0 = ballot(m0), M1 = ballot(m1);
+                    const int32_t ck = (int32_t)(__popcll(M0) + __popcll(M1));
+                    const int32_t rb = rem[k] + ck;                // remaining before this row, in [0, ck)
+                    const uint32_t seen = tcur[k] - (uint32_t)rb;  // exponent-k elements before this row
+                    const uint32_t rr0 = mbcnt(M0) + mbcnt(M1), rr1 = rr0 + (m0 ? 1u : 0u);
+                    uint32_t j = nxt[k], je = endj[k], tc = tcur[k];
+                    int32_t cur = rb, nrem = kFar;
+                    for (;;) {  // every target of exponent k inside this row, in order
+                        if (m0 && rr0 == (uint32_t)cur) {
+                            a.pos[j] = (uint32_t)i0;
+                            a.val[j] = (uint16_t)(o & 0xFFFF);
+                        }
+                        if (m1 && rr1 == (uint32_t)cur) {
+                            a.pos[j] = (uint32_t)i0 + 1;
+                            a.val[j] = (uint16_t)(o >> 16);
+                        }
+                        if (++j >= je) break;
+                        tc = a.local[j] - pre[k];
+                        // targets are < 2^17 apart inside a slab: the signed difference is exact
+                        const int32_t after_row = (int32_t)(tc - seen) - ck;
+                        if (after_row >= 0) {
+                            nrem = min(after_row, kFar);
+                            break;
+                        }
+                        cur = after_row + ck;
+                    }
+                    __syncthreads();
+                    if (ln == 0) {
+                        rem[k] = nrem;
+                        nxt[k] = j;
+                        tcur[k] = tc;
+                    }
+                    __syncthreads();
+                    H0 &= ~M0;
+                    H1 &= ~M1;
+                }
+            }
+        }
+    }
+}
+
+// new = (old + unzigzag(zz)) mod 2^16; checksum delta per tensor (codec.py:698-700).
+__global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
+    __shared__ unsigned long long sh[256];
+    if (*a.bad) return;
+    const uint64_t b = blockIdx.x;
+    const uint32_t g = group_of_block(a.groups, a.n_groups, b);
+    const GroupDev gr = a.groups[g];
+    const uint64_t kb = b - gr.blk_base;
+    const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
+    const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
+    const uint32_t s = threadIdx.x;
+    unsigned long long d = 0;
+    if (s < cnt) {
+        const uint64_t j = eb + s;
+        const uint32_t p = a.pos[j];
+        if (p == kNone) {
+            atomicOr(a.bad, kBadUnplaced);
+        } else {
+            const uint32_t zz = a.zz[j];
+            const int32_t delta = (int32_t)(zz >> 1) ^ -(int32_t)(zz & 1);
+            const uint32_t old = a.val[j];
+            const uint32_t nu = (uint32_t)((int32_t)old + delta) & 0xFFFF;
+            d = (uint64_t)((int64_t)nu - (int64_t)old) * weight(p);
+            a.val[j] = (uint16_t)nu;
+        }
+    }
+    unsigned long long total;
+    block_exclusive_sum(d, sh, &total);
+    if (s == 0) atomicAdd(&a.tdelta[gr.tensor], total);
+}
+
+__global__ __launch_bounds__(256) void k_scatter(BlockArgs a) {
+    const uint64_t b = blockIdx.x;
+    const uint32_t g = group_of_block(a.groups, a.n_groups, b);
+    const GroupDev gr = a.groups[g];
+    const uint64_t kb = b - gr.blk_base;
+    const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
+    const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
+    const uint32_t s = threadIdx.x;
+    if (s < cnt) a.descs[gr.tensor].base[a.pos[eb + s]] = a.val[eb + s];
+}
+
+inline uint32_t grid1(uint64_t n, uint32_t per) { return (uint32_t)((n + per - 1) / per); }
+
+}  // namespace
+
+// ================================================================== launchers
+#define CRX_LAUNCH(name, kernel, grid, block, stream, ...)                                   \
+    do {                                                                                     \
+        if ((grid) > 0) {                                                                    \
+            timing_begin(stream);                                                            \
+            hipLaunchKernelGGL(kernel, dim3(grid), dim3(block), 0, stream, __VA_ARGS__);     \
+            timing_end(name, stream);                                                        \
+        }                                                                                    \
+    } while (0)
+
+void launch_enc_rank(const EncRankArgs &a, uint32_t tiles, hipStream_t s) {
+    CRX_LAUNCH("enc_rank", k_enc_rank, tiles, 64, s, a);
+}
+void launch_hist(const HistArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("apply_hist", k_hist, tiles, 64, s, a); }
+
+void launch_scan_tables(uint32_t *h, const ScanChunk *chunks, uint32_t n_chunks, const uint32_t *tensor_chunk_begin,
+                        uint32_t n_tensors, uint32_t *csum, uint32_t *totals, hipStream_t s) {
+    CRX_LAUNCH("scan_sum", k_scan_sum, n_chunks, 256, s, h, chunks, csum);
+    CRX_LAUNCH("scan_mid", k_scan_mid, n_tensors, 256, s, csum, tensor_chunk_begin, totals);
+    CRX_LAUNCH("scan_fin", k_scan_fin, n_chunks, 256, s, h, chunks, csum);
+}
+
+void launch_enc_groups(const uint32_t *totals_chg, uint32_t n_tensors, GroupDev *groups, uint32_t *gbase,
+                       unsigned long long *counters, hipStream_t s) {
+    CRX_LAUNCH("enc_groups", k_enc_groups, 1, 1024, s, totals_chg, n_tensors, groups, gbase, counters);
+}
+
+void launch_place(const Chunk *chunks, uint32_t n_chunks, const uint64_t *rec, const TensorDesc *descs,
+                  uint32_t n_tensors, const uint32_t *hall_pre, const uint32_t *hchg_pre, const uint32_t *gbase,
+                  uint64_t *sorted, uint64_t n_sorted, hipStream_t s) {
+    CRX_LAUNCH("place", k_place, n_chunks, 64, s, chunks, rec, descs, n_tensors, hall_pre, hchg_pre, gbase, sorted,
+               n_sorted);
+}
+
+void launch_r0(GroupDev *groups, uint32_t n_groups, const uint64_t *sorted, hipStream_t s) {
+    CRX_LAUNCH("rice_r0", k_r0, grid1(n_groups, 256), 256, s, groups, n_groups, sorted);
+}
+
+void launch_stats(const StatsArgs &a, hipStream_t s) { CRX_LAUNCH("stats", k_stats, grid1(a.n, kElemsPerWG), 256, s, a); }
+
+void launch_code_lengths(const CodeArgs &a, hipStream_t s) {
+    CRX_LAUNCH("code_lengths", k_code_lengths, grid1(a.n, kElemsPerWG), 256, s, a);
+}
+
+void launch_pack(const CodeArgs &a, hipStream_t s) { CRX_LAUNCH("pack", k_pack, grid1(a.n, kElemsPerWG), 256, s, a); }
+
+void launch_block_bits(const unsigned long long *bstart, uint64_t n_blocks, uint32_t *out, unsigned int *overflow,
+                       hipStream_t s) {
+    CRX_LAUNCH("block_bits", k_block_bits, grid1(n_blocks, 256), 256, s, bstart, n_blocks, out, overflow);
+}
+
+void launch_scan_u64(const unsigned long long *in, uint64_t n, unsigned long long *out, hipStream_t s) {
+    CRX_LAUNCH("scan_u64", k_scan1<unsigned long long>, 1, 1024, s, in, n, out);
+}
+
+void launch_scan_u32(const uint32_t *in, uint64_t n, unsigned long long *out, hipStream_t s) {
+    CRX_LAUNCH("scan_u32", k_scan1<uint32_t>, 1, 1024, s, in, n, out);
+}
+
+void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint64_t *per_tile, uint64_t *out,
+                        hipStream_t s) {
+    CRX_LAUNCH("tensor_sums", k_tensor_sums, n_tensors, 256, s, descs, per_tile, out);
+}
+
+void launch_decode(const DecodeArgs &a, hipStream_t s) { CRX_LAUNCH("decode", k_decode, grid1(a.n_blocks, 64), 64, s, a); }
+
+void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
+    CRX_LAUNCH("local_fix", k_local_fix, (uint32_t)n_blocks, 256, s, a);
+}
+
+void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("locate", k_locate, tiles, 256, s, a); }
+
+void launch_select(const SelectArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("select", k_select, tiles, 64, s, a); }
+
+void launch_verify(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
+    CRX_LAUNCH("verify", k_verify, (uint32_t)n_blocks, 256, s, a);
+}
+
+void launch_scatter(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
+    CRX_LAUNCH("scatter", k_scatter, (uint32_t)n_blocks, 256, s, a);
+}
+
+void launch_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial, uint32_t n_parts,
+                     hipStream_t s) {
+    CRX_LAUNCH("checksum", k_checksum, n_parts, 256, s, frame, lead, n, partial, n_parts);
+}
+
+}  // namespace crx

@@ -1,0 +1,153 @@
+/*
+ * crukx.h -- C ABI of the MI355X (gfx950) implementation of the crukx-sync update codec,
+ * wire format version 2 ("CRXS" 0x02).
+ *
+ * The reference (Crukx-dev/crukx-sync v0.2.0) is pure Python/torch and has no FFI; these entry
+ * points replace the functions of its hot path, named per declaration below (paths relative to
+ * the reference repository).  The Python package crukx_sync in crukx-sync_amd/ binds them with
+ * ctypes (INTEGRATION.md shows the binding) and keeps the reference's public API unchanged.
+ *
+ * Conventions
+ *   - Status codes: CRX_OK, CRX_CORRUPT (-> crukx_sync.CorruptUpdate), CRX_INVALID (-> ValueError),
+ *     CRX_DEVICE (HIP runtime error -> RuntimeError), CRX_NOMEM (-> MemoryError).  No C++
+ *     exception crosses the ABI.  `err`/`errlen` receive a NUL-terminated message.
+ *   - Tensors are passed as device pointers to 16-bit bit patterns (bf16 or int16), 2-byte
+ *     aligned, contiguous, with an element count.
+ *   - Device memory: the library calls `alloc(alloc_ctx, nbytes)` for every device buffer it
+ *     needs (the Python layer hands out torch caching-allocator tensors); the caller frees them
+ *     after the call (encode: when the crx_encoded handle is freed).  Work runs on `stream`
+ *     (a hipStream_t); the calls are synchronous with respect to the host on return.
+ *   - `slab` is the number of elements ranked by one wavefront (a multiple of 128, at most
+ *     131072; 0 = default 65536).  It plays the role of codec._SLAB (codec.py:30): it changes
+ *     how the work is cut, never the bytes.
+ */
+#ifndef CRUKX_H
+#define CRUKX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CRX_ABI_VERSION 1
+
+#define CRX_OK 0
+#define CRX_CORRUPT 1
+#define CRX_INVALID 2
+#define CRX_DEVICE 3
+#define CRX_NOMEM 4
+
+typedef void *(*crx_alloc_fn)(void *alloc_ctx, uint64_t nbytes);
+
+typedef struct crx_update crx_update;   /* a parsed update (host header + block table) */
+typedef struct crx_encoded crx_encoded; /* an encoded update (host header, device bits) */
+
+/* ABI version of the loaded library (CRX_ABI_VERSION). */
+int32_t crx_abi_version(void);
+
+/* ------------------------------------------------------------------ wire format (host)
+ * Replaces wire.parse (src/crukx_sync/wire.py:126-212): magic, version, every limit of
+ * docs/FORMAT.md:46-57 in the reference's order.  `data` holds the whole update (host memory).
+ * With `payload_on_device` != 0 the caller promises only the bytes up to the payload start plus
+ * the final byte; crx_parse then checks the header and block table and stores the payload
+ * offset, and the payload itself must be passed to crx_apply as a device pointer. */
+int32_t crx_parse(const uint8_t *data, uint64_t len, crx_update **out, char *err, uint64_t errlen);
+/* Parses from a prefix of an update held elsewhere: `prefix` has `prefix_len` bytes of an update
+ * of `total_len` bytes whose last byte is `last_byte`.  Returns CRX_OK, CRX_CORRUPT, or
+ * CRX_INVALID with *need set to the prefix length required (then call again). */
+int32_t crx_parse_prefix(const uint8_t *prefix, uint64_t prefix_len, uint64_t total_len, uint8_t last_byte,
+                         crx_update **out, uint64_t *need, char *err, uint64_t errlen);
+void crx_update_free(crx_update *u);
+
+/* Accessors (wire.Update, wire.py:20-48). */
+int64_t crx_update_n_tables(const crx_update *u);
+int32_t crx_update_table(const crx_update *u, int64_t i, int32_t *exponent, int64_t *n_sym,
+                         uint32_t *symbols /* n_sym or NULL */, uint8_t *lengths /* n_sym or NULL */);
+int64_t crx_update_n_tensors(const crx_update *u);
+int32_t crx_update_tensor(const crx_update *u, int64_t i, const uint8_t **name, uint64_t *name_len,
+                          uint64_t *numel, uint64_t *checksum, int32_t *n_groups);
+int32_t crx_update_group(const crx_update *u, int64_t i, int32_t g, int32_t *exponent, uint64_t *count,
+                         int32_t *rice);
+uint64_t crx_update_n_blocks(const crx_update *u);
+/* Copies the block table (n_blocks u32) into `out`. */
+int32_t crx_update_block_bits(const crx_update *u, uint32_t *out);
+uint64_t crx_update_payload_offset(const crx_update *u);
+uint64_t crx_update_payload_len(const crx_update *u);
+uint64_t crx_update_total_changes(const crx_update *u);
+
+/* ------------------------------------------------------------------ apply (device)
+ * Replaces codec.apply (src/crukx_sync/codec.py:578-717) including the block decoder
+ * (codec.py:504-575, _triton.py:33-106): decode every block, locate every change in the stable
+ * exponent order of the receiver's old weights, verify each tensor's checksum, and only then
+ * write.  `targets[i]` is the receiver tensor for update tensor i (crx_update_tensor order) with
+ * `numels[i]` elements; `has_cache[i]`/`cache_vals[i]` give a trusted old checksum (else one is
+ * computed from the weights).  `payload_dev` is NULL to upload the payload from the parsed host
+ * bytes, or a device pointer to the payload bytes.  On any status but CRX_OK nothing is written.
+ * `*changed` receives the number of changed elements. */
+int32_t crx_apply(const crx_update *u, const uint8_t *payload_dev, uint16_t *const *targets,
+                  const uint64_t *numels, const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab,
+                  void *stream, crx_alloc_fn alloc, void *alloc_ctx, uint64_t *changed, char *err,
+                  uint64_t errlen);
+
+/* ------------------------------------------------------------------ encode (device)
+ * Replaces codec.encode (src/crukx_sync/codec.py:278-420): rank changes in stable exponent order,
+ * gaps and residuals, per-group Rice parameters, one canonical Huffman table per exponent, bit
+ * packing and the block table.  Tensors in caller order; `has_cache`/`cache_vals` give the
+ * sender's cached checksum of old (new checksum = cache + delta), else the checksum of new is
+ * computed in full.  Fails with CRX_INVALID if a block reaches 2^32 bits (codec.py:417-419). */
+int32_t crx_encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news, const uint64_t *numels,
+                   const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab, void *stream,
+                   crx_alloc_fn alloc, void *alloc_ctx, crx_encoded **out, char *err, uint64_t errlen);
+/* Tensor t of the encode call is in the update (has a changed element). */
+int32_t crx_encoded_present(const crx_encoded *e, int32_t t);
+/* New checksum of tensor t (valid when present). */
+uint64_t crx_encoded_checksum(const crx_encoded *e, int32_t t);
+uint64_t crx_encoded_total_changes(const crx_encoded *e);
+/* Serialized size (wire.serialize, wire.py:64-89) given the names of the encode call's tensors. */
+uint64_t crx_encoded_size(const crx_encoded *e, const char *const *names, const uint64_t *name_lens);
+/* Writes the serialized update to `dst` (host memory, or device memory when dst_on_device). */
+int32_t crx_encoded_write(const crx_encoded *e, const char *const *names, const uint64_t *name_lens, uint8_t *dst,
+                          int32_t dst_on_device, void *stream, char *err, uint64_t errlen);
+/* Header pieces for wire.Update materialisation. */
+int64_t crx_encoded_n_tables(const crx_encoded *e);
+int32_t crx_encoded_table(const crx_encoded *e, int64_t i, int32_t *exponent, int64_t *n_sym, uint32_t *symbols,
+                          uint8_t *lengths);
+int32_t crx_encoded_n_groups(const crx_encoded *e, int32_t t);
+int32_t crx_encoded_group(const crx_encoded *e, int32_t t, int32_t g, int32_t *exponent, uint64_t *count,
+                          int32_t *rice);
+uint64_t crx_encoded_n_blocks(const crx_encoded *e);
+int32_t crx_encoded_block_bits(const crx_encoded *e, uint32_t *out, void *stream);
+uint64_t crx_encoded_payload_len(const crx_encoded *e);
+int32_t crx_encoded_payload(const crx_encoded *e, uint8_t *out, void *stream);
+void crx_encoded_free(crx_encoded *e);
+
+/* ------------------------------------------------------------------ checksum (device)
+ * Replaces codec.checksum (src/crukx_sync/codec.py:61-68): sum(u_i * (splitmix64(i) | 1)) mod 2^64
+ * over n 16-bit patterns, as a deterministic device reduction. */
+int32_t crx_checksum(const uint16_t *data, uint64_t n, void *stream, crx_alloc_fn alloc, void *alloc_ctx,
+                     uint64_t *out, char *err, uint64_t errlen);
+
+/* ------------------------------------------------------------------ host helpers
+ * codec.huffman_lengths (codec.py:71-98): code lengths limited to 17 bits. */
+int32_t crx_huffman_lengths(const uint64_t *counts, int64_t n, int32_t *lengths);
+/* codec.canonical_codes (codec.py:101-111). */
+int32_t crx_canonical_codes(const int32_t *lengths, int64_t n, uint32_t *codes);
+/* codec._rice_params (codec.py:268-275) for one group from its sums: `count` changes whose gaps
+ * sum to `gap_sum`; `shifted[k]` = sum(gap >> cand[k]) for the candidates written to `cand`
+ * by crx_rice_candidates.  Returns the chosen parameter. */
+void crx_rice_candidates(uint64_t count, uint64_t gap_sum, int32_t cand[3]);
+int32_t crx_rice_choose(uint64_t count, const int32_t cand[3], const uint64_t shifted[3]);
+
+/* ------------------------------------------------------------------ timing
+ * When enabled, each kernel launch is bracketed by HIP events on its stream and the durations
+ * accumulate per kernel name.  crx_timing_read writes "name calls total_ms\n" lines. */
+void crx_timing_enable(int32_t on);
+void crx_timing_reset(void);
+int32_t crx_timing_read(char *buf, uint64_t len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CRUKX_H */

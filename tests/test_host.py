@@ -1,0 +1,176 @@
+"""Host-side parts of the product, on CPU: the C ABI exports, the native parser (every limit of the
+format), Huffman code lengths, canonical codes and the Rice choice against the reference's golden
+vectors, and the oracle's parser on every single-byte flip of golden updates.
+"""
+
+import hashlib
+import json
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import crukx_sync
+import oracle
+from crukx_sync import _native, codec, wire
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_every_declared_symbol():
+    header = open(os.path.join(ROOT, "include", "crukx.h")).read()
+    declared = set(re.findall(r"\b(crx_[a-z0-9_]+)\s*\(", header))
+    declared.discard("crx_alloc_fn")
+    L = _native.lib()
+    missing = [s for s in sorted(declared) if not hasattr(L, s)]
+    assert not missing, missing
+    assert declared == set(_native.SIGNATURES), declared ^ set(_native.SIGNATURES)
+    assert L.crx_abi_version() == _native.ABI_VERSION
+
+
+def test_huffman_lengths_match_reference(golden):
+    for c in golden["huffman"]["cases"]:
+        assert codec.huffman_lengths(c["counts"]) == c["lengths"], c["counts"][:8]
+        assert codec.canonical_codes(c["lengths"]) == c["codes"]
+    for b in golden["huffman"]["big"]:
+        cnt = [int(x) for x in np.random.default_rng(b["seed"]).integers(1, b["hi"], b["n"])]
+        assert hashlib.sha256(json.dumps(codec.huffman_lengths(cnt)).encode()).hexdigest() == b["lengths_sha"]
+
+
+def test_rice_choice_matches_reference(golden):
+    for c in golden["rice"]["cases"]:
+        g = np.array(c["gaps"], dtype=np.int64)
+        r = codec.rice_parameter(len(g), int(g.sum()), lambda k: int((g >> k).sum()))
+        assert r == c["rice"], c["gaps"][:5]
+
+
+def test_rice_r0_agrees_with_fp64_log2():
+    """The host r0 is the reference's fp64 form (codec.py:271-272); the device's exact integer form
+    (largest k with count * 2^k <= sum) agrees with it on its domain, sum < 2^32."""
+    import ctypes
+    L = _native.lib()
+    rng = np.random.default_rng(0)
+    cases = [(c, s) for c in (1, 2, 3, 7, 1000, 123457) for s in (0, 1, c - 1, c, c + 1, 2 * c, 2 * c - 1)]
+    cases += [(int(c), int(c) * (1 << k) + d) for c in rng.integers(1, 1 << 20, 50) for k in range(0, 31, 3)
+              for d in (-1, 0, 1)]
+    for count, gap_sum in cases:
+        if gap_sum < 0:
+            continue
+        cand = (ctypes.c_int32 * 3)()
+        L.crx_rice_candidates(count, gap_sum, cand)
+        r0 = int(np.clip(np.floor(np.log2(max(gap_sum / count, 1.0))), 0, 30))
+        assert cand[1] == r0, (count, gap_sum)
+        if gap_sum < 1 << 32:
+            k = 0
+            while k < 30 and count << (k + 1) <= gap_sum:
+                k += 1
+            assert k == r0, (count, gap_sum)
+
+
+def _golden_bytes(golden):
+    return {n: bytes.fromhex(r["update"]["hex"]) for n, r in golden["updates"]["single"].items()
+            if "hex" in r["update"]}
+
+
+def test_parse_golden_updates_round_trip(golden):
+    for name, data in _golden_bytes(golden).items():
+        u = wire.parse(data)
+        plain = wire.Update(u.tables, u.tensors, u.block_bits, u.payload)
+        assert wire.serialize(plain) == data, name
+        assert u.total_changes == sum(g.count for t in u.tensors for g in t.groups)
+
+
+def test_hostile_headers_fail_in_parse():
+    from test_oracle import hostile_updates
+    for h in hostile_updates():
+        with pytest.raises(crukx_sync.CorruptUpdate):
+            wire.parse(h)
+        a = torch.zeros(100, dtype=torch.int16)
+        with pytest.raises(crukx_sync.CorruptUpdate):
+            crukx_sync.apply_update({"w": a.clone()}, h)
+
+
+def test_hostile_counts_are_rejected_before_allocating():
+    out = bytearray(b"CRXS\x02")
+    wire.write_varint(out, 1)
+    out += b"\x00\x01\x02\x01"
+    wire.write_varint(out, 1)
+    wire.write_varint(out, 1)
+    out += b"w"
+    wire.write_varint(out, 1 << 22)
+    out += bytes(8)
+    wire.write_varint(out, 1)
+    out += b"\x00"
+    wire.write_varint(out, 1 << 22)
+    out += b"\x00"
+    out += bytes(4 * ((1 << 22) // 256))
+    wire.write_varint(out, 0)
+    with pytest.raises(crukx_sync.CorruptUpdate):
+        crukx_sync.apply_update({"w": torch.zeros(1 << 22, dtype=torch.int16)}, bytes(out))
+
+
+@pytest.mark.parametrize("name", ["rl_200k", "many_tensors", "slab_4097", "extreme", "three_tensors"])
+def test_parser_agrees_with_oracle_on_every_byte_flip(golden, name):
+    data = _golden_bytes(golden).get(name)
+    if data is None:
+        pytest.skip("not stored inline")
+    for i in range(len(data)):
+        for x in (0x01, 0x80, 0xFF):
+            bad = bytearray(data)
+            bad[i] ^= x
+            bad = bytes(bad)
+            try:
+                oracle.parse_check(bad)
+                ref_ok = True
+            except oracle.OracleCorrupt:
+                ref_ok = False
+            try:
+                wire.parse(bad)
+                ok = True
+            except crukx_sync.CorruptUpdate:
+                ok = False
+            assert ok == ref_ok, (name, i, x)
+
+
+def test_varint_limits():
+    out = bytearray()
+    wire.write_varint(out, (1 << 63) - 1)
+    assert len(out) == 9
+    with pytest.raises(ValueError):
+        wire.write_varint(bytearray(), 1 << 63)
+    # non-canonical varints (trailing zero groups) are accepted, as in the reference's reader
+    upd = b"CRXS\x02" + b"\x80\x00" + b"\x80\x80\x00" + b"\x00"
+    u = wire.parse(upd)
+    assert u.tensors == [] and u.tables == []
+    # 10th byte carrying bit 63 is out of range
+    with pytest.raises(crukx_sync.CorruptUpdate):
+        wire.parse(b"CRXS\x02" + b"\x80" * 9 + b"\x01" + b"\x00\x00")
+
+
+def test_empty_update_bytes():
+    assert crukx_sync.encode_update({}, {}) == b"CRXS\x02\x00\x00\x00"
+    assert crukx_sync.apply_update({}, b"CRXS\x02\x00\x00\x00").tensors == 0
+
+
+def test_api_errors_before_any_device_work():
+    a = torch.zeros(10, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        crukx_sync.encode_update({"w": a}, {"x": a})
+    with pytest.raises(ValueError):
+        crukx_sync.encode_update({"w": a}, {"w": a.float()})
+    with pytest.raises(ValueError):
+        crukx_sync.encode_update({"w": a}, {"w": torch.zeros(11, dtype=torch.bfloat16)})
+    with pytest.raises(ValueError):
+        crukx_sync.encode_update({"w": torch.zeros(4, 4, dtype=torch.bfloat16).t()},
+                                 {"w": torch.zeros(4, 4, dtype=torch.bfloat16)})
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the behaviour without a HIP device")
+def test_no_silent_cpu_fallback():
+    a = torch.zeros(10, dtype=torch.bfloat16)
+    b = a.clone()
+    b[3] = 1.0
+    with pytest.raises(RuntimeError, match="HIP"):
+        crukx_sync.encode_update({"w": a}, {"w": b})

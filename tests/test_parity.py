@@ -1,0 +1,192 @@
+"""Parity of the HIP path with the reference, on the GPU.
+
+- Encode: for every golden scenario, the bytes from the gfx950 kernels equal the bytes the
+  reference wrote (tests/golden/updates.json), and the sender checksums agree.
+- Apply: the golden updates applied by the HIP path reproduce the new weights; results equal the
+  oracle's on the same inputs, including rejections.
+- Chained steps with both checksum caches (four tensors of 26.6M weights, three steps).
+- Slab size (codec._SLAB) and the device-resident byte path never change the bytes.
+- At sizes the oracle cannot check in seconds: size-independent properties (round trip exact,
+  sender cache == receiver cache, checksum of the result equals a full recomputation).
+"""
+
+import hashlib
+
+import pytest
+import torch
+
+import crukx_sync
+import oracle
+import scenarios
+from crukx_sync import codec, workloads
+
+pytestmark = pytest.mark.gpu
+
+_SC = {}
+
+
+def _scen():
+    if not _SC:
+        _SC.update(scenarios.single_scenarios())
+    return _SC
+
+
+def _cuda(d):
+    return {k: v.to("cuda") for k, v in d.items()}
+
+
+def _check(upd, rec):
+    assert len(upd) == rec["len"]
+    if "hex" in rec:
+        assert upd.hex() == rec["hex"]
+    assert hashlib.sha256(upd).hexdigest() == rec["sha256"]
+
+
+@pytest.mark.parametrize("name", sorted(scenarios.single_scenarios().keys()))
+def test_encode_bytes_equal_reference(golden, name):
+    old, new = _scen()[name]
+    rec = golden["updates"]["single"][name]
+    assert scenarios.bits_sha(old) == rec["inputs_old"] and scenarios.bits_sha(new) == rec["inputs_new"]
+    chk = {}
+    upd = crukx_sync.encode_update(_cuda(old), _cuda(new), chk)
+    _check(upd, rec["update"])
+    assert chk == rec["sender_checksums"]
+
+
+@pytest.mark.parametrize("name", sorted(scenarios.single_scenarios().keys()))
+def test_apply_reference_bytes(golden, name):
+    old, new = _scen()[name]
+    rec = golden["updates"]["single"][name]
+    upd = oracle.encode_update(old, new)  # the oracle's bytes equal the reference's (test_oracle)
+    _check(upd, rec["update"])
+    w = _cuda({k: v.clone() for k, v in old.items()})
+    stats = crukx_sync.apply_update(w, upd)
+    ref = {k: v.clone() for k, v in old.items()}
+    n = oracle.apply_update(ref, upd)
+    assert stats.changed == n
+    for k in new:
+        assert torch.equal(w[k].cpu().view(torch.int16), new[k].view(torch.int16)), k
+
+
+def test_small4_chain_with_caches(golden):
+    states = scenarios.chain_small4(3)
+    rec = golden["updates"]["chains"]["small4_chain"]
+    assert scenarios.bits_sha(states[0]) == rec["inputs_0"]
+    send, recv = {}, {}
+    w = _cuda(states[0])
+    prev = _cuda(states[0])
+    for s in range(1, len(states)):
+        cur = _cuda(states[s])
+        upd = crukx_sync.encode_update(prev, cur, send)
+        _check(upd, rec["steps"][s - 1]["update"])
+        assert send == rec["steps"][s - 1]["sender_checksums"]
+        crukx_sync.apply_update(w, upd, recv)
+        for k in w:
+            assert torch.equal(w[k].view(torch.int16), cur[k].view(torch.int16))
+        prev = cur
+    assert send == {k: v[0] for k, v in recv.items()}
+
+
+def test_cache_chain(golden):
+    states = scenarios.chain_cache(5)
+    rec = golden["updates"]["chains"]["cache_chain"]
+    send, recv = {}, {}
+    w = _cuda(states[0])
+    for s in range(1, len(states)):
+        upd = crukx_sync.encode_update(_cuda(states[s - 1]), _cuda(states[s]), send)
+        _check(upd, rec["steps"][s - 1]["update"])
+        crukx_sync.apply_update(w, upd, recv)
+    assert torch.equal(w["w"].cpu().view(torch.int16), states[-1]["w"].view(torch.int16))
+
+
+@pytest.mark.parametrize("slab", [128, 256, 4096, 1 << 17])
+@pytest.mark.parametrize("name", ["rl_200k", "many_tensors", "slab_12293", "edges", "sweep_rho0.03_p0.7"])
+def test_slab_size_never_changes_bytes(golden, monkeypatch, slab, name):
+    monkeypatch.setattr(codec, "_SLAB", slab)
+    old, new = _scen()[name]
+    upd = crukx_sync.encode_update(_cuda(old), _cuda(new))
+    _check(upd, golden["updates"]["single"][name]["update"])
+    w = _cuda({k: v.clone() for k, v in old.items()})
+    crukx_sync.apply_update(w, upd)
+    for k in new:
+        assert torch.equal(w[k].cpu().view(torch.int16), new[k].view(torch.int16))
+
+
+def test_device_resident_bytes_and_apply(golden):
+    old, new = _scen()["three_tensors"]
+    dev_upd = crukx_sync.encode_update_device(_cuda(old), _cuda(new))
+    assert dev_upd.is_cuda and dev_upd.dtype == torch.uint8
+    _check(dev_upd.cpu().numpy().tobytes(), golden["updates"]["single"]["three_tensors"]["update"])
+    w = _cuda({k: v.clone() for k, v in old.items()})
+    stats = crukx_sync.apply_update(w, dev_upd)
+    assert stats.bytes == dev_upd.numel()
+    for k in new:
+        assert torch.equal(w[k].cpu().view(torch.int16), new[k].view(torch.int16))
+
+
+def test_device_resident_corruption_is_rejected():
+    a, b = scenarios.rl_pair(20_000, seed=13)
+    dev_upd = crukx_sync.encode_update_device({"w": a.cuda()}, {"w": b.cuda()})
+    host = dev_upd.cpu().numpy().tobytes()
+    for i in range(len(host) - 1, len(host) - 200, -7):  # payload bytes
+        bad = dev_upd.clone()
+        bad[i] ^= 0x10
+        w = {"w": a.cuda()}
+        try:
+            crukx_sync.apply_update(w, bad)
+        except crukx_sync.CorruptUpdate:
+            assert torch.equal(w["w"].cpu().view(torch.int16), a.view(torch.int16))
+        else:
+            assert torch.equal(w["w"].cpu().view(torch.int16), b.view(torch.int16))
+
+
+def test_checksum_matches_oracle():
+    for n in (1, 2, 3, 255, 4097, 1 << 20, 3_000_001):
+        t = torch.randint(-32768, 32768, (n,), dtype=torch.int16, generator=torch.Generator().manual_seed(n))
+        assert codec.checksum(t.cuda()) == oracle.checksum(t)
+        if n > 2:  # an odd 16-bit offset (not 32-bit aligned)
+            assert codec.checksum(t.cuda()[1:]) == oracle.checksum(t[1:])
+
+
+def test_corruptions_match_oracle_verdicts():
+    """Random multi-byte corruptions: the HIP apply and the oracle agree on accept/reject, and the
+    accepted results are identical."""
+    a, b = scenarios.rl_pair(50_000, seed=21)
+    upd = bytearray(crukx_sync.encode_update({"w": a.cuda()}, {"w": b.cuda()}))
+    g = torch.Generator().manual_seed(3)
+    for _ in range(200):
+        bad = bytearray(upd)
+        for i in torch.randint(0, len(upd), (3,), generator=g).tolist():
+            bad[i] = int(torch.randint(0, 256, (1,), generator=g))
+        bad = bytes(bad)
+        w_hip, w_ref = {"w": a.cuda()}, {"w": a.clone()}
+        hip_ok = ref_ok = True
+        try:
+            crukx_sync.apply_update(w_hip, bad)
+        except ValueError:
+            hip_ok = False
+        try:
+            oracle.apply_update(w_ref, bad)
+        except ValueError:
+            ref_ok = False
+        assert hip_ok == ref_ok
+        assert torch.equal(w_hip["w"].cpu().view(torch.int16), w_ref["w"].view(torch.int16))
+
+
+def test_qwen_layer_sized_round_trip_properties():
+    """One 7B-shaped decoder layer plus the final norm (233M weights), three chained steps with
+    caches: exact round trips, sender cache == receiver cache == full checksums of the result."""
+    shapes = [s for s in workloads.qwen25_shapes("qwen2.5-7b") if s[0].startswith("model.layers.0.")
+              or s[0] == "model.norm.weight"]
+    prev = workloads.make_weights(shapes, seed=3, device="cuda")
+    recv = {k: v.clone() for k, v in prev.items()}
+    send, rc = {}, {}
+    for s in range(1, 4):
+        cur = workloads.make_step(prev, s, rho=0.01, seed=3)
+        crukx_sync.apply_update(recv, crukx_sync.encode_update(prev, cur, send), rc)
+        for k in cur:
+            assert torch.equal(recv[k].view(torch.int16), cur[k].view(torch.int16)), k
+        prev = cur
+    assert send == {k: v[0] for k, v in rc.items()}
+    for k in ("model.layers.0.mlp.down_proj.weight", "model.norm.weight"):
+        assert send[k] == codec.checksum(prev[k])
