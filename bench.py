@@ -41,7 +41,19 @@ def main():
     ap.add_argument("--cpu-baseline-layers", type=int, default=2,
                     help="decoder layers in the CPU baseline sample (0 disables it)")
     ap.add_argument("--host-bytes", action="store_true", help="also time the bytes API (PCIe-inclusive)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run three 2 GiB device-to-device copies (reference for HBM traffic counters)")
     args = ap.parse_args()
+
+    if args.calibrate_copy:
+        import torch
+        a = torch.ones(1 << 31, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read_per_copy": a.numel(), "bytes_written_per_copy": b.numel()}))
+        return
 
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the update codec has no multi-GPU path "

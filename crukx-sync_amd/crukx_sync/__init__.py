@@ -78,4 +78,4 @@ def apply_update(weights: Mapping[str, torch.Tensor], update, checksums: dict | 
     with torch.no_grad():
         changed = codec.apply(weights, u, checksums)
     n = update.numel() if isinstance(update, torch.Tensor) else len(update)
-    return UpdateStats(len(u.tensors), changed, n)
+    return UpdateStats(len(u.headers()[0]), changed, n)

@@ -39,6 +39,7 @@ SIGNATURES = {
     "crx_update_n_tensors": (_i64, [_vp]),
     "crx_update_tensor": (_i32, [_vp, _i64, ctypes.POINTER(_vp), _u64p, _u64p, _u64p, _i32p]),
     "crx_update_group": (_i32, [_vp, _i64, _i32, _i32p, _u64p, _i32p]),
+    "crx_update_headers": (_i32, [_vp, _vp, _u64, _u64p, _vp, _vp, _vp]),
     "crx_update_n_blocks": (_u64, [_vp]),
     "crx_update_block_bits": (_i32, [_vp, _vp]),
     "crx_update_payload_offset": (_u64, [_vp]),

@@ -268,23 +268,23 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     (codec.py:578-717)."""
     if not isinstance(u, ParsedUpdate):
         u = parse(serialize(u))
-    headers = u.tensors
-    if not headers:
+    names, numels, header_chk = u.headers()
+    if not names:
         return 0
     targets = []
-    for h in headers:
-        if h.name not in weights:
-            raise ValueError(f"update has tensor {h.name!r} that the receiver does not have")
-        a = bits16(h.name, weights[h.name])
-        if a.numel() != h.numel:
-            raise ValueError(f"{h.name}: update is for {h.numel} elements, receiver has {a.numel()}")
+    for name, numel in zip(names, numels):
+        if name not in weights:
+            raise ValueError(f"update has tensor {name!r} that the receiver does not have")
+        a = bits16(name, weights[name])
+        if a.numel() != numel:
+            raise ValueError(f"{name}: update is for {numel} elements, receiver has {a.numel()}")
         targets.append(a)
     src = targets[0].device
     if any(a.device != src for a in targets):
         raise ValueError("all updated tensors must be on one device")
     dev = _hip_device(src)
     staged = [a.to(dev) for a in targets] if src != dev else targets
-    cache = [_cache_get(checksums, h.name, weights[h.name]) for h in headers]
+    cache = [_cache_get(checksums, name, weights[name]) for name in names]
     has = [0 if c is None else 1 for c in cache]
     vals = [0 if c is None else c & _MASK64 for c in cache]
     payload_dev = 0
@@ -305,11 +305,11 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     ws.check()
     ws.release()
     _native.raise_for(rc, err)
-    for h, a, s in zip(headers, targets, staged):
+    for name, a, s in zip(names, targets, staged):
         if s is not a:
             a.copy_(s)  # an in-place op: bumps the tensor's version like index_put_ does
         else:
-            torch.autograd.graph.increment_version(weights[h.name])
+            torch.autograd.graph.increment_version(weights[name])
     if checksums is not None:  # record the version after our own write
-        checksums.update({h.name: (h.checksum, weights[h.name]._version) for h in headers})
+        checksums.update({name: (c, weights[name]._version) for name, c in zip(names, header_chk)})
     return changed.value

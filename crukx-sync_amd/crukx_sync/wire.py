@@ -144,6 +144,26 @@ class ParsedUpdate(Update):
     def handle(self):
         return self._h
 
+    def headers(self) -> tuple[list[str], list[int], list[int]]:
+        """(names, numels, checksums) of the update's tensors, in order, from one native call."""
+        if getattr(self, "_headers", None) is None:
+            from . import _native
+            L = _native.lib()
+            n = L.crx_update_n_tensors(self._h)
+            need = ctypes.c_uint64()
+            L.crx_update_headers(self._h, None, 0, ctypes.byref(need), None, None, None)
+            names = ctypes.create_string_buffer(max(need.value, 1))
+            ends, numels, chks = ((ctypes.c_uint64 * max(n, 1))() for _ in range(3))
+            _native.raise_for(L.crx_update_headers(self._h, names, need.value, ctypes.byref(need), ends, numels,
+                                                   chks), None)
+            raw = names.raw
+            out, start = [], 0
+            for i in range(n):
+                out.append(raw[start:ends[i]].decode("utf-8"))
+                start = ends[i]
+            self._headers = (out, list(numels[:n]), list(chks[:n]))
+        return self._headers
+
     @property
     def tensors(self) -> list[TensorHeader]:
         if self._tensors is None:

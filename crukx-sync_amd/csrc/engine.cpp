@@ -695,6 +695,24 @@ int32_t crx_update_group(const crx_update *u, int64_t i, int32_t g, int32_t *exp
     return CRX_OK;
 }
 
+int32_t crx_update_headers(const crx_update *u, char *names, uint64_t names_cap, uint64_t *names_len,
+                           uint64_t *name_ends, uint64_t *numels, uint64_t *checksums) {
+    uint64_t total = 0;
+    for (const TensorHeader &t : u->u.tensors) total += t.name.size();
+    *names_len = total;
+    if (total > names_cap) return CRX_INVALID;
+    uint64_t off = 0;
+    for (size_t i = 0; i < u->u.tensors.size(); ++i) {
+        const TensorHeader &t = u->u.tensors[i];
+        std::memcpy(names + off, t.name.data(), t.name.size());
+        off += t.name.size();
+        name_ends[i] = off;
+        numels[i] = t.numel;
+        checksums[i] = t.checksum;
+    }
+    return CRX_OK;
+}
+
 uint64_t crx_update_n_blocks(const crx_update *u) { return u->u.block_bits.size(); }
 
 int32_t crx_update_block_bits(const crx_update *u, uint32_t *out) {

@@ -73,73 +73,100 @@ __device__ uint32_t group_of_block(const GroupDev *g, uint32_t n, uint64_t b) {
     return lo;
 }
 
+// ================================================================== slab streaming
+// A wavefront reads its slab as rows of 64 lanes x one 32-bit word (two consecutive bf16), 32-bit
+// offsets relative to the slab's first frame word.  Interior rows need no masking; only the first
+// (odd start) and last (partial) rows do.
 struct Slab {
-    uint64_t lo, hi;          // tensor elements [lo, hi)
-    uint64_t d_begin, d_end;  // 32-bit frame words covering them
+    uint32_t first;   // frame word index of the slab's first word
+    uint32_t nwords;  // words covering the slab
+    uint32_t f_lo;    // valid 16-bit offsets within the slab's words: [f_lo, f_hi)
+    uint32_t f_hi;
+    uint32_t base;    // tensor index of offset 0 (mod 2^32): element f is tensor element base + f
     uint32_t nrows;
 };
 
 __device__ __forceinline__ Slab slab_of(const TensorDesc &td, uint32_t local, uint32_t slab) {
+    const uint64_t lo = (uint64_t)local * slab, hi = min(lo + slab, td.numel);
+    const uint64_t d_begin = (lo + td.lead) >> 1, d_end = (hi + td.lead + 1) >> 1;
     Slab s;
-    s.lo = (uint64_t)local * slab;
-    s.hi = min(s.lo + slab, td.numel);
-    s.d_begin = (s.lo + td.lead) >> 1;
-    s.d_end = (s.hi + td.lead + 1) >> 1;
-    s.nrows = (uint32_t)((s.d_end - s.d_begin + 63) / 64);
+    s.first = (uint32_t)d_begin;
+    s.nwords = (uint32_t)(d_end - d_begin);
+    s.f_lo = (uint32_t)(lo + td.lead - 2 * d_begin);
+    s.f_hi = (uint32_t)(hi + td.lead - 2 * d_begin);
+    s.base = (uint32_t)(2 * d_begin - td.lead);
+    s.nrows = (s.nwords + 63) / 64;
     return s;
 }
 
+__device__ __forceinline__ bool row_full(const Slab &s, uint32_t r) {
+    return r * kRow >= s.f_lo && r * kRow + kRow <= s.f_hi;
+}
+
 // ================================================================== encode: rank pass
-// One wavefront per slab.  Reads old and new once.  For every changed element it records its rank
-// among same-exponent elements of the slab (`rank`), its rank among same-exponent *changes* of the
-// slab (`rc`), the old exponent and the zigzag residual; per slab it writes both histograms, the
-// checksum delta of the changes and (cold) the full checksum of new.
-__device__ void flush_records(const EncRankArgs &a, uint32_t tau, const uint64_t *rbuf, uint32_t cnt) {
+// One wavefront per slab; reads old and new once.  For every changed element it needs its rank among
+// the slab's elements with the same old exponent (`rank`) and among the slab's changes with that
+// exponent (`rc`): the running per-exponent counts in LDS give the part before the row, ballots and
+// mbcnt the stable part inside the row.  Changed elements are buffered in LDS as (rank, rc, exponent,
+// offset, old, new) and finished in dense batches: zigzag residual, checksum delta, 64-bit record.
+constexpr int kChgCap = 384;  // buffered changes; a flush leaves room for one full row
+
+__device__ void flush_changes(const EncRankArgs &a, uint32_t tau, const Slab &sl, const uint64_t *meta,
+                              const uint32_t *vals, uint32_t cnt, uint64_t &dacc) {
     __syncthreads();
     unsigned long long base = 0;
     if (lane() == 0) base = atomicAdd(&a.counters[0], (unsigned long long)cnt);
     base = __shfl(base, 0, 64);
-    if (base + cnt <= a.rec_cap) {
-        for (uint32_t j = lane(); j < cnt; j += 64) a.rec[base + j] = rbuf[j];
-        if (lane() == 0) {
-            unsigned long long ci = atomicAdd(&a.counters[1], 1ULL);
+    const bool fits = base + cnt <= a.rec_cap;
+    for (uint32_t j = lane(); j < cnt; j += 64) {
+        const uint64_t m = meta[j];
+        const uint32_t v = vals[j];
+        const uint32_t o16 = v & 0xFFFF, n16 = v >> 16;
+        const uint32_t f = (uint32_t)(m >> 42);
+        dacc += (uint64_t)((int64_t)n16 - (int64_t)o16) * weight(sl.base + f);
+        if (fits) a.rec[base + j] = (m & ((1ULL << 42) - 1)) | ((uint64_t)zigzag(o16, n16) << 42);
+    }
+    if (lane() == 0) {
+        if (fits) {
+            const unsigned long long ci = atomicAdd(&a.counters[1], 1ULL);
             if (ci < a.chunk_cap) a.chunks[ci] = Chunk{tau, cnt, base};
             else atomicOr(&a.counters[2], 2ULL);
+        } else {
+            atomicOr(&a.counters[2], 1ULL);
         }
-    } else if (lane() == 0) {
-        atomicOr(&a.counters[2], 1ULL);
     }
     __syncthreads();
 }
 
 template <bool COLD>
 __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32_t tau, const Slab &sl,
-                              uint32_t *hall, uint32_t *hchg, uint64_t *rbuf) {
-    const uint32_t ln = lane();
-    const uint32_t rep = ln & 3;
+                              uint32_t *hall, uint32_t *hchg, uint64_t *meta, uint32_t *vals) {
+    const uint32_t ln = lane(), rep = ln & 3;
+    const uint32_t *po = td.frame + sl.first, *pn = td.frame_new + sl.first;
     uint32_t cnt = 0;
     uint64_t dacc = 0, facc = 0;
-    const uint32_t *po = td.frame, *pn = td.frame_new;
-    for (uint32_t r = 0; r < sl.nrows; r += kUnroll) {
+    for (uint32_t r0 = 0; r0 < sl.nrows; r0 += kUnroll) {
         uint32_t ov[kUnroll], nv[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            uint64_t d = sl.d_begin + (uint64_t)(r + u) * 64 + ln;
-            bool in = d < sl.d_end;
-            ov[u] = in ? po[d] : 0u;
-            nv[u] = in ? pn[d] : 0u;
+            const uint32_t d = (r0 + u) * 64 + ln;
+            ov[u] = d < sl.nwords ? po[d] : 0u;
+            nv[u] = d < sl.nwords ? pn[d] : 0u;
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            if (r + u >= sl.nrows) break;
-            const uint64_t d = sl.d_begin + (uint64_t)(r + u) * 64 + ln;
-            const int64_t i0 = (int64_t)(2 * d) - (int64_t)td.lead;
-            const bool v0 = i0 >= (int64_t)sl.lo && i0 < (int64_t)sl.hi;
-            const bool v1 = i0 + 1 >= (int64_t)sl.lo && i0 + 1 < (int64_t)sl.hi;
+            const uint32_t r = r0 + u;
+            if (r >= sl.nrows) break;
+            const uint32_t f = r * kRow + 2 * ln;
+            bool v0 = true, v1 = true;
+            if (!row_full(sl, r)) {
+                v0 = f >= sl.f_lo && f < sl.f_hi;
+                v1 = f + 1 >= sl.f_lo && f + 1 < sl.f_hi;
+            }
             const uint32_t o = ov[u], n = nv[u];
             const uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF;
             const uint32_t x = o ^ n;
-            const bool c0 = v0 && (x & 0xFFFF), c1 = v1 && (x >> 16);
+            const bool c0 = v0 && (x & 0xFFFF), c1 = v1 && x > 0xFFFF;
             const uint64_t C0 = ballot(c0), C1 = ballot(c1);
             if (C0 | C1) {
                 uint32_t rk0 = 0, rc0 = 0, rk1 = 0, rc1 = 0;
@@ -149,7 +176,8 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
                                           : rdlane(k1, (uint32_t)__builtin_ctzll(P1));
                     const bool m0 = v0 && k0 == k, m1 = v1 && k1 == k;
                     const uint64_t M0 = ballot(m0), M1 = ballot(m1);
-                    const uint32_t R = hall[4 * k] + hall[4 * k + 1] + hall[4 * k + 2] + hall[4 * k + 3];
+                    const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
+                    const uint32_t R = h.x + h.y + h.z + h.w;
                     const uint32_t Rc = hchg[k];
                     const uint32_t before = mbcnt(M0) + mbcnt(M1);
                     const uint32_t beforec = mbcnt(M0 & C0) + mbcnt(M1 & C1);
@@ -166,16 +194,15 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
                     P0 &= ~M0;
                     P1 &= ~M1;
                 }
-                const uint32_t cb = mbcnt(C0) + mbcnt(C1);  // changes in lower lanes of this row
+                const uint32_t cb = cnt + mbcnt(C0) + mbcnt(C1);  // buffer slot of this lane's first change
                 if (c0) {
-                    rbuf[cnt + cb] = (uint64_t)rk0 | ((uint64_t)rc0 << 17) | ((uint64_t)k0 << 34) |
-                                     ((uint64_t)zigzag(o & 0xFFFF, n & 0xFFFF) << 42);
-                    dacc += (uint64_t)((int64_t)(n & 0xFFFF) - (int64_t)(o & 0xFFFF)) * weight((uint64_t)i0);
+                    meta[cb] = (uint64_t)rk0 | ((uint64_t)rc0 << 17) | ((uint64_t)k0 << 34) | ((uint64_t)f << 42);
+                    vals[cb] = (o & 0xFFFF) | (n << 16);
                 }
                 if (c1) {
-                    rbuf[cnt + cb + (c0 ? 1u : 0u)] = (uint64_t)rk1 | ((uint64_t)rc1 << 17) | ((uint64_t)k1 << 34) |
-                                                      ((uint64_t)zigzag(o >> 16, n >> 16) << 42);
-                    dacc += (uint64_t)((int64_t)(n >> 16) - (int64_t)(o >> 16)) * weight((uint64_t)i0 + 1);
+                    const uint32_t s = cb + (c0 ? 1u : 0u);
+                    meta[s] = (uint64_t)rk1 | ((uint64_t)rc1 << 17) | ((uint64_t)k1 << 34) | ((uint64_t)(f + 1) << 42);
+                    vals[s] = (o >> 16) | (n & 0xFFFF0000u);
                 }
                 cnt += (uint32_t)(__popcll(C0) + __popcll(C1));
                 __syncthreads();
@@ -183,19 +210,20 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
             if (v0) atomicAdd(&hall[4 * k0 + rep], 1u);
             if (v1) atomicAdd(&hall[4 * k1 + rep], 1u);
             if (COLD) {
-                if (v0) facc += (uint64_t)(n & 0xFFFF) * weight((uint64_t)i0);
-                if (v1) facc += (uint64_t)(n >> 16) * weight((uint64_t)i0 + 1);
+                if (v0) facc += (uint64_t)(n & 0xFFFF) * weight(sl.base + f);
+                if (v1) facc += (uint64_t)(n >> 16) * weight(sl.base + f + 1);
             }
-            if (cnt > kRecCap - kRow) {
-                flush_records(a, tau, rbuf, cnt);
+            if (cnt > kChgCap - kRow) {
+                flush_changes(a, tau, sl, meta, vals, cnt, dacc);
                 cnt = 0;
             }
         }
     }
-    if (cnt) flush_records(a, tau, rbuf, cnt);
+    if (cnt) flush_changes(a, tau, sl, meta, vals, cnt, dacc);
     __syncthreads();
     for (uint32_t k = ln; k < 256; k += 64) {
-        a.hall[(uint64_t)tau * 256 + k] = hall[4 * k] + hall[4 * k + 1] + hall[4 * k + 2] + hall[4 * k + 3];
+        const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
+        a.hall[(uint64_t)tau * 256 + k] = h.x + h.y + h.z + h.w;
         a.hchg[(uint64_t)tau * 256 + k] = hchg[k];
     }
     dacc = wave_sum(dacc);
@@ -207,57 +235,67 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
 }
 
 __global__ __launch_bounds__(64) void k_enc_rank(EncRankArgs a) {
-    __shared__ uint32_t hall[256 * 4];  // 4 copies per exponent: fewer same-address LDS atomics
+    __shared__ __attribute__((aligned(16))) uint32_t hall[256 * 4];  // 4 copies per exponent
     __shared__ uint32_t hchg[256];
-    __shared__ uint64_t rbuf[kRecCap];
+    __shared__ uint64_t meta[kChgCap];
+    __shared__ uint32_t vals[kChgCap];
     const uint32_t tau = blockIdx.x;
     const TensorDesc td = a.descs[tensor_of_tile(a.descs, a.n_tensors, tau)];
     const Slab sl = slab_of(td, tau - td.tile_begin, a.slab);
     for (uint32_t i = lane(); i < 1024; i += 64) hall[i] = 0;
     for (uint32_t i = lane(); i < 256; i += 64) hchg[i] = 0;
     __syncthreads();
-    if (td.cold) enc_rank_slab<true>(a, td, tau, sl, hall, hchg, rbuf);
-    else enc_rank_slab<false>(a, td, tau, sl, hall, hchg, rbuf);
+    if (td.cold) enc_rank_slab<true>(a, td, tau, sl, hall, hchg, meta, vals);
+    else enc_rank_slab<false>(a, td, tau, sl, hall, hchg, meta, vals);
 }
 
 // ================================================================== apply: histogram pass
 template <bool COLD>
 __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau, const Slab &sl, uint32_t *hall) {
     const uint32_t ln = lane(), rep = ln & 3;
+    const uint32_t *po = td.frame + sl.first;
     uint64_t facc = 0;
-    const uint32_t *po = td.frame;
-    for (uint32_t r = 0; r < sl.nrows; r += kUnroll) {
+    for (uint32_t r0 = 0; r0 < sl.nrows; r0 += kUnroll) {
         uint32_t ov[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            uint64_t d = sl.d_begin + (uint64_t)(r + u) * 64 + ln;
-            ov[u] = d < sl.d_end ? po[d] : 0u;
+            const uint32_t d = (r0 + u) * 64 + ln;
+            ov[u] = d < sl.nwords ? po[d] : 0u;
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            if (r + u >= sl.nrows) break;
-            const uint64_t d = sl.d_begin + (uint64_t)(r + u) * 64 + ln;
-            const int64_t i0 = (int64_t)(2 * d) - (int64_t)td.lead;
-            const bool v0 = i0 >= (int64_t)sl.lo && i0 < (int64_t)sl.hi;
-            const bool v1 = i0 + 1 >= (int64_t)sl.lo && i0 + 1 < (int64_t)sl.hi;
-            const uint32_t o = ov[u];
-            if (v0) atomicAdd(&hall[4 * ((o >> 7) & 0xFF) + rep], 1u);
-            if (v1) atomicAdd(&hall[4 * ((o >> 23) & 0xFF) + rep], 1u);
-            if (COLD) {
-                if (v0) facc += (uint64_t)(o & 0xFFFF) * weight((uint64_t)i0);
-                if (v1) facc += (uint64_t)(o >> 16) * weight((uint64_t)i0 + 1);
+            const uint32_t r = r0 + u;
+            if (r >= sl.nrows) break;
+            const uint32_t o = ov[u], f = r * kRow + 2 * ln;
+            if (row_full(sl, r)) {
+                atomicAdd(&hall[4 * ((o >> 7) & 0xFF) + rep], 1u);
+                atomicAdd(&hall[4 * ((o >> 23) & 0xFF) + rep], 1u);
+                if (COLD) {
+                    facc += (uint64_t)(o & 0xFFFF) * weight(sl.base + f);
+                    facc += (uint64_t)(o >> 16) * weight(sl.base + f + 1);
+                }
+            } else {
+                const bool v0 = f >= sl.f_lo && f < sl.f_hi, v1 = f + 1 >= sl.f_lo && f + 1 < sl.f_hi;
+                if (v0) atomicAdd(&hall[4 * ((o >> 7) & 0xFF) + rep], 1u);
+                if (v1) atomicAdd(&hall[4 * ((o >> 23) & 0xFF) + rep], 1u);
+                if (COLD) {
+                    if (v0) facc += (uint64_t)(o & 0xFFFF) * weight(sl.base + f);
+                    if (v1) facc += (uint64_t)(o >> 16) * weight(sl.base + f + 1);
+                }
             }
         }
     }
     __syncthreads();
-    for (uint32_t k = ln; k < 256; k += 64)
-        a.hall[(uint64_t)tau * 256 + k] = hall[4 * k] + hall[4 * k + 1] + hall[4 * k + 2] + hall[4 * k + 3];
+    for (uint32_t k = ln; k < 256; k += 64) {
+        const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
+        a.hall[(uint64_t)tau * 256 + k] = h.x + h.y + h.z + h.w;
+    }
     facc = wave_sum(facc);
     if (ln == 0) a.full[tau] = facc;
 }
 
 __global__ __launch_bounds__(64) void k_hist(HistArgs a) {
-    __shared__ uint32_t hall[256 * 4];
+    __shared__ __attribute__((aligned(16))) uint32_t hall[256 * 4];
     const uint32_t tau = blockIdx.x;
     const TensorDesc td = a.descs[tensor_of_tile(a.descs, a.n_tensors, tau)];
     const Slab sl = slab_of(td, tau - td.tile_begin, a.slab);
@@ -805,97 +843,142 @@ __global__ __launch_bounds__(256) void k_locate(SelectArgs a) {
 }
 
 // ================================================================== apply: select pass
-// One wavefront per slab.  rem[e] = (slab rank of the next target of exponent e) - (elements of
-// exponent e seen so far).  Every element decrements its exponent's counter; the lane that takes it
-// from 0 shows that a target lies in this row, whose position then follows from the stable in-row
-// ranks (ballot + mbcnt).  The order in which same-address LDS atomics return does not matter: only
-// whether some lane saw 0 is used.
+// One wavefront per slab.  The slab's targets (group-local indices of its changes, minus the
+// exponent's count before the slab = ranks within the slab) are copied to LDS, per exponent in
+// order.  Streaming the slab, every element adds one to its exponent's count (4 copies by lane, few
+// same-address conflicts) and reads back the total: when the total passes the exponent's next target
+// rank, the target lies in this row and its lane follows from the stable in-row ranks.
+constexpr uint32_t kTgtCap = 2048;  // targets per slab held in LDS; more are read from HBM
+
 __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
-    __shared__ int32_t rem[256];
-    __shared__ uint32_t nxt[256], endj[256], tcur[256], pre[256];
+    __shared__ __attribute__((aligned(16))) uint32_t cnt[256 * 4];
+    __shared__ uint32_t tgt[256], tix[256], tend[256], jofs[256], toff[256], pre[256];
+    __shared__ uint32_t list[kTgtCap];
     if (*a.bad) return;
-    const uint32_t tau = blockIdx.x, ln = lane();
+    const uint32_t tau = blockIdx.x, ln = lane(), rep = ln & 3;
     const uint32_t t = tensor_of_tile(a.descs, a.n_tensors, tau);
     const TensorDesc td = a.descs[t];
     const uint32_t local_tile = tau - td.tile_begin;
     const Slab sl = slab_of(td, local_tile, a.slab);
-    for (uint32_t k = ln; k < 256; k += 64) {
+
+    // targets of this slab: group changes [lb(slab), lb(next slab)) of each exponent
+    uint32_t n4[4], j4[4], mine = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t k = 4 * ln + q;
         const int32_t g = a.group_of[(uint64_t)t * 256 + k];
-        int32_t r = kFar;
-        uint32_t p = a.pre[(uint64_t)tau * 256 + k];
+        n4[q] = 0;
+        j4[q] = 0;
         if (g >= 0) {
             const GroupDev gr = a.groups[g];
             const uint32_t j0 = a.lb[(uint64_t)tau * 256 + k];
             const uint32_t je = local_tile + 1 < td.n_tiles ? a.lb[(uint64_t)(tau + 1) * 256 + k] : gr.elem_base + gr.count;
             if (j0 < je) {
-                const uint32_t tc = a.local[j0] - p;
-                r = (int32_t)min<uint32_t>(tc, (uint32_t)kFar);
-                nxt[k] = j0;
-                endj[k] = je;
-                tcur[k] = tc;
+                n4[q] = je - j0;
+                j4[q] = j0;
             }
         }
-        rem[k] = r;
-        pre[k] = p;
+        mine += n4[q];
+    }
+    uint32_t incl = mine;  // inclusive scan of per-lane totals across the wave
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(incl, o, 64);
+        if (ln >= (uint32_t)o) incl += v;
+    }
+    const uint32_t total = __shfl(incl, 63, 64);
+    const bool in_lds = total <= kTgtCap;
+    uint32_t off = incl - mine;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t k = 4 * ln + q;
+        toff[k] = off;
+        tix[k] = off;
+        tend[k] = off + n4[q];
+        jofs[k] = j4[q] - off;
+        pre[k] = a.pre[(uint64_t)tau * 256 + k];
+        cnt[4 * k] = cnt[4 * k + 1] = cnt[4 * k + 2] = cnt[4 * k + 3] = 0;
+        off += n4[q];
     }
     __syncthreads();
-    const uint32_t *po = td.frame;
-    for (uint32_t r = 0; r < sl.nrows; r += kUnroll) {
+    if (in_lds) {
+        for (uint32_t x = ln; x < total; x += 64) {
+            uint32_t lo = 0, hi = 256;  // last exponent whose list starts at or before x
+            while (hi - lo > 1) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (toff[mid] <= x) lo = mid;
+                else hi = mid;
+            }
+            list[x] = a.local[jofs[lo] + x] - pre[lo];
+        }
+        __syncthreads();
+    }
+    for (uint32_t k = ln; k < 256; k += 64) {
+        const uint32_t i = tix[k];
+        tgt[k] = i < tend[k] ? (in_lds ? list[i] : a.local[jofs[k] + i] - pre[k]) : (uint32_t)kFar;
+    }
+    __syncthreads();
+
+    const uint32_t *po = td.frame + sl.first;
+    for (uint32_t r0 = 0; r0 < sl.nrows; r0 += kUnroll) {
         uint32_t ov[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            uint64_t d = sl.d_begin + (uint64_t)(r + u) * 64 + ln;
-            ov[u] = d < sl.d_end ? po[d] : 0u;
+            const uint32_t d = (r0 + u) * 64 + ln;
+            ov[u] = d < sl.nwords ? po[d] : 0u;
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            if (r + u >= sl.nrows) break;
-            const uint64_t d = sl.d_begin + (uint64_t)(r + u) * 64 + ln;
-            const int64_t i0 = (int64_t)(2 * d) - (int64_t)td.lead;
-            const bool v0 = i0 >= (int64_t)sl.lo && i0 < (int64_t)sl.hi;
-            const bool v1 = i0 + 1 >= (int64_t)sl.lo && i0 + 1 < (int64_t)sl.hi;
-            const uint32_t o = ov[u];
+            const uint32_t r = r0 + u;
+            if (r >= sl.nrows) break;
+            const uint32_t o = ov[u], f = r * kRow + 2 * ln;
+            bool v0 = true, v1 = true;
+            if (!row_full(sl, r)) {
+                v0 = f >= sl.f_lo && f < sl.f_hi;
+                v1 = f + 1 >= sl.f_lo && f + 1 < sl.f_hi;
+            }
             const uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF;
-            const int32_t r0 = v0 ? atomicSub(&rem[k0], 1) : -1;
-            const int32_t r1 = v1 ? atomicSub(&rem[k1], 1) : -1;
-            uint64_t H0 = ballot(r0 == 0), H1 = ballot(r1 == 0);
+            if (v0) atomicAdd(&cnt[4 * k0 + rep], 1u);
+            if (v1) atomicAdd(&cnt[4 * k1 + rep], 1u);
+            const uint4 a0 = *reinterpret_cast<const uint4 *>(&cnt[4 * k0]);
+            const uint4 a1 = *reinterpret_cast<const uint4 *>(&cnt[4 * k1]);
+            const bool h0 = v0 && a0.x + a0.y + a0.z + a0.w > tgt[k0];
+            const bool h1 = v1 && a1.x + a1.y + a1.z + a1.w > tgt[k1];
+            uint64_t H0 = ballot(h0), H1 = ballot(h1);
             if (H0 | H1) {
                 __syncthreads();
-                while (H0 | H1) {
+                while (H0 | H1) {  // once per exponent with a target in this row
                     const uint32_t k = H0 ? rdlane(k0, (uint32_t)__builtin_ctzll(H0))
                                           : rdlane(k1, (uint32_t)__builtin_ctzll(H1));
                     const bool m0 = v0 && k0 == k, m1 = v1 && k1 == k;
                     const uint64_t M0 = ballot(m0), M1 = ballot(m1);
-                    const int32_t ck = (int32_t)(__popcll(M0) + __popcll(M1));
-                    const int32_t rb = rem[k] + ck;                // remaining before this row, in [0, ck)
-                    const uint32_t seen = tcur[k] - (uint32_t)rb;  // exponent-k elements before this row
+                    const uint32_t ck = (uint32_t)(__popcll(M0) + __popcll(M1));
+                    const uint4 c = *reinterpret_cast<const uint4 *>(&cnt[4 * k]);
+                    const uint32_t after = c.x + c.y + c.z + c.w;  // exponent-k elements up to this row's end
+                    const uint32_t seen = after - ck;               // ... before this row
                     const uint32_t rr0 = mbcnt(M0) + mbcnt(M1), rr1 = rr0 + (m0 ? 1u : 0u);
-                    uint32_t j = nxt[k], je = endj[k], tc = tcur[k];
-                    int32_t cur = rb, nrem = kFar;
+                    uint32_t i = tix[k], tc = tgt[k];
+                    const uint32_t ie = tend[k], jo = jofs[k];
                     for (;;) {  // every target of exponent k inside this row, in order
-                        if (m0 && rr0 == (uint32_t)cur) {
-                            a.pos[j] = (uint32_t)i0;
-                            a.val[j] = (uint16_t)(o & 0xFFFF);
+                        const uint32_t q = tc - seen;
+                        if (m0 && rr0 == q) {
+                            a.pos[jo + i] = sl.base + f;
+                            a.val[jo + i] = (uint16_t)(o & 0xFFFF);
                         }
-                        if (m1 && rr1 == (uint32_t)cur) {
-                            a.pos[j] = (uint32_t)i0 + 1;
-                            a.val[j] = (uint16_t)(o >> 16);
+                        if (m1 && rr1 == q) {
+                            a.pos[jo + i] = sl.base + f + 1;
+                            a.val[jo + i] = (uint16_t)(o >> 16);
                         }
-                        if (++j >= je) break;
-                        tc = a.local[j] - pre[k];
-                        // targets are < 2^17 apart inside a slab: the signed difference is exact
-                        const int32_t after_row = (int32_t)(tc - seen) - ck;
-                        if (after_row >= 0) {
-                            nrem = min(after_row, kFar);
+                        if (++i >= ie) {
+                            tc = (uint32_t)kFar;
                             break;
                         }
-                        cur = after_row + ck;
+                        tc = in_lds ? list[i] : a.local[jo + i] - pre[k];
+                        if (tc >= after) break;
                     }
                     __syncthreads();
                     if (ln == 0) {
-                        rem[k] = nrem;
-                        nxt[k] = j;
-                        tcur[k] = tc;
+                        tix[k] = i;
+                        tgt[k] = tc;
                     }
                     __syncthreads();
                     H0 &= ~M0;

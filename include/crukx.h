@@ -69,6 +69,11 @@ int32_t crx_update_tensor(const crx_update *u, int64_t i, const uint8_t **name, 
                           uint64_t *numel, uint64_t *checksum, int32_t *n_groups);
 int32_t crx_update_group(const crx_update *u, int64_t i, int32_t g, int32_t *exponent, uint64_t *count,
                          int32_t *rice);
+/* All tensor headers at once: names concatenated into `names` (capacity `names_cap`; the total
+ * length is returned in *names_len), name_ends[i] = end offset of name i, plus numels and checksums
+ * (n_tensors entries each).  Returns CRX_INVALID with *names_len set if `names_cap` is too small. */
+int32_t crx_update_headers(const crx_update *u, char *names, uint64_t names_cap, uint64_t *names_len,
+                           uint64_t *name_ends, uint64_t *numels, uint64_t *checksums);
 uint64_t crx_update_n_blocks(const crx_update *u);
 /* Copies the block table (n_blocks u32) into `out`. */
 int32_t crx_update_block_bits(const crx_update *u, uint32_t *out);
