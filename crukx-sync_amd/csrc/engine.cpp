@@ -266,7 +266,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     Chunk *chunks = nullptr;
     unsigned long long h[8];
     for (int attempt = 0;; ++attempt) {
-        const uint64_t chunk_cap = tiles + rec_cap / (kRecCap - kRow) + 16;
+        const uint64_t chunk_cap = tiles + rec_cap / (kChgCap - kRow) + 16;  // one flush per slab + full ones
         rec = ar.get<uint64_t>(rec_cap);
         chunks = ar.get<Chunk>(chunk_cap);
         zero(cnt, 8, s);

@@ -14,7 +14,8 @@ namespace {
 constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ULL;
 constexpr uint64_t kMix1 = 0xBF58476D1CE4E5B9ULL;
 constexpr uint64_t kMix2 = 0x94D049BB133111EBULL;
-constexpr int kUnroll = 8;            // rows loaded ahead per wavefront
+constexpr int kRankRows = 8;    // rows per batch of the encode rank pass (two streams)
+constexpr int kScanRows = 16;   // rows per batch of the apply histogram and select passes
 
 // splitmix64(i) | 1: the per-position checksum weight (docs/FORMAT.md:61-64).
 __device__ __forceinline__ uint64_t weight(uint64_t i) {
@@ -25,6 +26,10 @@ __device__ __forceinline__ uint64_t weight(uint64_t i) {
 }
 
 __device__ __forceinline__ uint32_t lane() { return __lane_id(); }
+// Orders this wavefront's LDS accesses in the compiler's view without waiting on outstanding memory
+// operations (LDS instructions of one wavefront execute in order).  The streaming kernels run one
+// wavefront per workgroup, so a workgroup barrier would only drain the rows loaded ahead.
+__device__ __forceinline__ void wave_fence() { asm volatile("" ::: "memory"); }
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 // number of set bits of m below this lane
 __device__ __forceinline__ uint32_t mbcnt(uint64_t m) {
@@ -103,17 +108,53 @@ __device__ __forceinline__ bool row_full(const Slab &s, uint32_t r) {
     return r * kRow >= s.f_lo && r * kRow + kRow <= s.f_hi;
 }
 
+// Raw buffer resource over the slab's words [p, p + nwords): the hardware range check returns 0 for
+// any load at or past the end, so rows fetched ahead of the slab's end need neither masks nor
+// addresses inside the allocation.  Dword 3 is the gfx9-family default format.
+using Rsrc = __amdgpu_buffer_rsrc_t;
+__device__ __forceinline__ Rsrc slab_rsrc(const uint32_t *frame, const Slab &s) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(frame + s.first), (short)0,
+                                             (int)(s.nwords * 4u), 0x00020000);
+}
+
+// Streams the slab's rows through `body(row, word of stream 0, word of stream S-1)`, U rows per batch
+// with the next batch already in flight (double buffering keeps U..2U rows of loads outstanding
+// per wavefront while a batch is processed).
+template <int U, int S, typename Body>
+__device__ __forceinline__ void stream_rows(const Slab &sl, const Rsrc (&src)[S], Body &&body) {
+    const uint32_t lb = lane() * 4u;
+    uint32_t cur[S][U], nxt[S][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int q = 0; q < S; ++q) cur[q][u] = __builtin_amdgcn_raw_buffer_load_b32(src[q], lb + u * 256u, 0, 0);
+    for (uint32_t r0 = 0; r0 < sl.nrows; r0 += U) {
+        const uint32_t nb = (r0 + U) * 256u + lb;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int q = 0; q < S; ++q) nxt[q][u] = __builtin_amdgcn_raw_buffer_load_b32(src[q], nb + u * 256u, 0, 0);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (r0 + u >= sl.nrows) break;
+            body(r0 + u, cur[0][u], cur[S - 1][u]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int q = 0; q < S; ++q) cur[q][u] = nxt[q][u];
+    }
+}
+
 // ================================================================== encode: rank pass
 // One wavefront per slab; reads old and new once.  For every changed element it needs its rank among
 // the slab's elements with the same old exponent (`rank`) and among the slab's changes with that
 // exponent (`rc`): the running per-exponent counts in LDS give the part before the row, ballots and
 // mbcnt the stable part inside the row.  Changed elements are buffered in LDS as (rank, rc, exponent,
 // offset, old, new) and finished in dense batches: zigzag residual, checksum delta, 64-bit record.
-constexpr int kChgCap = 384;  // buffered changes; a flush leaves room for one full row
-
 __device__ void flush_changes(const EncRankArgs &a, uint32_t tau, const Slab &sl, const uint64_t *meta,
                               const uint32_t *vals, uint32_t cnt, uint64_t &dacc) {
-    __syncthreads();
+    wave_fence();
     unsigned long long base = 0;
     if (lane() == 0) base = atomicAdd(&a.counters[0], (unsigned long long)cnt);
     base = __shfl(base, 0, 64);
@@ -135,92 +176,79 @@ __device__ void flush_changes(const EncRankArgs &a, uint32_t tau, const Slab &sl
             atomicOr(&a.counters[2], 1ULL);
         }
     }
-    __syncthreads();
+    wave_fence();
 }
 
 template <bool COLD>
 __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32_t tau, const Slab &sl,
                               uint32_t *hall, uint32_t *hchg, uint64_t *meta, uint32_t *vals) {
     const uint32_t ln = lane(), rep = ln & 3;
-    const uint32_t *po = td.frame + sl.first, *pn = td.frame_new + sl.first;
+    const Rsrc src[2] = {slab_rsrc(td.frame, sl), slab_rsrc(td.frame_new, sl)};
     uint32_t cnt = 0;
     uint64_t dacc = 0, facc = 0;
-    for (uint32_t r0 = 0; r0 < sl.nrows; r0 += kUnroll) {
-        uint32_t ov[kUnroll], nv[kUnroll];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t d = (r0 + u) * 64 + ln;
-            ov[u] = d < sl.nwords ? po[d] : 0u;
-            nv[u] = d < sl.nwords ? pn[d] : 0u;
+    stream_rows<kRankRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t n) {
+        const uint32_t f = r * kRow + 2 * ln;
+        bool v0 = true, v1 = true;
+        if (!row_full(sl, r)) {
+            v0 = f >= sl.f_lo && f < sl.f_hi;
+            v1 = f + 1 >= sl.f_lo && f + 1 < sl.f_hi;
         }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t r = r0 + u;
-            if (r >= sl.nrows) break;
-            const uint32_t f = r * kRow + 2 * ln;
-            bool v0 = true, v1 = true;
-            if (!row_full(sl, r)) {
-                v0 = f >= sl.f_lo && f < sl.f_hi;
-                v1 = f + 1 >= sl.f_lo && f + 1 < sl.f_hi;
-            }
-            const uint32_t o = ov[u], n = nv[u];
-            const uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF;
-            const uint32_t x = o ^ n;
-            const bool c0 = v0 && (x & 0xFFFF), c1 = v1 && x > 0xFFFF;
-            const uint64_t C0 = ballot(c0), C1 = ballot(c1);
-            if (C0 | C1) {
-                uint32_t rk0 = 0, rc0 = 0, rk1 = 0, rc1 = 0;
-                uint64_t P0 = C0, P1 = C1;
-                while (P0 | P1) {  // once per distinct exponent among this row's changes
-                    const uint32_t k = P0 ? rdlane(k0, (uint32_t)__builtin_ctzll(P0))
-                                          : rdlane(k1, (uint32_t)__builtin_ctzll(P1));
-                    const bool m0 = v0 && k0 == k, m1 = v1 && k1 == k;
-                    const uint64_t M0 = ballot(m0), M1 = ballot(m1);
-                    const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
-                    const uint32_t R = h.x + h.y + h.z + h.w;
-                    const uint32_t Rc = hchg[k];
-                    const uint32_t before = mbcnt(M0) + mbcnt(M1);
-                    const uint32_t beforec = mbcnt(M0 & C0) + mbcnt(M1 & C1);
-                    if (c0 && m0) {
-                        rk0 = R + before;
-                        rc0 = Rc + beforec;
-                    }
-                    if (c1 && m1) {
-                        rk1 = R + before + (m0 ? 1u : 0u);
-                        rc1 = Rc + beforec + ((c0 && m0) ? 1u : 0u);
-                    }
-                    __syncthreads();
-                    if (ln == 0) hchg[k] = Rc + (uint32_t)__popcll(M0 & C0) + (uint32_t)__popcll(M1 & C1);
-                    P0 &= ~M0;
-                    P1 &= ~M1;
+        const uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF;
+        const uint32_t x = o ^ n;
+        const bool c0 = v0 && (x & 0xFFFF), c1 = v1 && x > 0xFFFF;
+        const uint64_t C0 = ballot(c0), C1 = ballot(c1);
+        if (C0 | C1) {
+            uint32_t rk0 = 0, rc0 = 0, rk1 = 0, rc1 = 0;
+            uint64_t P0 = C0, P1 = C1;
+            while (P0 | P1) {  // once per distinct exponent among this row's changes
+                const uint32_t k = P0 ? rdlane(k0, (uint32_t)__builtin_ctzll(P0))
+                                      : rdlane(k1, (uint32_t)__builtin_ctzll(P1));
+                const bool m0 = v0 && k0 == k, m1 = v1 && k1 == k;
+                const uint64_t M0 = ballot(m0), M1 = ballot(m1);
+                const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
+                const uint32_t R = h.x + h.y + h.z + h.w;
+                const uint32_t Rc = hchg[k];
+                const uint32_t before = mbcnt(M0) + mbcnt(M1);
+                const uint32_t beforec = mbcnt(M0 & C0) + mbcnt(M1 & C1);
+                if (c0 && m0) {
+                    rk0 = R + before;
+                    rc0 = Rc + beforec;
                 }
-                const uint32_t cb = cnt + mbcnt(C0) + mbcnt(C1);  // buffer slot of this lane's first change
-                if (c0) {
-                    meta[cb] = (uint64_t)rk0 | ((uint64_t)rc0 << 17) | ((uint64_t)k0 << 34) | ((uint64_t)f << 42);
-                    vals[cb] = (o & 0xFFFF) | (n << 16);
+                if (c1 && m1) {
+                    rk1 = R + before + (m0 ? 1u : 0u);
+                    rc1 = Rc + beforec + ((c0 && m0) ? 1u : 0u);
                 }
-                if (c1) {
-                    const uint32_t s = cb + (c0 ? 1u : 0u);
-                    meta[s] = (uint64_t)rk1 | ((uint64_t)rc1 << 17) | ((uint64_t)k1 << 34) | ((uint64_t)(f + 1) << 42);
-                    vals[s] = (o >> 16) | (n & 0xFFFF0000u);
-                }
-                cnt += (uint32_t)(__popcll(C0) + __popcll(C1));
-                __syncthreads();
+                wave_fence();
+                if (ln == 0) hchg[k] = Rc + (uint32_t)__popcll(M0 & C0) + (uint32_t)__popcll(M1 & C1);
+                P0 &= ~M0;
+                P1 &= ~M1;
             }
-            if (v0) atomicAdd(&hall[4 * k0 + rep], 1u);
-            if (v1) atomicAdd(&hall[4 * k1 + rep], 1u);
-            if (COLD) {
-                if (v0) facc += (uint64_t)(n & 0xFFFF) * weight(sl.base + f);
-                if (v1) facc += (uint64_t)(n >> 16) * weight(sl.base + f + 1);
+            const uint32_t cb = cnt + mbcnt(C0) + mbcnt(C1);  // buffer slot of this lane's first change
+            if (c0) {
+                meta[cb] = (uint64_t)rk0 | ((uint64_t)rc0 << 17) | ((uint64_t)k0 << 34) | ((uint64_t)f << 42);
+                vals[cb] = (o & 0xFFFF) | (n << 16);
             }
-            if (cnt > kChgCap - kRow) {
-                flush_changes(a, tau, sl, meta, vals, cnt, dacc);
-                cnt = 0;
+            if (c1) {
+                const uint32_t s = cb + (c0 ? 1u : 0u);
+                meta[s] = (uint64_t)rk1 | ((uint64_t)rc1 << 17) | ((uint64_t)k1 << 34) | ((uint64_t)(f + 1) << 42);
+                vals[s] = (o >> 16) | (n & 0xFFFF0000u);
             }
+            cnt += (uint32_t)(__popcll(C0) + __popcll(C1));
+            wave_fence();
         }
-    }
+        if (v0) atomicAdd(&hall[4 * k0 + rep], 1u);
+        if (v1) atomicAdd(&hall[4 * k1 + rep], 1u);
+        if (COLD) {
+            if (v0) facc += (uint64_t)(n & 0xFFFF) * weight(sl.base + f);
+            if (v1) facc += (uint64_t)(n >> 16) * weight(sl.base + f + 1);
+        }
+        if (cnt > kChgCap - kRow) {
+            flush_changes(a, tau, sl, meta, vals, cnt, dacc);
+            cnt = 0;
+        }
+    });
     if (cnt) flush_changes(a, tau, sl, meta, vals, cnt, dacc);
-    __syncthreads();
+    wave_fence();
     for (uint32_t k = ln; k < 256; k += 64) {
         const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
         a.hall[(uint64_t)tau * 256 + k] = h.x + h.y + h.z + h.w;
@@ -244,7 +272,7 @@ __global__ __launch_bounds__(64) void k_enc_rank(EncRankArgs a) {
     const Slab sl = slab_of(td, tau - td.tile_begin, a.slab);
     for (uint32_t i = lane(); i < 1024; i += 64) hall[i] = 0;
     for (uint32_t i = lane(); i < 256; i += 64) hchg[i] = 0;
-    __syncthreads();
+    wave_fence();
     if (td.cold) enc_rank_slab<true>(a, td, tau, sl, hall, hchg, meta, vals);
     else enc_rank_slab<false>(a, td, tau, sl, hall, hchg, meta, vals);
 }
@@ -253,39 +281,28 @@ __global__ __launch_bounds__(64) void k_enc_rank(EncRankArgs a) {
 template <bool COLD>
 __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau, const Slab &sl, uint32_t *hall) {
     const uint32_t ln = lane(), rep = ln & 3;
-    const uint32_t *po = td.frame + sl.first;
+    const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
     uint64_t facc = 0;
-    for (uint32_t r0 = 0; r0 < sl.nrows; r0 += kUnroll) {
-        uint32_t ov[kUnroll];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t d = (r0 + u) * 64 + ln;
-            ov[u] = d < sl.nwords ? po[d] : 0u;
-        }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t r = r0 + u;
-            if (r >= sl.nrows) break;
-            const uint32_t o = ov[u], f = r * kRow + 2 * ln;
-            if (row_full(sl, r)) {
-                atomicAdd(&hall[4 * ((o >> 7) & 0xFF) + rep], 1u);
-                atomicAdd(&hall[4 * ((o >> 23) & 0xFF) + rep], 1u);
-                if (COLD) {
-                    facc += (uint64_t)(o & 0xFFFF) * weight(sl.base + f);
-                    facc += (uint64_t)(o >> 16) * weight(sl.base + f + 1);
-                }
-            } else {
-                const bool v0 = f >= sl.f_lo && f < sl.f_hi, v1 = f + 1 >= sl.f_lo && f + 1 < sl.f_hi;
-                if (v0) atomicAdd(&hall[4 * ((o >> 7) & 0xFF) + rep], 1u);
-                if (v1) atomicAdd(&hall[4 * ((o >> 23) & 0xFF) + rep], 1u);
-                if (COLD) {
-                    if (v0) facc += (uint64_t)(o & 0xFFFF) * weight(sl.base + f);
-                    if (v1) facc += (uint64_t)(o >> 16) * weight(sl.base + f + 1);
-                }
+    stream_rows<kScanRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
+        const uint32_t f = r * kRow + 2 * ln;
+        if (row_full(sl, r)) {
+            atomicAdd(&hall[4 * ((o >> 7) & 0xFF) + rep], 1u);
+            atomicAdd(&hall[4 * ((o >> 23) & 0xFF) + rep], 1u);
+            if (COLD) {
+                facc += (uint64_t)(o & 0xFFFF) * weight(sl.base + f);
+                facc += (uint64_t)(o >> 16) * weight(sl.base + f + 1);
+            }
+        } else {
+            const bool v0 = f >= sl.f_lo && f < sl.f_hi, v1 = f + 1 >= sl.f_lo && f + 1 < sl.f_hi;
+            if (v0) atomicAdd(&hall[4 * ((o >> 7) & 0xFF) + rep], 1u);
+            if (v1) atomicAdd(&hall[4 * ((o >> 23) & 0xFF) + rep], 1u);
+            if (COLD) {
+                if (v0) facc += (uint64_t)(o & 0xFFFF) * weight(sl.base + f);
+                if (v1) facc += (uint64_t)(o >> 16) * weight(sl.base + f + 1);
             }
         }
-    }
-    __syncthreads();
+    });
+    wave_fence();
     for (uint32_t k = ln; k < 256; k += 64) {
         const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
         a.hall[(uint64_t)tau * 256 + k] = h.x + h.y + h.z + h.w;
@@ -847,13 +864,17 @@ __global__ __launch_bounds__(256) void k_locate(SelectArgs a) {
 // exponent's count before the slab = ranks within the slab) are copied to LDS, per exponent in
 // order.  Streaming the slab, every element adds one to its exponent's count (4 copies by lane, few
 // same-address conflicts) and reads back the total: when the total passes the exponent's next target
-// rank, the target lies in this row and its lane follows from the stable in-row ranks.
-constexpr uint32_t kTgtCap = 2048;  // targets per slab held in LDS; more are read from HBM
+// rank, targets lie in this row.  The row's elements of that exponent are then published in LDS by
+// in-row rank (stable: ballots and mbcnt), and the targets, one per lane, read their element there.
+constexpr uint32_t kTgtCap = 1024;  // targets per slab held in LDS; more are read from HBM
+constexpr uint32_t kNoKey = 256;    // exponent slot of lanes outside the slab (partial rows only)
 
 __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
-    __shared__ __attribute__((aligned(16))) uint32_t cnt[256 * 4];
-    __shared__ uint32_t tgt[256], tix[256], tend[256], jofs[256], toff[256], pre[256];
+    __shared__ __attribute__((aligned(16))) uint32_t cnt[(kNoKey + 1) * 4];
+    __shared__ uint32_t tgt[kNoKey + 1], tix[256], tend[256], jofs[256], pre[256];
     __shared__ uint32_t list[kTgtCap];
+    __shared__ uint32_t slot[kRow];
+    uint32_t *toff = cnt;  // list offsets per exponent, needed only while the list is copied
     if (*a.bad) return;
     const uint32_t tau = blockIdx.x, ln = lane(), rep = ln & 3;
     const uint32_t t = tensor_of_tile(a.descs, a.n_tensors, tau);
@@ -896,10 +917,9 @@ __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
         tend[k] = off + n4[q];
         jofs[k] = j4[q] - off;
         pre[k] = a.pre[(uint64_t)tau * 256 + k];
-        cnt[4 * k] = cnt[4 * k + 1] = cnt[4 * k + 2] = cnt[4 * k + 3] = 0;
         off += n4[q];
     }
-    __syncthreads();
+    wave_fence();
     if (in_lds) {
         for (uint32_t x = ln; x < total; x += 64) {
             uint32_t lo = 0, hi = 256;  // last exponent whose list starts at or before x
@@ -910,83 +930,73 @@ __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
             }
             list[x] = a.local[jofs[lo] + x] - pre[lo];
         }
-        __syncthreads();
     }
+    wave_fence();
     for (uint32_t k = ln; k < 256; k += 64) {
         const uint32_t i = tix[k];
         tgt[k] = i < tend[k] ? (in_lds ? list[i] : a.local[jofs[k] + i] - pre[k]) : (uint32_t)kFar;
     }
-    __syncthreads();
+    if (ln == 0) tgt[kNoKey] = (uint32_t)kFar;
+    wave_fence();
+    for (uint32_t i = ln; i < (kNoKey + 1) * 4; i += 64) cnt[i] = 0;
+    wave_fence();
 
-    const uint32_t *po = td.frame + sl.first;
-    for (uint32_t r0 = 0; r0 < sl.nrows; r0 += kUnroll) {
-        uint32_t ov[kUnroll];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t d = (r0 + u) * 64 + ln;
-            ov[u] = d < sl.nwords ? po[d] : 0u;
+    const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
+    stream_rows<kScanRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
+        uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF;
+        if (!row_full(sl, r)) {
+            const uint32_t f = r * kRow + 2 * ln;
+            if (f < sl.f_lo || f >= sl.f_hi) k0 = kNoKey;
+            if (f + 1 < sl.f_lo || f + 1 >= sl.f_hi) k1 = kNoKey;
         }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t r = r0 + u;
-            if (r >= sl.nrows) break;
-            const uint32_t o = ov[u], f = r * kRow + 2 * ln;
-            bool v0 = true, v1 = true;
-            if (!row_full(sl, r)) {
-                v0 = f >= sl.f_lo && f < sl.f_hi;
-                v1 = f + 1 >= sl.f_lo && f + 1 < sl.f_hi;
-            }
-            const uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF;
-            if (v0) atomicAdd(&cnt[4 * k0 + rep], 1u);
-            if (v1) atomicAdd(&cnt[4 * k1 + rep], 1u);
-            const uint4 a0 = *reinterpret_cast<const uint4 *>(&cnt[4 * k0]);
-            const uint4 a1 = *reinterpret_cast<const uint4 *>(&cnt[4 * k1]);
-            const bool h0 = v0 && a0.x + a0.y + a0.z + a0.w > tgt[k0];
-            const bool h1 = v1 && a1.x + a1.y + a1.z + a1.w > tgt[k1];
-            uint64_t H0 = ballot(h0), H1 = ballot(h1);
-            if (H0 | H1) {
-                __syncthreads();
-                while (H0 | H1) {  // once per exponent with a target in this row
-                    const uint32_t k = H0 ? rdlane(k0, (uint32_t)__builtin_ctzll(H0))
-                                          : rdlane(k1, (uint32_t)__builtin_ctzll(H1));
-                    const bool m0 = v0 && k0 == k, m1 = v1 && k1 == k;
-                    const uint64_t M0 = ballot(m0), M1 = ballot(m1);
-                    const uint32_t ck = (uint32_t)(__popcll(M0) + __popcll(M1));
-                    const uint4 c = *reinterpret_cast<const uint4 *>(&cnt[4 * k]);
-                    const uint32_t after = c.x + c.y + c.z + c.w;  // exponent-k elements up to this row's end
-                    const uint32_t seen = after - ck;               // ... before this row
-                    const uint32_t rr0 = mbcnt(M0) + mbcnt(M1), rr1 = rr0 + (m0 ? 1u : 0u);
-                    uint32_t i = tix[k], tc = tgt[k];
-                    const uint32_t ie = tend[k], jo = jofs[k];
-                    for (;;) {  // every target of exponent k inside this row, in order
-                        const uint32_t q = tc - seen;
-                        if (m0 && rr0 == q) {
-                            a.pos[jo + i] = sl.base + f;
-                            a.val[jo + i] = (uint16_t)(o & 0xFFFF);
-                        }
-                        if (m1 && rr1 == q) {
-                            a.pos[jo + i] = sl.base + f + 1;
-                            a.val[jo + i] = (uint16_t)(o >> 16);
-                        }
-                        if (++i >= ie) {
-                            tc = (uint32_t)kFar;
-                            break;
-                        }
-                        tc = in_lds ? list[i] : a.local[jo + i] - pre[k];
-                        if (tc >= after) break;
-                    }
-                    __syncthreads();
-                    if (ln == 0) {
-                        tix[k] = i;
-                        tgt[k] = tc;
-                    }
-                    __syncthreads();
-                    H0 &= ~M0;
-                    H1 &= ~M1;
+        atomicAdd(&cnt[4 * k0 + rep], 1u);
+        atomicAdd(&cnt[4 * k1 + rep], 1u);
+        const uint4 a0 = *reinterpret_cast<const uint4 *>(&cnt[4 * k0]);
+        const uint4 a1 = *reinterpret_cast<const uint4 *>(&cnt[4 * k1]);
+        const uint32_t s0 = a0.x + a0.y + a0.z + a0.w, s1 = a1.x + a1.y + a1.z + a1.w;
+        uint64_t H0 = ballot(s0 > tgt[k0]), H1 = ballot(s1 > tgt[k1]);
+        if (!(H0 | H1)) return;
+        wave_fence();
+        do {  // once per exponent with targets in this row
+            const bool from0 = H0 != 0;
+            const uint32_t l = (uint32_t)__builtin_ctzll(from0 ? H0 : H1);
+            const uint32_t k = from0 ? rdlane(k0, l) : rdlane(k1, l);
+            const uint32_t after = from0 ? rdlane(s0, l) : rdlane(s1, l);  // exponent-k count up to row end
+            const bool m0 = k0 == k, m1 = k1 == k;
+            const uint64_t M0 = ballot(m0), M1 = ballot(m1);
+            const uint32_t seen = after - (uint32_t)(__popcll(M0) + __popcll(M1));  // ... before this row
+            const uint32_t rr0 = mbcnt(M0) + mbcnt(M1);
+            if (m0) slot[rr0] = ((2 * ln) << 16) | (o & 0xFFFF);
+            if (m1) slot[rr0 + (m0 ? 1u : 0u)] = ((2 * ln + 1) << 16) | (o >> 16);
+            wave_fence();
+            uint32_t i = tix[k], next;
+            const uint32_t ie = tend[k], jo = jofs[k], pk = pre[k];
+            for (;;) {  // this row's targets of exponent k, one per lane
+                const uint32_t j = i + ln;
+                const uint32_t tc = j < ie ? (in_lds ? list[j] : a.local[jo + j] - pk) : (uint32_t)kFar;
+                const bool take = tc < after;
+                const uint32_t n = (uint32_t)__popcll(ballot(take));
+                if (take) {
+                    const uint32_t w = slot[tc - seen];
+                    a.pos[jo + j] = sl.base + r * kRow + (w >> 16);
+                    a.val[jo + j] = (uint16_t)w;
+                }
+                i += n;
+                if (n < 64) {
+                    next = rdlane(tc, n);  // the first target not taken, or kFar
+                    break;
                 }
             }
-        }
-    }
+            wave_fence();
+            if (ln == 0) {
+                tix[k] = i;
+                tgt[k] = next;
+            }
+            wave_fence();
+            H0 &= ~M0;
+            H1 &= ~M1;
+        } while (H0 | H1);
+    });
 }
 
 // new = (old + unzigzag(zz)) mod 2^16; checksum delta per tensor (codec.py:698-700).
