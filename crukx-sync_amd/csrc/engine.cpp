@@ -152,10 +152,13 @@ struct ScanDev {
     ScanChunk *chunks;
     uint32_t *tcb, *csum;
     uint32_t n_chunks;
+    uint32_t *tile_tensor;  // [tiles]
 };
 
-ScanDev upload_scan(Arena &ar, const Layout &L, hipStream_t s) {
+ScanDev upload_scan(Arena &ar, const Layout &L, const TensorDesc *d_descs, hipStream_t s) {
     ScanDev sd;
+    sd.tile_tensor = ar.get<uint32_t>(L.tiles);
+    launch_tile_map(d_descs, (uint32_t)L.descs.size(), sd.tile_tensor, s);
     sd.n_chunks = (uint32_t)L.chunks.size();
     sd.chunks = ar.get<ScanChunk>(sd.n_chunks);
     sd.tcb = ar.get<uint32_t>(L.tensor_chunk_begin.size());
@@ -255,7 +258,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     uint32_t *hall = ar.get<uint32_t>((uint64_t)tiles * 256), *hchg = ar.get<uint32_t>((uint64_t)tiles * 256);
     uint64_t *delta = ar.get<uint64_t>(tiles), *full = ar.get<uint64_t>(tiles);
     unsigned long long *cnt = ar.get<unsigned long long>(8);
-    ScanDev sd = upload_scan(ar, L, s);
+    ScanDev sd = upload_scan(ar, L, d_descs, s);
     uint32_t *tot_all = ar.get<uint32_t>((uint64_t)T * 256), *tot_chg = ar.get<uint32_t>((uint64_t)T * 256);
     GroupDev *d_groups = ar.get<GroupDev>((uint64_t)T * 256);
     uint32_t *gbase = ar.get<uint32_t>((uint64_t)T * 256);
@@ -270,7 +273,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
         rec = ar.get<uint64_t>(rec_cap);
         chunks = ar.get<Chunk>(chunk_cap);
         zero(cnt, 8, s);
-        EncRankArgs a{d_descs, T, slab, hall, hchg, rec, rec_cap, chunks, chunk_cap, cnt, delta, full};
+        EncRankArgs a{d_descs, sd.tile_tensor, T, slab, hall, hchg, rec, rec_cap, chunks, chunk_cap, cnt, delta, full};
         launch_enc_rank(a, tiles, s);
         d2h(h, cnt, 3, s);
         sync(s);
@@ -290,7 +293,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     if (C >= (1ULL << 32)) throw Invalid("2^32 or more changes in one update are not supported");
 
     uint64_t *sorted = ar.get<uint64_t>(C);
-    launch_place(chunks, (uint32_t)h[1], rec, d_descs, T, hall, hchg, gbase, sorted, C, s);
+    launch_place(chunks, (uint32_t)h[1], rec, sd.tile_tensor, hall, hchg, gbase, sorted, C, s);
     launch_r0(d_groups, (uint32_t)G, sorted, s);
     uint32_t *dense = ar.get<uint32_t>(256 * kDense);
     uint32_t *rare = ar.get<uint32_t>(C);
@@ -487,7 +490,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     h2d(d_descs, L.descs.data(), T, s);
     uint32_t *hall = ar.get<uint32_t>((uint64_t)tiles * 256);
     uint64_t *full = ar.get<uint64_t>(tiles), *t_full = ar.get<uint64_t>(T);
-    ScanDev sd = upload_scan(ar, L, s);
+    ScanDev sd = upload_scan(ar, L, d_descs, s);
     uint32_t *sizes = ar.get<uint32_t>((uint64_t)T * 256);
     GroupDev *d_groups = ar.get<GroupDev>(G);
     int32_t *d_gof = ar.get<int32_t>((uint64_t)T * 256);
@@ -510,27 +513,27 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     }
 
     // pass A: receiver exponent histograms (+ full old checksums on a cache miss)
-    HistArgs ha{d_descs, T, slab, hall, full};
+    HistArgs ha{d_descs, sd.tile_tensor, T, slab, hall, full};
     launch_hist(ha, tiles, s);
     launch_scan_tables(hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, sizes, s);
     launch_tensor_sums(d_descs, T, full, t_full, s);
     launch_scan_u32(d_bb, B, boff, s);
 
-    uint32_t *zz = ar.get<uint32_t>(C), *local = ar.get<uint32_t>(C), *pos = ar.get<uint32_t>(C);
-    uint16_t *val = ar.get<uint16_t>(C);
+    uint32_t *zz = ar.get<uint32_t>(C), *local = ar.get<uint32_t>(C);
+    unsigned long long *pv = ar.get<unsigned long long>(C);
     unsigned long long *blk_sum = ar.get<unsigned long long>(B), *blk_prefix = ar.get<unsigned long long>(B + 1);
     unsigned long long *tdelta = ar.get<unsigned long long>(T);
     unsigned int *bad = ar.get<unsigned int>(1);
-    uint32_t *lb = ar.get<uint32_t>((uint64_t)tiles * 256);
+    uint32_t *lb = ar.get<uint32_t>((uint64_t)(tiles + 1) * 256);  // row tiles: read, never used
     zero(bad, 1, s);
     zero(tdelta, T, s);
     DecodeArgs da{pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, sizes, d_tab, d_syms, (uint32_t)syms.size(),
                   zz, local, blk_sum, bad};
     launch_decode(da, s);
     launch_scan_u64(blk_sum, B, blk_prefix, s);
-    BlockArgs ba{d_groups, (uint32_t)G, d_descs, sizes, blk_prefix, local, zz, pos, val, tdelta, bad};
+    BlockArgs ba{d_groups, (uint32_t)G, d_descs, sizes, blk_prefix, local, zz, pv, tdelta, bad};
     launch_local_fix(ba, B, s);
-    SelectArgs sa{d_descs, T, slab, hall, lb, d_gof, d_groups, local, pos, val, bad};
+    SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, pv, bad};
     launch_locate(sa, tiles, s);
     launch_select(sa, tiles, s);
     launch_verify(ba, B, s);

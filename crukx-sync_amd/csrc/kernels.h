@@ -56,6 +56,7 @@ struct GroupDev {
 
 struct EncRankArgs {
     const TensorDesc *descs;
+    const uint32_t *tile_tensor;    // [tiles] tensor of each slab
     uint32_t n_tensors, slab;
     uint32_t *hall, *hchg;          // [tiles][256]
     uint64_t *rec;
@@ -68,6 +69,7 @@ struct EncRankArgs {
 
 struct HistArgs {
     const TensorDesc *descs;
+    const uint32_t *tile_tensor;
     uint32_t n_tensors, slab;
     uint32_t *hall;                 // [tiles][256]
     uint64_t *full;                 // [tiles]
@@ -124,14 +126,14 @@ struct DecodeArgs {
 
 struct SelectArgs {
     const TensorDesc *descs;
+    const uint32_t *tile_tensor;
     uint32_t n_tensors, slab;
     const uint32_t *pre;            // [tiles][256] exponent counts before the slab (in its tensor)
-    const uint32_t *lb;             // [tiles][256] first change of the group at or after the slab
+    const uint32_t *lb;             // [tiles + 1][256] first change of the group at or after the slab
     const int32_t *group_of;        // [tensor][256] group index or -1
     const GroupDev *groups;
     const uint32_t *local;          // group-local index of every change
-    uint32_t *pos;                  // [changes] element index
-    uint16_t *val;                  // [changes] old, then new bits
+    unsigned long long *pv;         // [changes] element index | bits << 32 (old, then new bits)
     const unsigned int *bad;
 };
 
@@ -143,8 +145,7 @@ struct BlockArgs {                  // per-block kernels over the change list (o
     const unsigned long long *blk_prefix;
     uint32_t *local;
     const uint32_t *zz;
-    uint32_t *pos;
-    uint16_t *val;
+    unsigned long long *pv;         // [changes] element index | bits << 32
     unsigned long long *tdelta;     // [tensors]
     unsigned int *bad;
 };
@@ -155,8 +156,8 @@ void launch_scan_tables(uint32_t *h, const ScanChunk *chunks, uint32_t n_chunks,
                         uint32_t n_tensors, uint32_t *csum, uint32_t *totals, hipStream_t s);
 void launch_enc_groups(const uint32_t *totals_chg, uint32_t n_tensors, GroupDev *groups, uint32_t *gbase,
                        unsigned long long *counters, hipStream_t s);
-void launch_place(const Chunk *chunks, uint32_t n_chunks, const uint64_t *rec, const TensorDesc *descs,
-                  uint32_t n_tensors, const uint32_t *hall_pre, const uint32_t *hchg_pre, const uint32_t *gbase,
+void launch_place(const Chunk *chunks, uint32_t n_chunks, const uint64_t *rec, const uint32_t *tile_tensor,
+                  const uint32_t *hall_pre, const uint32_t *hchg_pre, const uint32_t *gbase,
                   uint64_t *sorted, uint64_t n_sorted, hipStream_t s);
 void launch_r0(GroupDev *groups, uint32_t n_groups, const uint64_t *sorted, hipStream_t s);
 void launch_stats(const StatsArgs &a, hipStream_t s);
@@ -171,6 +172,8 @@ void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint6
 void launch_decode(const DecodeArgs &a, hipStream_t s);
 void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
 void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s);
+// tile_tensor[tile] = tensor of every slab of the layout
+void launch_tile_map(const TensorDesc *descs, uint32_t n_tensors, uint32_t *tile_tensor, hipStream_t s);
 void launch_select(const SelectArgs &a, uint32_t tiles, hipStream_t s);
 void launch_verify(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
 void launch_scatter(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);

@@ -46,14 +46,9 @@ __device__ __forceinline__ uint32_t zigzag(uint32_t o16, uint32_t n16) {
     return res >= 0 ? (uint32_t)(2 * res) : (uint32_t)(-2 * res - 1);
 }
 
-__device__ uint32_t tensor_of_tile(const TensorDesc *d, uint32_t n, uint32_t tau) {
-    uint32_t lo = 0, hi = n;  // last tensor whose first slab is <= tau
-    while (hi - lo > 1) {
-        uint32_t mid = (lo + hi) >> 1;
-        if (d[mid].tile_begin <= tau) lo = mid;
-        else hi = mid;
-    }
-    return lo;
+__global__ __launch_bounds__(256) void k_tile_map(const TensorDesc *descs, uint32_t *tile_tensor) {
+    const TensorDesc d = descs[blockIdx.x];
+    for (uint32_t i = threadIdx.x; i < d.n_tiles; i += 256) tile_tensor[d.tile_begin + i] = blockIdx.x;
 }
 
 // last group whose first change is <= i
@@ -268,7 +263,7 @@ __global__ __launch_bounds__(64) void k_enc_rank(EncRankArgs a) {
     __shared__ uint64_t meta[kChgCap];
     __shared__ uint32_t vals[kChgCap];
     const uint32_t tau = blockIdx.x;
-    const TensorDesc td = a.descs[tensor_of_tile(a.descs, a.n_tensors, tau)];
+    const TensorDesc td = a.descs[a.tile_tensor[tau]];
     const Slab sl = slab_of(td, tau - td.tile_begin, a.slab);
     for (uint32_t i = lane(); i < 1024; i += 64) hall[i] = 0;
     for (uint32_t i = lane(); i < 256; i += 64) hchg[i] = 0;
@@ -314,7 +309,7 @@ __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau,
 __global__ __launch_bounds__(64) void k_hist(HistArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t hall[256 * 4];
     const uint32_t tau = blockIdx.x;
-    const TensorDesc td = a.descs[tensor_of_tile(a.descs, a.n_tensors, tau)];
+    const TensorDesc td = a.descs[a.tile_tensor[tau]];
     const Slab sl = slab_of(td, tau - td.tile_begin, a.slab);
     for (uint32_t i = lane(); i < 1024; i += 64) hall[i] = 0;
     __syncthreads();
@@ -405,11 +400,11 @@ __global__ __launch_bounds__(1024) void k_enc_groups(const uint32_t *tot, uint32
 
 // Records -> update order: position = group start + changes of the group in earlier slabs + rank
 // among the slab's changes of that exponent; value = zz and the group-local index.
-__global__ __launch_bounds__(64) void k_place(const Chunk *chunks, const uint64_t *rec, const TensorDesc *descs,
-                                              uint32_t n_tensors, const uint32_t *hall_pre, const uint32_t *hchg_pre,
+__global__ __launch_bounds__(64) void k_place(const Chunk *chunks, const uint64_t *rec, const uint32_t *tile_tensor,
+                                              const uint32_t *hall_pre, const uint32_t *hchg_pre,
                                               const uint32_t *gbase, uint64_t *sorted, uint64_t n_sorted) {
     const Chunk c = chunks[blockIdx.x];
-    const uint32_t t = tensor_of_tile(descs, n_tensors, c.tile);
+    const uint32_t t = tile_tensor[c.tile];
     for (uint32_t j = lane(); j < c.count; j += 64) {
         const uint64_t r = rec[c.base + j];
         const uint32_t rank = (uint32_t)(r & 0x1FFFF), rc = (uint32_t)((r >> 17) & 0x1FFFF);
@@ -833,7 +828,7 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
         const unsigned long long local = base + a.local[eb + s];
         if (local >= size) atomicOr(a.bad, kBadLocal);
         a.local[eb + s] = (uint32_t)min<unsigned long long>(local, 0xFFFFFFFFULL);
-        a.pos[eb + s] = kNone;
+        a.pv[eb + s] = kNone;
     }
 }
 
@@ -842,7 +837,7 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
 __global__ __launch_bounds__(256) void k_locate(SelectArgs a) {
     if (*a.bad) return;
     const uint32_t tau = blockIdx.x, k = threadIdx.x;
-    const uint32_t t = tensor_of_tile(a.descs, a.n_tensors, tau);
+    const uint32_t t = a.tile_tensor[tau];
     const int32_t g = a.group_of[(uint64_t)t * 256 + k];
     uint32_t lb = kNone;
     if (g >= 0) {
@@ -863,44 +858,147 @@ __global__ __launch_bounds__(256) void k_locate(SelectArgs a) {
 // One wavefront per slab.  The slab's targets (group-local indices of its changes, minus the
 // exponent's count before the slab = ranks within the slab) are copied to LDS, per exponent in
 // order.  Streaming the slab, every element adds one to its exponent's count (4 copies by lane, few
-// same-address conflicts) and reads back the total: when the total passes the exponent's next target
-// rank, targets lie in this row.  The row's elements of that exponent are then published in LDS by
-// in-row rank (stable: ballots and mbcnt), and the targets, one per lane, read their element there.
+// same-address conflicts) and reads back the total with the exponent's next target: when the total
+// passes it, targets lie in this row.  The row's elements of that exponent are then published in
+// LDS by in-row rank (stable: ballots and mbcnt), and the targets, one per lane, read their element
+// there.
+//
+// The pass is bound by LDS latency, so the LDS footprint sets the speed through occupancy.  Only
+// exponents with targets in the slab need counting; they normally span a few consecutive values, so
+// the common kernel keeps state for a window of kWin exponents starting at the slab's lowest target
+// exponent and sends every other element to one of 16 spare counters (by lane, so the spare counts
+// never conflict).  Slabs whose target exponents span more than kWin values go to a second kernel
+// with state for all 256.
 constexpr uint32_t kTgtCap = 1024;  // targets per slab held in LDS; more are read from HBM
-constexpr uint32_t kNoKey = 256;    // exponent slot of lanes outside the slab (partial rows only)
+constexpr uint32_t kWin = 32;       // exponent window of the common kernel
+constexpr uint32_t kSpare = 16;     // spare counters for elements outside the window
 
+template <uint32_t W>
+struct SelectLds {
+    uint32_t cnt[(W + kSpare) * 4];  // running counts, 4 copies (lane & 3)
+    uint2 next[W + kSpare];          // per exponent: {rank of the next target, its list index}
+    uint2 range[W];                  // per exponent: {end of its list, group-local index - list index}
+    uint32_t pre[W];                 // exponent count before the slab (targets read from HBM only)
+    alignas(16) uint32_t list[kTgtCap];  // slab ranks of the targets, per exponent in order
+    uint32_t slot[kRow];             // in-row rank -> (in-row offset << 16) | bits, one exponent
+};
+
+template <uint32_t W, bool LDS_LIST>
+__device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase,
+                            SelectLds<W> &S) {
+    const uint32_t ln = lane(), rep = ln & 3, spare = W + (ln >> 2);
+    const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
+    stream_rows<kScanRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
+        // window index of each exponent; outside the window (or the slab): a spare counter
+        uint32_t c0 = min(((o >> 7) & 0xFF) - kbase, spare), c1 = min(((o >> 23) & 0xFF) - kbase, spare);
+        if (!row_full(sl, r)) {
+            const uint32_t f = r * kRow + 2 * ln;
+            if (f < sl.f_lo || f >= sl.f_hi) c0 = spare;
+            if (f + 1 < sl.f_lo || f + 1 >= sl.f_hi) c1 = spare;
+        }
+        atomicAdd(&S.cnt[4 * c0 + rep], 1u);
+        atomicAdd(&S.cnt[4 * c1 + rep], 1u);
+        const uint4 a0 = *reinterpret_cast<const uint4 *>(&S.cnt[4 * c0]);
+        const uint4 a1 = *reinterpret_cast<const uint4 *>(&S.cnt[4 * c1]);
+        const uint2 q0 = S.next[c0], q1 = S.next[c1];
+        const uint32_t s0 = a0.x + a0.y + a0.z + a0.w, s1 = a1.x + a1.y + a1.z + a1.w;
+        uint64_t H0 = ballot(s0 > q0.x), H1 = ballot(s1 > q1.x);
+        if (!(H0 | H1)) return;
+        wave_fence();
+        do {  // once per exponent with targets in this row
+            const bool from0 = H0 != 0;
+            const uint32_t l = (uint32_t)__builtin_ctzll(from0 ? H0 : H1);
+            const uint32_t k = from0 ? rdlane(c0, l) : rdlane(c1, l);
+            const uint32_t after = from0 ? rdlane(s0, l) : rdlane(s1, l);  // exponent-k count up to row end
+            uint32_t i = from0 ? rdlane(q0.y, l) : rdlane(q1.y, l);
+            const bool m0 = c0 == k, m1 = c1 == k;
+            const uint64_t M0 = ballot(m0), M1 = ballot(m1);
+            const uint32_t seen = after - (uint32_t)(__popcll(M0) + __popcll(M1));  // ... before this row
+            const uint32_t rr0 = mbcnt(M0) + mbcnt(M1);
+            if (m0) S.slot[rr0] = ((2 * ln) << 16) | (o & 0xFFFF);
+            if (m1) S.slot[rr0 + (m0 ? 1u : 0u)] = ((2 * ln + 1) << 16) | (o >> 16);
+            const uint2 rg = S.range[k];
+            wave_fence();
+            uint32_t nx;
+            for (;;) {  // this row's targets of exponent k, one per lane
+                const uint32_t j = i + ln;
+                uint32_t tc;
+                if (LDS_LIST) {
+                    const uint32_t lv = S.list[min(j, kTgtCap - 1)];
+                    tc = j < rg.x ? lv : (uint32_t)kFar;
+                } else {
+                    tc = j < rg.x ? a.local[rg.y + j] - S.pre[k] : (uint32_t)kFar;
+                }
+                const bool take = tc < after;
+                const uint32_t n = (uint32_t)__popcll(ballot(take));
+                if (take) {
+                    const uint32_t w = S.slot[tc - seen];
+                    a.pv[rg.y + j] = (unsigned long long)(sl.base + r * kRow + (w >> 16)) |
+                                     ((unsigned long long)(w & 0xFFFF) << 32);
+                }
+                i += n;
+                if (n < 64) {
+                    nx = rdlane(tc, n);  // the first target not taken, or kFar
+                    break;
+                }
+            }
+            wave_fence();
+            if (ln == 0) S.next[k] = make_uint2(nx, i);
+            wave_fence();
+            H0 &= ~M0;
+            H1 &= ~M1;
+        } while (H0 | H1);
+    });
+}
+
+// W == kWin: slabs whose target exponents lie within kWin consecutive values; W == 256: the others.
+template <uint32_t W>
 __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
-    __shared__ __attribute__((aligned(16))) uint32_t cnt[(kNoKey + 1) * 4];
-    __shared__ uint32_t tgt[kNoKey + 1], tix[256], tend[256], jofs[256], pre[256];
-    __shared__ uint32_t list[kTgtCap];
-    __shared__ uint32_t slot[kRow];
-    uint32_t *toff = cnt;  // list offsets per exponent, needed only while the list is copied
+    __shared__ __attribute__((aligned(16))) SelectLds<W> S;
     if (*a.bad) return;
-    const uint32_t tau = blockIdx.x, ln = lane(), rep = ln & 3;
-    const uint32_t t = tensor_of_tile(a.descs, a.n_tensors, tau);
+    const uint32_t tau = blockIdx.x, ln = lane();
+    const uint32_t t = a.tile_tensor[tau];
     const TensorDesc td = a.descs[t];
+    int32_t g4[4];
+    uint32_t j0[4], j1[4], pr[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {  // independent loads, issued together
+        const uint32_t k = 4 * ln + q;
+        g4[q] = a.group_of[(uint64_t)t * 256 + k];
+        j0[q] = a.lb[(uint64_t)tau * 256 + k];
+        j1[q] = a.lb[(uint64_t)(tau + 1) * 256 + k];
+        pr[q] = a.pre[(uint64_t)tau * 256 + k];
+    }
     const uint32_t local_tile = tau - td.tile_begin;
-    const Slab sl = slab_of(td, local_tile, a.slab);
+    const bool last = local_tile + 1 >= td.n_tiles;
 
     // targets of this slab: group changes [lb(slab), lb(next slab)) of each exponent
-    uint32_t n4[4], j4[4], mine = 0;
+    uint32_t n4[4], mine = 0, klo = 256, khi = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const uint32_t k = 4 * ln + q;
-        const int32_t g = a.group_of[(uint64_t)t * 256 + k];
         n4[q] = 0;
-        j4[q] = 0;
-        if (g >= 0) {
-            const GroupDev gr = a.groups[g];
-            const uint32_t j0 = a.lb[(uint64_t)tau * 256 + k];
-            const uint32_t je = local_tile + 1 < td.n_tiles ? a.lb[(uint64_t)(tau + 1) * 256 + k] : gr.elem_base + gr.count;
-            if (j0 < je) {
-                n4[q] = je - j0;
-                j4[q] = j0;
+        if (g4[q] >= 0) {
+            uint32_t je = j1[q];
+            if (last) {
+                const GroupDev gr = a.groups[g4[q]];
+                je = gr.elem_base + gr.count;
             }
+            if (j0[q] < je) n4[q] = je - j0[q];
         }
         mine += n4[q];
+        if (n4[q]) {
+            klo = min(klo, 4 * ln + q);
+            khi = max(khi, 4 * ln + q);
+        }
     }
+    for (int o = 32; o > 0; o >>= 1) {
+        klo = min(klo, (uint32_t)__shfl_xor(klo, o, 64));
+        khi = max(khi, (uint32_t)__shfl_xor(khi, o, 64));
+    }
+    if (klo > khi) return;                       // no targets in this slab
+    if ((khi - klo < kWin) != (W == kWin)) return;  // the other kernel's slab
+    const uint32_t kbase = W == kWin ? klo : 0;
+
     uint32_t incl = mine;  // inclusive scan of per-lane totals across the wave
     for (int o = 1; o < 64; o <<= 1) {
         const uint32_t v = __shfl_up(incl, o, 64);
@@ -908,95 +1006,74 @@ __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
     }
     const uint32_t total = __shfl(incl, 63, 64);
     const bool in_lds = total <= kTgtCap;
-    uint32_t off = incl - mine;
+    uint32_t start[4], off = incl - mine;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const uint32_t k = 4 * ln + q;
-        toff[k] = off;
-        tix[k] = off;
-        tend[k] = off + n4[q];
-        jofs[k] = j4[q] - off;
-        pre[k] = a.pre[(uint64_t)tau * 256 + k];
+        const uint32_t c = 4 * ln + q - kbase;
+        start[q] = off;
+        if (c < W) {
+            S.range[c] = make_uint2(off + n4[q], j0[q] - off);
+            S.pre[c] = pr[q];
+        }
         off += n4[q];
     }
-    wave_fence();
     if (in_lds) {
-        for (uint32_t x = ln; x < total; x += 64) {
-            uint32_t lo = 0, hi = 256;  // last exponent whose list starts at or before x
-            while (hi - lo > 1) {
-                const uint32_t mid = (lo + hi) >> 1;
-                if (toff[mid] <= x) lo = mid;
-                else hi = mid;
-            }
-            list[x] = a.local[jofs[lo] + x] - pre[lo];
-        }
-    }
-    wave_fence();
-    for (uint32_t k = ln; k < 256; k += 64) {
-        const uint32_t i = tix[k];
-        tgt[k] = i < tend[k] ? (in_lds ? list[i] : a.local[jofs[k] + i] - pre[k]) : (uint32_t)kFar;
-    }
-    if (ln == 0) tgt[kNoKey] = (uint32_t)kFar;
-    wave_fence();
-    for (uint32_t i = ln; i < (kNoKey + 1) * 4; i += 64) cnt[i] = 0;
-    wave_fence();
-
-    const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
-    stream_rows<kScanRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
-        uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF;
-        if (!row_full(sl, r)) {
-            const uint32_t f = r * kRow + 2 * ln;
-            if (f < sl.f_lo || f >= sl.f_hi) k0 = kNoKey;
-            if (f + 1 < sl.f_lo || f + 1 >= sl.f_hi) k1 = kNoKey;
-        }
-        atomicAdd(&cnt[4 * k0 + rep], 1u);
-        atomicAdd(&cnt[4 * k1 + rep], 1u);
-        const uint4 a0 = *reinterpret_cast<const uint4 *>(&cnt[4 * k0]);
-        const uint4 a1 = *reinterpret_cast<const uint4 *>(&cnt[4 * k1]);
-        const uint32_t s0 = a0.x + a0.y + a0.z + a0.w, s1 = a1.x + a1.y + a1.z + a1.w;
-        uint64_t H0 = ballot(s0 > tgt[k0]), H1 = ballot(s1 > tgt[k1]);
-        if (!(H0 | H1)) return;
+        // list entry x belongs to the last exponent whose list starts at or before x: mark the starts
+        // of the non-empty lists, then a running maximum over the entries (16 per lane, in order)
+        uint32_t *mark = S.list;  // read into registers before the list overwrites it
+        for (uint32_t x = ln; x < kTgtCap; x += 64) mark[x] = 0;
         wave_fence();
-        do {  // once per exponent with targets in this row
-            const bool from0 = H0 != 0;
-            const uint32_t l = (uint32_t)__builtin_ctzll(from0 ? H0 : H1);
-            const uint32_t k = from0 ? rdlane(k0, l) : rdlane(k1, l);
-            const uint32_t after = from0 ? rdlane(s0, l) : rdlane(s1, l);  // exponent-k count up to row end
-            const bool m0 = k0 == k, m1 = k1 == k;
-            const uint64_t M0 = ballot(m0), M1 = ballot(m1);
-            const uint32_t seen = after - (uint32_t)(__popcll(M0) + __popcll(M1));  // ... before this row
-            const uint32_t rr0 = mbcnt(M0) + mbcnt(M1);
-            if (m0) slot[rr0] = ((2 * ln) << 16) | (o & 0xFFFF);
-            if (m1) slot[rr0 + (m0 ? 1u : 0u)] = ((2 * ln + 1) << 16) | (o >> 16);
-            wave_fence();
-            uint32_t i = tix[k], next;
-            const uint32_t ie = tend[k], jo = jofs[k], pk = pre[k];
-            for (;;) {  // this row's targets of exponent k, one per lane
-                const uint32_t j = i + ln;
-                const uint32_t tc = j < ie ? (in_lds ? list[j] : a.local[jo + j] - pk) : (uint32_t)kFar;
-                const bool take = tc < after;
-                const uint32_t n = (uint32_t)__popcll(ballot(take));
-                if (take) {
-                    const uint32_t w = slot[tc - seen];
-                    a.pos[jo + j] = sl.base + r * kRow + (w >> 16);
-                    a.val[jo + j] = (uint16_t)w;
-                }
-                i += n;
-                if (n < 64) {
-                    next = rdlane(tc, n);  // the first target not taken, or kFar
-                    break;
-                }
-            }
-            wave_fence();
-            if (ln == 0) {
-                tix[k] = i;
-                tgt[k] = next;
-            }
-            wave_fence();
-            H0 &= ~M0;
-            H1 &= ~M1;
-        } while (H0 | H1);
-    });
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (n4[q]) mark[start[q]] = 4 * ln + q - kbase + 1;
+        wave_fence();
+        uint32_t v[16], run = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const uint4 m = *reinterpret_cast<const uint4 *>(&mark[16 * ln + i]);
+            v[i] = run = max(run, m.x);
+            v[i + 1] = run = max(run, m.y);
+            v[i + 2] = run = max(run, m.z);
+            v[i + 3] = run = max(run, m.w);
+        }
+        uint32_t before = run;  // inclusive max-scan of the lane maxima, then shifted by one lane
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t w = __shfl_up(before, o, 64);
+            if (ln >= (uint32_t)o) before = max(before, w);
+        }
+        before = __shfl_up(before, 1, 64);
+        if (ln == 0) before = 0;
+        uint32_t idx[16], sub[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t c = max(before, v[i]);
+            const uint32_t cc = c ? c - 1 : 0;
+            idx[i] = S.range[cc].y + 16 * ln + i;
+            sub[i] = S.pre[cc];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t x = 16 * ln + i;
+            if (x < total) S.list[x] = a.local[idx[i]] - sub[i];
+        }
+    }
+    wave_fence();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t c = 4 * ln + q - kbase;
+        if (c < W) {
+            uint32_t first = (uint32_t)kFar;
+            if (n4[q]) first = in_lds ? S.list[start[q]] : a.local[j0[q]] - pr[q];
+            S.next[c] = make_uint2(first, start[q]);
+        }
+    }
+    if (ln < kSpare) S.next[W + ln] = make_uint2((uint32_t)kFar, 0u);
+    wave_fence();
+    for (uint32_t i = ln; i < (W + kSpare) * 4; i += 64) S.cnt[i] = 0;
+    wave_fence();
+    const Slab sl = slab_of(td, local_tile, a.slab);
+    if (in_lds) select_slab<W, true>(a, td, sl, kbase, S);
+    else select_slab<W, false>(a, td, sl, kbase, S);
 }
 
 // new = (old + unzigzag(zz)) mod 2^16; checksum delta per tensor (codec.py:698-700).
@@ -1013,16 +1090,17 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
     unsigned long long d = 0;
     if (s < cnt) {
         const uint64_t j = eb + s;
-        const uint32_t p = a.pos[j];
+        const unsigned long long pv = a.pv[j];
+        const uint32_t p = (uint32_t)pv;
         if (p == kNone) {
             atomicOr(a.bad, kBadUnplaced);
         } else {
             const uint32_t zz = a.zz[j];
             const int32_t delta = (int32_t)(zz >> 1) ^ -(int32_t)(zz & 1);
-            const uint32_t old = a.val[j];
+            const uint32_t old = (uint32_t)(pv >> 32);
             const uint32_t nu = (uint32_t)((int32_t)old + delta) & 0xFFFF;
             d = (uint64_t)((int64_t)nu - (int64_t)old) * weight(p);
-            a.val[j] = (uint16_t)nu;
+            a.pv[j] = p | ((unsigned long long)nu << 32);
         }
     }
     unsigned long long total;
@@ -1038,7 +1116,10 @@ __global__ __launch_bounds__(256) void k_scatter(BlockArgs a) {
     const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
     const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
     const uint32_t s = threadIdx.x;
-    if (s < cnt) a.descs[gr.tensor].base[a.pos[eb + s]] = a.val[eb + s];
+    if (s < cnt) {
+        const unsigned long long pv = a.pv[eb + s];
+        a.descs[gr.tensor].base[(uint32_t)pv] = (uint16_t)(pv >> 32);
+    }
 }
 
 inline uint32_t grid1(uint64_t n, uint32_t per) { return (uint32_t)((n + per - 1) / per); }
@@ -1072,11 +1153,14 @@ void launch_enc_groups(const uint32_t *totals_chg, uint32_t n_tensors, GroupDev 
     CRX_LAUNCH("enc_groups", k_enc_groups, 1, 1024, s, totals_chg, n_tensors, groups, gbase, counters);
 }
 
-void launch_place(const Chunk *chunks, uint32_t n_chunks, const uint64_t *rec, const TensorDesc *descs,
-                  uint32_t n_tensors, const uint32_t *hall_pre, const uint32_t *hchg_pre, const uint32_t *gbase,
+void launch_place(const Chunk *chunks, uint32_t n_chunks, const uint64_t *rec, const uint32_t *tile_tensor,
+                  const uint32_t *hall_pre, const uint32_t *hchg_pre, const uint32_t *gbase,
                   uint64_t *sorted, uint64_t n_sorted, hipStream_t s) {
-    CRX_LAUNCH("place", k_place, n_chunks, 64, s, chunks, rec, descs, n_tensors, hall_pre, hchg_pre, gbase, sorted,
-               n_sorted);
+    CRX_LAUNCH("place", k_place, n_chunks, 64, s, chunks, rec, tile_tensor, hall_pre, hchg_pre, gbase, sorted, n_sorted);
+}
+
+void launch_tile_map(const TensorDesc *descs, uint32_t n_tensors, uint32_t *tile_tensor, hipStream_t s) {
+    CRX_LAUNCH("tile_map", k_tile_map, n_tensors, 256, s, descs, tile_tensor);
 }
 
 void launch_r0(GroupDev *groups, uint32_t n_groups, const uint64_t *sorted, hipStream_t s) {
@@ -1117,7 +1201,10 @@ void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
 
 void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("locate", k_locate, tiles, 256, s, a); }
 
-void launch_select(const SelectArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("select", k_select, tiles, 64, s, a); }
+void launch_select(const SelectArgs &a, uint32_t tiles, hipStream_t s) {
+    CRX_LAUNCH("select", k_select<kWin>, tiles, 64, s, a);
+    CRX_LAUNCH("select_wide", k_select<256>, tiles, 64, s, a);
+}
 
 void launch_verify(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
     CRX_LAUNCH("verify", k_verify, (uint32_t)n_blocks, 256, s, a);
