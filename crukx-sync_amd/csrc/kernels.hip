@@ -76,7 +76,8 @@ __device__ uint32_t group_of_block(const GroupDev *g, uint32_t n, uint64_t b) {
 // ================================================================== slab streaming
 // A wavefront reads its slab as rows of 64 lanes x one 32-bit word (two consecutive bf16), 32-bit
 // offsets relative to the slab's first frame word.  Interior rows need no masking; only the first
-// (odd start) and last (partial) rows do.
+// (odd start) and last (partial) rows do, and the rows past the end that complete the last batch
+// (every lane outside [f_lo, f_hi)).
 struct Slab {
     uint32_t first;   // frame word index of the slab's first word
     uint32_t nwords;  // words covering the slab
@@ -84,6 +85,7 @@ struct Slab {
     uint32_t f_hi;
     uint32_t base;    // tensor index of offset 0 (mod 2^32): element f is tensor element base + f
     uint32_t nrows;
+    uint32_t full_lo, full_n;  // rows [full_lo, full_lo + full_n) lie entirely in [f_lo, f_hi)
 };
 
 __device__ __forceinline__ Slab slab_of(const TensorDesc &td, uint32_t local, uint32_t slab) {
@@ -96,12 +98,13 @@ __device__ __forceinline__ Slab slab_of(const TensorDesc &td, uint32_t local, ui
     s.f_hi = (uint32_t)(hi + td.lead - 2 * d_begin);
     s.base = (uint32_t)(2 * d_begin - td.lead);
     s.nrows = (s.nwords + 63) / 64;
+    s.full_lo = (s.f_lo + kRow - 1) / kRow;
+    const uint32_t full_hi = s.f_hi / kRow;
+    s.full_n = full_hi > s.full_lo ? full_hi - s.full_lo : 0;
     return s;
 }
 
-__device__ __forceinline__ bool row_full(const Slab &s, uint32_t r) {
-    return r * kRow >= s.f_lo && r * kRow + kRow <= s.f_hi;
-}
+__device__ __forceinline__ bool row_full(const Slab &s, uint32_t r) { return r - s.full_lo < s.full_n; }
 
 // Raw buffer resource over the slab's words [p, p + nwords): the hardware range check returns 0 for
 // any load at or past the end, so rows fetched ahead of the slab's end need neither masks nor
@@ -114,7 +117,8 @@ __device__ __forceinline__ Rsrc slab_rsrc(const uint32_t *frame, const Slab &s) 
 
 // Streams the slab's rows through `body(row, word of stream 0, word of stream S-1)`, U rows per batch
 // with the next batch already in flight (double buffering keeps U..2U rows of loads outstanding
-// per wavefront while a batch is processed).
+// per wavefront while a batch is processed).  Every batch is whole: rows at or past nrows read as
+// zero and lie outside [f_lo, f_hi), so the body treats them as partial rows with no valid lane.
 template <int U, int S, typename Body>
 __device__ __forceinline__ void stream_rows(const Slab &sl, const Rsrc (&src)[S], Body &&body) {
     const uint32_t lb = lane() * 4u;
@@ -130,10 +134,7 @@ __device__ __forceinline__ void stream_rows(const Slab &sl, const Rsrc (&src)[S]
 #pragma unroll
             for (int q = 0; q < S; ++q) nxt[q][u] = __builtin_amdgcn_raw_buffer_load_b32(src[q], nb + u * 256u, 0, 0);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (r0 + u >= sl.nrows) break;
-            body(r0 + u, cur[0][u], cur[S - 1][u]);
-        }
+        for (int u = 0; u < U; ++u) body(r0 + u, cur[0][u], cur[S - 1][u]);
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -880,7 +881,7 @@ struct SelectLds {
     uint2 range[W];                  // per exponent: {end of its list, group-local index - list index}
     uint32_t pre[W];                 // exponent count before the slab (targets read from HBM only)
     alignas(16) uint32_t list[kTgtCap];  // slab ranks of the targets, per exponent in order
-    uint32_t slot[kRow];             // in-row rank -> (in-row offset << 16) | bits, one exponent
+    uint32_t slot[2 * kRow];         // in-row rank -> (in-row offset << 16) | bits; [kRow, 2 kRow): per lane, unused
 };
 
 template <uint32_t W, bool LDS_LIST>
@@ -906,23 +907,24 @@ __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Sla
         if (!(H0 | H1)) return;
         wave_fence();
         do {  // once per exponent with targets in this row
-            const bool from0 = H0 != 0;
-            const uint32_t l = (uint32_t)__builtin_ctzll(from0 ? H0 : H1);
-            const uint32_t k = from0 ? rdlane(c0, l) : rdlane(c1, l);
-            const uint32_t after = from0 ? rdlane(s0, l) : rdlane(s1, l);  // exponent-k count up to row end
-            uint32_t i = from0 ? rdlane(q0.y, l) : rdlane(q1.y, l);
+            // a lane whose element of that exponent triggered: its count, and the next target's index
+            const uint32_t l = (uint32_t)__builtin_ctzll(H0 | H1);
+            const bool use0 = (H0 >> l) & 1;
+            const uint32_t k = rdlane(use0 ? c0 : c1, l);
+            const uint32_t after = rdlane(use0 ? s0 : s1, l);  // exponent-k count up to the row's end
+            uint32_t i = rdlane(use0 ? q0.y : q1.y, l);
             const bool m0 = c0 == k, m1 = c1 == k;
             const uint64_t M0 = ballot(m0), M1 = ballot(m1);
             const uint32_t seen = after - (uint32_t)(__popcll(M0) + __popcll(M1));  // ... before this row
             const uint32_t rr0 = mbcnt(M0) + mbcnt(M1);
-            if (m0) S.slot[rr0] = ((2 * ln) << 16) | (o & 0xFFFF);
-            if (m1) S.slot[rr0 + (m0 ? 1u : 0u)] = ((2 * ln + 1) << 16) | (o >> 16);
+            // publish by in-row rank; other lanes write a slot of their own past the ranks
+            S.slot[m0 ? rr0 : kRow + ln] = ((2 * ln) << 16) | (o & 0xFFFF);
+            S.slot[m1 ? rr0 + (m0 ? 1u : 0u) : kRow + ln] = ((2 * ln + 1) << 16) | (o >> 16);
             const uint2 rg = S.range[k];
             wave_fence();
-            uint32_t nx;
-            for (;;) {  // this row's targets of exponent k, one per lane
+            uint32_t n, tc;
+            do {  // this row's targets of exponent k, one per lane (64 more if all lanes take one)
                 const uint32_t j = i + ln;
-                uint32_t tc;
                 if (LDS_LIST) {
                     const uint32_t lv = S.list[min(j, kTgtCap - 1)];
                     tc = j < rg.x ? lv : (uint32_t)kFar;
@@ -930,18 +932,15 @@ __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Sla
                     tc = j < rg.x ? a.local[rg.y + j] - S.pre[k] : (uint32_t)kFar;
                 }
                 const bool take = tc < after;
-                const uint32_t n = (uint32_t)__popcll(ballot(take));
+                n = (uint32_t)__popcll(ballot(take));
                 if (take) {
                     const uint32_t w = S.slot[tc - seen];
                     a.pv[rg.y + j] = (unsigned long long)(sl.base + r * kRow + (w >> 16)) |
                                      ((unsigned long long)(w & 0xFFFF) << 32);
                 }
                 i += n;
-                if (n < 64) {
-                    nx = rdlane(tc, n);  // the first target not taken, or kFar
-                    break;
-                }
-            }
+            } while (n == 64);
+            const uint32_t nx = rdlane(tc, n);  // the first target not taken, or kFar
             wave_fence();
             if (ln == 0) S.next[k] = make_uint2(nx, i);
             wave_fence();
