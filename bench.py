@@ -136,7 +136,8 @@ def main():
     avg_ms = tot_ms / calls
     achieved = alg_bytes[dom] / (avg_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(args.workload, args.rho, dom),
                 "avg_launch_ms": round(avg_ms, 4), "alg_bytes_per_launch": alg_bytes[dom]}
     whole = (6 * N + upd_bytes + 2 * changes) / (ms_step * 1e-3) / 1e9  # encode 4N+P, apply 2N+P+2C
 
@@ -174,6 +175,19 @@ def main():
                       "tensors": len(shapes), "weights": N, "rho": args.rho},
            "roofline": roofline, "cpu_baseline": cpu, "detail": detail}
     print(json.dumps(out), flush=True)
+
+
+def measured_traffic(workload, rho, kernel):
+    """HBM bytes per launch of `kernel` (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, calibrated against a 2 GiB
+    copy) as recorded by rocprofv3 for this workload in profiles/, or None when not recorded."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f)
+    if rec.get("rho") != rho or kernel not in rec.get("kernels", {}):
+        return None
+    return rec["kernels"][kernel]["bytes"]
 
 
 def cpu_baseline(args, shapes, states, N, log):

@@ -48,10 +48,9 @@ int32_t crx_abi_version(void);
 
 /* ------------------------------------------------------------------ wire format (host)
  * Replaces wire.parse (src/crukx_sync/wire.py:126-212): magic, version, every limit of
- * docs/FORMAT.md:46-57 in the reference's order.  `data` holds the whole update (host memory).
- * With `payload_on_device` != 0 the caller promises only the bytes up to the payload start plus
- * the final byte; crx_parse then checks the header and block table and stores the payload
- * offset, and the payload itself must be passed to crx_apply as a device pointer. */
+ * docs/FORMAT.md:46-57 in the reference's order.  `data` holds the whole update (host memory);
+ * crx_apply uploads the payload from it unless given a device copy.  For an update held in
+ * device memory, crx_parse_prefix parses a host copy of its leading bytes. */
 int32_t crx_parse(const uint8_t *data, uint64_t len, crx_update **out, char *err, uint64_t errlen);
 /* Parses from a prefix of an update held elsewhere: `prefix` has `prefix_len` bytes of an update
  * of `total_len` bytes whose last byte is `last_byte`.  Returns CRX_OK, CRX_CORRUPT, or
