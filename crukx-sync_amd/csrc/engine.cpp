@@ -396,7 +396,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     unsigned long long *wsum = ar.get<unsigned long long>(n_wg), *woff = ar.get<unsigned long long>(n_wg + 1);
     CodeArgs ca{sorted, C, d_groups2, (uint32_t)G, d_lut, d_rk, d_rv, (uint32_t)rkeys.size(), wsum, woff, nullptr, nullptr};
     launch_code_lengths(ca, s);
-    launch_scan_u64(wsum, n_wg, woff, s);
+    launch_scan_u64(wsum, n_wg, woff, ar.get<unsigned long long>(scan_parts(n_wg)), s);
     unsigned long long total_bits = 0;
     d2h(&total_bits, woff + n_wg, 1, s);
     sync(s);
@@ -447,7 +447,10 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     // groups, decoding tables and the group lookup (codec.py:594-625)
     int table_of[256];
     std::fill(table_of, table_of + 256, -1);
-    std::vector<uint32_t> tab(u.tables.size() * 54, 0), syms;
+    // per table and code length l: lim = end of the length-l codes left-justified to 17 bits (the
+    // canonical ranges are consecutive, so the length of a 17-bit peek p is 1 + #{l : lim[l] <= p}),
+    // off = symbol index of the length-l code 0
+    std::vector<uint32_t> lim(u.tables.size() * 17, 0), off(u.tables.size() * 17, 0), syms;
     for (size_t ti = 0; ti < u.tables.size(); ++ti) {
         const Table &tb = u.tables[ti];
         table_of[tb.exponent] = (int)ti;
@@ -458,9 +461,8 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
         std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return tb.lengths[a] < tb.lengths[b]; });
         uint32_t code = 0, idx = (uint32_t)syms.size();
         for (int l = 1; l <= kMaxCodeLen; ++l) {
-            tab[ti * 54 + l] = code;
-            tab[ti * 54 + 18 + l] = per_len[l];
-            tab[ti * 54 + 36 + l] = idx;
+            lim[ti * 17 + l - 1] = (code + per_len[l]) << (kMaxCodeLen - l);
+            off[ti * 17 + l - 1] = idx - code;
             code = (code + per_len[l]) << 1;
             idx += per_len[l];
         }
@@ -494,14 +496,16 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     uint32_t *sizes = ar.get<uint32_t>((uint64_t)T * 256);
     GroupDev *d_groups = ar.get<GroupDev>(G);
     int32_t *d_gof = ar.get<int32_t>((uint64_t)T * 256);
-    uint32_t *d_tab = ar.get<uint32_t>(tab.size()), *d_syms = ar.get<uint32_t>(syms.size());
+    uint32_t *d_lim = ar.get<uint32_t>(lim.size()), *d_off = ar.get<uint32_t>(off.size());
+    uint32_t *d_syms = ar.get<uint32_t>(syms.size());
     uint32_t *d_bb = ar.get<uint32_t>(B);
     unsigned long long *boff = ar.get<unsigned long long>(B + 1);
     const uint64_t pay_words = (u.payload_len + 7) / 8 + 2;
     uint64_t *pay = ar.get<uint64_t>(pay_words);
     h2d(d_groups, groups.data(), G, s);
     h2d(d_gof, group_of.data(), group_of.size(), s);
-    h2d(d_tab, tab.data(), tab.size(), s);
+    h2d(d_lim, lim.data(), lim.size(), s);
+    h2d(d_off, off.data(), off.size(), s);
     h2d(d_syms, syms.data(), syms.size(), s);
     h2d(d_bb, u.block_bits.data(), B, s);
     zero(pay, pay_words, s);
@@ -517,7 +521,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     launch_hist(ha, tiles, s);
     launch_scan_tables(hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, sizes, s);
     launch_tensor_sums(d_descs, T, full, t_full, s);
-    launch_scan_u32(d_bb, B, boff, s);
+    launch_scan_u32(d_bb, B, boff, ar.get<unsigned long long>(scan_parts(B)), s);
 
     uint32_t *zz = ar.get<uint32_t>(C), *local = ar.get<uint32_t>(C);
     unsigned long long *pv = ar.get<unsigned long long>(C);
@@ -527,13 +531,16 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     uint32_t *lb = ar.get<uint32_t>((uint64_t)(tiles + 1) * 256);  // row tiles: read, never used
     zero(bad, 1, s);
     zero(tdelta, T, s);
-    DecodeArgs da{pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, sizes, d_tab, d_syms, (uint32_t)syms.size(),
+    DecodeArgs da{pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, sizes, d_lim, d_off, d_syms, (uint32_t)syms.size(),
                   zz, local, blk_sum, bad};
     launch_decode(da, s);
-    launch_scan_u64(blk_sum, B, blk_prefix, s);
+    launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), s);
     BlockArgs ba{d_groups, (uint32_t)G, d_descs, sizes, blk_prefix, local, zz, pv, tdelta, bad};
     launch_local_fix(ba, B, s);
-    SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, pv, bad};
+    uint32_t *wide = ar.get<uint32_t>(tiles);
+    unsigned int *n_wide = ar.get<unsigned int>(1);
+    zero(n_wide, 1, s);
+    SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, pv, bad, wide, n_wide};
     launch_locate(sa, tiles, s);
     launch_select(sa, tiles, s);
     launch_verify(ba, B, s);

@@ -115,7 +115,8 @@ struct DecodeArgs {
     const GroupDev *groups;
     uint32_t n_groups;
     const uint32_t *sizes;          // [tensor][256] group sizes of the receiver
-    const uint32_t *tab;            // [tables][3][18]: first, count, base per code length
+    const uint32_t *lim;            // [tables][17]: end of length l's codes, left-justified to 17 bits
+    const uint32_t *off;            // [tables][17]: symbol index of code 0 of length l (mod 2^32)
     const uint32_t *syms;
     uint32_t n_syms;
     uint32_t *zz;                   // [changes]
@@ -135,6 +136,8 @@ struct SelectArgs {
     const uint32_t *local;          // group-local index of every change
     unsigned long long *pv;         // [changes] element index | bits << 32 (old, then new bits)
     const unsigned int *bad;
+    uint32_t *wide;                 // [tiles] slabs left to the all-exponent select kernel
+    unsigned int *n_wide;           // their number (zero before the select pass)
 };
 
 struct BlockArgs {                  // per-block kernels over the change list (one workgroup per block)
@@ -165,11 +168,15 @@ void launch_code_lengths(const CodeArgs &a, hipStream_t s);
 void launch_pack(const CodeArgs &a, hipStream_t s);
 void launch_block_bits(const unsigned long long *bstart, uint64_t n_blocks, uint32_t *out, unsigned int *overflow,
                        hipStream_t s);
-void launch_scan_u64(const unsigned long long *in, uint64_t n, unsigned long long *out, hipStream_t s);
-void launch_scan_u32(const uint32_t *in, uint64_t n, unsigned long long *out, hipStream_t s);
+// Exclusive prefix sums with out[n] = total; `part` holds scan_parts(n) values of scratch.
+uint64_t scan_parts(uint64_t n);
+void launch_scan_u64(const unsigned long long *in, uint64_t n, unsigned long long *out, unsigned long long *part,
+                     hipStream_t s);
+void launch_scan_u32(const uint32_t *in, uint64_t n, unsigned long long *out, unsigned long long *part, hipStream_t s);
 void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint64_t *per_tile, uint64_t *out,
                         hipStream_t s);
 void launch_decode(const DecodeArgs &a, hipStream_t s);
+constexpr uint32_t kDecSyms = 2048;  // decoding symbols staged in LDS when they fit
 void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
 void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s);
 // tile_tensor[tile] = tensor of every slab of the layout

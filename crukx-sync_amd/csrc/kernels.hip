@@ -274,46 +274,56 @@ __global__ __launch_bounds__(64) void k_enc_rank(EncRankArgs a) {
 }
 
 // ================================================================== apply: histogram pass
+// 16 copies of every exponent's count, copy = lane & 15: within a half-wavefront each lane owns a
+// bank, so the atomics of a row rarely collide.  Lanes outside the slab count into exponent slot 256.
+constexpr uint32_t kHistCopies = 16;
+
 template <bool COLD>
 __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau, const Slab &sl, uint32_t *hall) {
-    const uint32_t ln = lane(), rep = ln & 3;
+    const uint32_t ln = lane(), rep = ln & (kHistCopies - 1);
     const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
     uint64_t facc = 0;
     stream_rows<kScanRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
         const uint32_t f = r * kRow + 2 * ln;
-        if (row_full(sl, r)) {
-            atomicAdd(&hall[4 * ((o >> 7) & 0xFF) + rep], 1u);
-            atomicAdd(&hall[4 * ((o >> 23) & 0xFF) + rep], 1u);
-            if (COLD) {
-                facc += (uint64_t)(o & 0xFFFF) * weight(sl.base + f);
-                facc += (uint64_t)(o >> 16) * weight(sl.base + f + 1);
+        uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF, v = o;
+        if (!row_full(sl, r)) {
+            if (f < sl.f_lo || f >= sl.f_hi) {
+                k0 = 256;
+                v &= 0xFFFF0000u;
             }
-        } else {
-            const bool v0 = f >= sl.f_lo && f < sl.f_hi, v1 = f + 1 >= sl.f_lo && f + 1 < sl.f_hi;
-            if (v0) atomicAdd(&hall[4 * ((o >> 7) & 0xFF) + rep], 1u);
-            if (v1) atomicAdd(&hall[4 * ((o >> 23) & 0xFF) + rep], 1u);
-            if (COLD) {
-                if (v0) facc += (uint64_t)(o & 0xFFFF) * weight(sl.base + f);
-                if (v1) facc += (uint64_t)(o >> 16) * weight(sl.base + f + 1);
+            if (f + 1 < sl.f_lo || f + 1 >= sl.f_hi) {
+                k1 = 256;
+                v &= 0xFFFFu;
             }
+        }
+        atomicAdd(&hall[k0 * kHistCopies + rep], 1u);
+        atomicAdd(&hall[k1 * kHistCopies + rep], 1u);
+        if (COLD) {
+            facc += (uint64_t)(v & 0xFFFF) * weight(sl.base + f);
+            facc += (uint64_t)(v >> 16) * weight(sl.base + f + 1);
         }
     });
     wave_fence();
     for (uint32_t k = ln; k < 256; k += 64) {
-        const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
-        a.hall[(uint64_t)tau * 256 + k] = h.x + h.y + h.z + h.w;
+        uint32_t sum = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < kHistCopies; q += 4) {
+            const uint4 h = *reinterpret_cast<const uint4 *>(&hall[k * kHistCopies + q]);
+            sum += h.x + h.y + h.z + h.w;
+        }
+        a.hall[(uint64_t)tau * 256 + k] = sum;
     }
     facc = wave_sum(facc);
     if (ln == 0) a.full[tau] = facc;
 }
 
 __global__ __launch_bounds__(64) void k_hist(HistArgs a) {
-    __shared__ __attribute__((aligned(16))) uint32_t hall[256 * 4];
+    __shared__ __attribute__((aligned(16))) uint32_t hall[257 * kHistCopies];
     const uint32_t tau = blockIdx.x;
     const TensorDesc td = a.descs[a.tile_tensor[tau]];
     const Slab sl = slab_of(td, tau - td.tile_begin, a.slab);
-    for (uint32_t i = lane(); i < 1024; i += 64) hall[i] = 0;
-    __syncthreads();
+    for (uint32_t i = lane(); i < 257 * kHistCopies; i += 64) hall[i] = 0;
+    wave_fence();
     if (td.cold) hist_slab<true>(a, td, tau, sl, hall);
     else hist_slab<false>(a, td, tau, sl, hall);
 }
@@ -577,20 +587,27 @@ __device__ __forceinline__ Code walk_next(const CodeArgs &a, Walk &w, uint64_t i
     return code_of(a, gap, (uint32_t)(v >> 32), w.gr.exponent, w.gr.rice);
 }
 
+// Exclusive sum over a 256-thread workgroup (4 wavefronts): wavefront scans by shuffles, then the
+// 4 wavefront totals through `sh` (at least 4 entries).  *total receives the workgroup's sum.
 __device__ unsigned long long block_exclusive_sum(unsigned long long v, unsigned long long *sh, unsigned long long *total) {
-    const uint32_t tid = threadIdx.x;
-    sh[tid] = v;
-    __syncthreads();
-    for (uint32_t off = 1; off < 256; off <<= 1) {
-        unsigned long long x = tid >= off ? sh[tid - off] : 0ULL;
-        __syncthreads();
-        sh[tid] += x;
-        __syncthreads();
+    const uint32_t ln = lane(), w = threadIdx.x >> 6;
+    unsigned long long incl = v;
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long t = __shfl_up(incl, o, 64);
+        if (ln >= (uint32_t)o) incl += t;
     }
-    const unsigned long long incl = sh[tid];
-    *total = sh[255];
+    if (ln == 63) sh[w] = incl;
     __syncthreads();
-    return incl - v;
+    unsigned long long before = 0, tot = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+        const unsigned long long x = sh[q];
+        if (q < w) before += x;
+        tot += x;
+    }
+    __syncthreads();  // sh may be reused by the caller
+    *total = tot;
+    return before + incl - v;
 }
 
 __global__ __launch_bounds__(256) void k_code_lengths(CodeArgs a) {
@@ -675,31 +692,65 @@ __global__ __launch_bounds__(256) void k_block_bits(const unsigned long long *bs
 }
 
 // ================================================================== generic scans and sums
-// Exclusive prefix sums of n values with one workgroup; out[n] = total.
+// Exclusive prefix sums, out[i] = in[0] + ... + in[i-1] and out[n] = total, in three coalesced
+// passes: per-chunk sums, a scan of the chunk sums (one workgroup), then the chunks themselves.
+constexpr uint32_t kScanChunk = 4096;  // elements per workgroup: 256 threads x 16
+
 template <typename T>
-__global__ __launch_bounds__(1024) void k_scan1(const T *in, uint64_t n, unsigned long long *out) {
-    __shared__ unsigned long long part[1024];
-    const uint32_t tid = threadIdx.x;
-    const uint64_t per = (n + 1023) / 1024;
-    const uint64_t b = min((uint64_t)tid * per, n), e = min(b + per, n);
+__global__ __launch_bounds__(256) void k_scan_reduce(const T *in, uint64_t n, unsigned long long *part) {
+    __shared__ unsigned long long sh[4];
+    const uint64_t b = (uint64_t)blockIdx.x * kScanChunk;
     unsigned long long s = 0;
-    for (uint64_t i = b; i < e; ++i) s += in[i];
-    part[tid] = s;
-    __syncthreads();
-    for (uint32_t off = 1; off < 1024; off <<= 1) {
-        unsigned long long v = tid >= off ? part[tid - off] : 0ULL;
-        __syncthreads();
-        part[tid] += v;
-        __syncthreads();
+    for (uint32_t j = threadIdx.x; j < kScanChunk; j += 256)
+        if (b + j < n) s += in[b + j];
+    unsigned long long tot;
+    block_exclusive_sum(s, sh, &tot);
+    if (threadIdx.x == 0) part[blockIdx.x] = tot;
+}
+
+// part[0..m) -> exclusive prefix in place, part[m] = total
+__global__ __launch_bounds__(256) void k_scan_parts(unsigned long long *part, uint64_t m) {
+    __shared__ unsigned long long sh[4];
+    unsigned long long carry = 0;
+    for (uint64_t base = 0; base < m; base += 256) {
+        const uint64_t i = base + threadIdx.x;
+        const unsigned long long v = i < m ? part[i] : 0ULL;
+        unsigned long long tot;
+        const unsigned long long ex = block_exclusive_sum(v, sh, &tot);
+        if (i < m) part[i] = carry + ex;
+        carry += tot;
     }
-    unsigned long long run = part[tid] - s;
-    for (uint64_t i = b; i < e; ++i) {
-        const unsigned long long v = in[i];
-        out[i] = run;
+    if (threadIdx.x == 0) part[m] = carry;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_scan_down(const T *in, uint64_t n, const unsigned long long *part,
+                                                  unsigned long long *out) {
+    __shared__ unsigned long long buf[kScanChunk + kScanChunk / 16];  // element j at j + j / 16
+    __shared__ unsigned long long sh[4];
+    const uint32_t tid = threadIdx.x;
+    const uint64_t b = (uint64_t)blockIdx.x * kScanChunk;
+    for (uint32_t j = tid; j < kScanChunk; j += 256) buf[j + (j >> 4)] = b + j < n ? (unsigned long long)in[b + j] : 0ULL;
+    __syncthreads();
+    unsigned long long *mine = buf + tid * 17;  // this thread's 16 consecutive elements
+    unsigned long long s = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) s += mine[k];
+    unsigned long long tot;
+    unsigned long long run = part[blockIdx.x] + block_exclusive_sum(s, sh, &tot);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const unsigned long long v = mine[k];
+        mine[k] = run;
         run += v;
     }
-    if (tid == 1023) out[n] = part[1023];
+    __syncthreads();
+    for (uint32_t j = tid; j < kScanChunk; j += 256)
+        if (b + j < n) out[b + j] = buf[j + (j >> 4)];
+    if (blockIdx.x == gridDim.x - 1 && tid == 0) out[n] = part[gridDim.x];
 }
+
+__global__ void k_scan_empty(unsigned long long *out) { out[0] = 0; }
 
 __global__ __launch_bounds__(256) void k_tensor_sums(const TensorDesc *descs, const uint64_t *per_tile, uint64_t *out) {
     __shared__ unsigned long long sh[256];
@@ -736,80 +787,145 @@ __global__ __launch_bounds__(256) void k_checksum(const uint32_t *frame, uint32_
 // block end or the group's bound q_max), a zero, `rice` remainder bits, then the canonical Huffman
 // code found by length with the first/count/base tables (codec.py:434-454).  Bits past the payload
 // read as zero.  Any violation raises the shared `bad` flag; nothing here can read out of bounds.
-__device__ __forceinline__ uint64_t read64(const uint64_t *p, uint64_t nw, uint64_t pos) {
-    const uint64_t w = pos >> 6;
+// ================================================================== apply: block decode
+// One lane per 256-change block (codec.py:504-575), 64 consecutive blocks per wavefront.  The
+// wavefront's payload bits (contiguous: blocks are stored in order) are staged in LDS as
+// host-order 64-bit words, and so are the decoding symbols when they fit; every change then costs
+// two LDS reads of the stream and one of the symbol.  Code lengths come from comparisons of the
+// 17-bit peek with the canonical limits held in registers.  Outputs are staged per 16 changes and
+// written as 64-byte runs per block.
+constexpr uint32_t kDecPayWords = 4096;  // 32 KiB of payload per wavefront; more is read from HBM
+constexpr uint32_t kDecStage = 16;
+
+struct DecodeLds {
+    uint64_t pay[kDecPayWords];
+    uint32_t syms[kDecSyms];
+    uint32_t zz[64][kDecStage + 1];
+    uint32_t loc[64][kDecStage + 1];
+    uint32_t cnt[64];
+    unsigned long long eb[64];
+};
+
+// 64 bits of the stream from bit `pos`: LDS words [w0, ...) when staged, else HBM.
+template <bool LDS>
+__device__ __forceinline__ uint64_t bits64(const DecodeArgs &a, const uint64_t *W, uint64_t w0, uint64_t pos) {
     const uint32_t s = (uint32_t)(pos & 63);
-    const uint64_t hi = w < nw ? __builtin_bswap64(p[w]) : 0ULL;
-    const uint64_t lo = w + 1 < nw ? __builtin_bswap64(p[w + 1]) : 0ULL;
+    uint64_t hi, lo;
+    if (LDS) {
+        const uint32_t w = (uint32_t)min<uint64_t>((pos >> 6) - w0, kDecPayWords - 2);
+        hi = W[w];
+        lo = W[w + 1];
+    } else {
+        const uint64_t w = pos >> 6;
+        hi = w < a.n_words ? __builtin_bswap64(a.payload[w]) : 0ULL;
+        lo = w + 1 < a.n_words ? __builtin_bswap64(a.payload[w + 1]) : 0ULL;
+    }
     return s ? (hi << s) | (lo >> (64 - s)) : hi;
 }
 
-__global__ __launch_bounds__(64) void k_decode(DecodeArgs a) {
-    const uint64_t b = (uint64_t)blockIdx.x * 64 + threadIdx.x;
-    if (b >= a.n_blocks) return;
-    const uint32_t g = group_of_block(a.groups, a.n_groups, b);
-    const GroupDev gr = a.groups[g];
-    const uint64_t kb = b - gr.blk_base;
-    const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
-    const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
-    const uint64_t size = a.sizes[(uint64_t)gr.tensor * 256 + gr.exponent];
-    const uint32_t rice = gr.rice;
-    const uint64_t qmax = size >> rice;
-    const uint32_t *first = a.tab + (uint64_t)gr.table * 54, *count = first + 18, *base = first + 36;
-    uint64_t cur = a.block_off[b];
-    const uint64_t end = cur + a.block_bits[b];
-    bool bad = kb == 0 && gr.count > size;  // a group with more changes than elements
-    uint64_t rel = 0;                         // sum of (gap + 1) so far in this block
-    for (uint32_t s = 0; s < cnt && !bad; ++s) {
-        if (cur >= end) {
-            bad = true;
-            break;
+template <bool LDS_PAY, bool LDS_SYMS>
+__device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
+    const uint32_t ln = lane();
+    const uint64_t b = (uint64_t)blockIdx.x * 64 + ln;
+    uint32_t cnt = 0, rice = 0, lim[17], off[17];
+    uint64_t eb = 0, size = 0, qmax = 0, cur = 0, end = 0;
+    bool bad = false;
+    if (b < a.n_blocks) {
+        const uint32_t g = group_of_block(a.groups, a.n_groups, b);
+        const GroupDev gr = a.groups[g];
+        const uint64_t kb = b - gr.blk_base;
+        cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
+        eb = (uint64_t)gr.elem_base + kb * 256;
+        size = a.sizes[(uint64_t)gr.tensor * 256 + gr.exponent];
+        rice = gr.rice;
+        qmax = size >> rice;
+        cur = a.block_off[b];
+        end = cur + a.block_bits[b];
+        bad = kb == 0 && gr.count > size;  // a group with more changes than elements
+#pragma unroll
+        for (int l = 0; l < 17; ++l) {
+            lim[l] = a.lim[(uint64_t)gr.table * 17 + l];
+            off[l] = a.off[(uint64_t)gr.table * 17 + l];
         }
-        uint64_t q = 0;
-        for (;;) {
-            const uint64_t y = ~read64(a.payload, a.n_words, cur + q);
-            if (y) {
-                q += (uint64_t)__builtin_clzll(y);
-                break;
-            }
-            q += 64;
-            if (q > qmax || cur + q >= end) break;
-        }
-        if (q > qmax || cur + q >= end) {
-            bad = true;
-            break;
-        }
-        const uint64_t c = cur + q + 1;
-        const uint64_t x = read64(a.payload, a.n_words, c);
-        const uint64_t rem = rice ? x >> (64 - rice) : 0ULL;
-        const uint32_t peek = (uint32_t)((x << rice) >> (64 - 17));
-        uint32_t L = 0, idx = 0;
-        for (uint32_t l = 1; l <= 17; ++l) {
-            const uint32_t code = peek >> (17 - l);
-            const uint32_t d = code - first[l];
-            if (d < count[l]) {
-                L = l;
-                idx = base[l] + d;
-                break;
-            }
-        }
-        if (!L) {
-            bad = true;
-            break;
-        }
-        const uint64_t gap = (q << rice) | rem;
-        if (gap >= size) {
-            bad = true;
-            break;
-        }
-        rel += gap + 1;
-        a.zz[eb + s] = a.syms[min(idx, a.n_syms - 1)];
-        a.local[eb + s] = (uint32_t)min<uint64_t>(rel - 1, 0xFFFFFFFFULL);
-        cur = c + rice + L;
+    } else {
+#pragma unroll
+        for (int l = 0; l < 17; ++l) lim[l] = off[l] = 0;
     }
-    if (!bad && cur != end) bad = true;
-    a.blk_sum[b] = rel;
-    if (bad) atomicOr(a.bad, kBadDecode);
+    S.cnt[ln] = cnt;
+    S.eb[ln] = eb;
+    uint64_t rel = 0;  // sum of (gap + 1) so far in this block
+    for (uint32_t s = 0; s < 256; ++s) {  // the same trip count on every lane: flushes are wave-wide
+        if (s < cnt && !bad) {
+            uint64_t q = 0;
+            for (;;) {
+                const uint64_t y = ~bits64<LDS_PAY>(a, S.pay, w0, cur + q);
+                if (y) {
+                    q += (uint64_t)__builtin_clzll(y);
+                    break;
+                }
+                q += 64;
+                if (q > qmax || cur + q >= end) break;
+            }
+            const uint64_t c = cur + q + 1;
+            const uint64_t x = bits64<LDS_PAY>(a, S.pay, w0, c);
+            const uint64_t rem = rice ? x >> (64 - rice) : 0ULL;
+            const uint32_t peek = (uint32_t)((x << rice) >> (64 - 17));
+            uint32_t L = 1, o = 0;
+#pragma unroll
+            for (int l = 0; l < 17; ++l) L += lim[l] <= peek ? 1u : 0u;  // lim is non-decreasing
+#pragma unroll
+            for (int l = 0; l < 17; ++l) o = L == (uint32_t)(l + 1) ? off[l] : o;
+            const uint32_t idx = o + (L <= 17 ? peek >> (17 - L) : 0u);
+            const uint64_t gap = (q << rice) | rem;
+            if (q > qmax || cur + q >= end || L > 17 || gap >= size) {
+                bad = true;
+            } else {
+                rel += gap + 1;
+                const uint32_t si = min(idx, a.n_syms - 1);
+                S.zz[ln][s & (kDecStage - 1)] = LDS_SYMS ? S.syms[si] : a.syms[si];
+                S.loc[ln][s & (kDecStage - 1)] = (uint32_t)min<uint64_t>(rel - 1, 0xFFFFFFFFULL);
+                cur = c + rice + L;
+            }
+        }
+        if ((s & (kDecStage - 1)) == kDecStage - 1) {  // write 16 changes of every block: 4 blocks per store
+            wave_fence();
+            const uint32_t s0 = s + 1 - kDecStage, e = ln & (kDecStage - 1);
+#pragma unroll 4
+            for (uint32_t i = 0; i < 64; i += 4) {
+                const uint32_t blk = i + (ln >> 4);
+                if (s0 + e < S.cnt[blk]) {
+                    const uint64_t j = S.eb[blk] + s0 + e;
+                    a.zz[j] = S.zz[blk][e];
+                    a.local[j] = S.loc[blk][e];
+                }
+            }
+            wave_fence();
+        }
+    }
+    if (b < a.n_blocks) {
+        if (!bad && cur != end) bad = true;
+        a.blk_sum[b] = rel;
+        if (bad) atomicOr(a.bad, kBadDecode);
+    }
+}
+
+template <bool LDS_SYMS>
+__global__ __launch_bounds__(64) void k_decode(DecodeArgs a) {
+    __shared__ __attribute__((aligned(16))) DecodeLds S;
+    const uint32_t ln = lane();
+    const uint64_t b0 = (uint64_t)blockIdx.x * 64;
+    const uint64_t nb = min<uint64_t>(64, a.n_blocks - b0);
+    // this wavefront's bits [block_off[b0], block_off[b0 + nb]) lie in words [w0, wend)
+    const uint64_t w0 = a.block_off[b0] >> 6;
+    const uint64_t wend = min<uint64_t>(a.n_words, ((a.block_off[b0 + nb] + 63) >> 6) + 2);
+    const bool lds_pay = wend > w0 && wend - w0 <= kDecPayWords;
+    if (lds_pay)
+        for (uint64_t w = w0 + ln; w < wend; w += 64) S.pay[w - w0] = __builtin_bswap64(a.payload[w]);
+    if (LDS_SYMS)
+        for (uint32_t i = ln; i < a.n_syms; i += 64) S.syms[i] = a.syms[i];
+    wave_fence();
+    if (lds_pay) decode_blocks<true, LDS_SYMS>(a, S, w0);
+    else decode_blocks<false, LDS_SYMS>(a, S, w0);
 }
 
 // local = (sum of (gap + 1) over earlier blocks of the group) + block-relative local; must stay
@@ -950,12 +1066,11 @@ __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Sla
     });
 }
 
-// W == kWin: slabs whose target exponents lie within kWin consecutive values; W == 256: the others.
+// W == kWin: slabs whose target exponents lie within kWin consecutive values (the others are
+// listed for the W == 256 kernel); W == 256: a listed slab.
 template <uint32_t W>
-__global__ __launch_bounds__(64) void k_select(SelectArgs a) {
-    __shared__ __attribute__((aligned(16))) SelectLds<W> S;
-    if (*a.bad) return;
-    const uint32_t tau = blockIdx.x, ln = lane();
+__device__ void select_tile(const SelectArgs &a, uint32_t tau, SelectLds<W> &S) {
+    const uint32_t ln = lane();
     const uint32_t t = a.tile_tensor[tau];
     const TensorDesc td = a.descs[t];
     int32_t g4[4];
@@ -994,8 +1109,11 @@ __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
         klo = min(klo, (uint32_t)__shfl_xor(klo, o, 64));
         khi = max(khi, (uint32_t)__shfl_xor(khi, o, 64));
     }
-    if (klo > khi) return;                       // no targets in this slab
-    if ((khi - klo < kWin) != (W == kWin)) return;  // the other kernel's slab
+    if (klo > khi) return;  // no targets in this slab
+    if (W == kWin && khi - klo >= kWin) {
+        if (ln == 0) a.wide[atomicAdd(a.n_wide, 1u)] = tau;
+        return;
+    }
     const uint32_t kbase = W == kWin ? klo : 0;
 
     uint32_t incl = mine;  // inclusive scan of per-lane totals across the wave
@@ -1073,6 +1191,23 @@ __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
     const Slab sl = slab_of(td, local_tile, a.slab);
     if (in_lds) select_slab<W, true>(a, td, sl, kbase, S);
     else select_slab<W, false>(a, td, sl, kbase, S);
+}
+
+__global__ __launch_bounds__(64) void k_select(SelectArgs a) {
+    __shared__ __attribute__((aligned(16))) SelectLds<kWin> S;
+    if (*a.bad) return;
+    select_tile<kWin>(a, blockIdx.x, S);
+}
+
+// The slabs k_select listed; a fixed grid walks the list.
+__global__ __launch_bounds__(64) void k_select_wide(SelectArgs a) {
+    __shared__ __attribute__((aligned(16))) SelectLds<256> S;
+    if (*a.bad) return;
+    const uint32_t n = *a.n_wide;
+    for (uint32_t i = blockIdx.x; i < n; i += gridDim.x) {
+        select_tile<256>(a, a.wide[i], S);
+        wave_fence();
+    }
 }
 
 // new = (old + unzigzag(zz)) mod 2^16; checksum delta per tensor (codec.py:698-700).
@@ -1179,12 +1314,28 @@ void launch_block_bits(const unsigned long long *bstart, uint64_t n_blocks, uint
     CRX_LAUNCH("block_bits", k_block_bits, grid1(n_blocks, 256), 256, s, bstart, n_blocks, out, overflow);
 }
 
-void launch_scan_u64(const unsigned long long *in, uint64_t n, unsigned long long *out, hipStream_t s) {
-    CRX_LAUNCH("scan_u64", k_scan1<unsigned long long>, 1, 1024, s, in, n, out);
+uint64_t scan_parts(uint64_t n) { return (n + kScanChunk - 1) / kScanChunk + 1; }
+
+template <typename T>
+static void launch_scan(const char *name, const T *in, uint64_t n, unsigned long long *out, unsigned long long *part,
+                        hipStream_t s) {
+    if (!n) {
+        CRX_LAUNCH(name, k_scan_empty, 1, 1, s, out);
+        return;
+    }
+    const uint64_t m = (n + kScanChunk - 1) / kScanChunk;
+    CRX_LAUNCH(name, k_scan_reduce<T>, (uint32_t)m, 256, s, in, n, part);
+    CRX_LAUNCH(name, k_scan_parts, 1, 256, s, part, m);
+    CRX_LAUNCH(name, k_scan_down<T>, (uint32_t)m, 256, s, in, n, part, out);
 }
 
-void launch_scan_u32(const uint32_t *in, uint64_t n, unsigned long long *out, hipStream_t s) {
-    CRX_LAUNCH("scan_u32", k_scan1<uint32_t>, 1, 1024, s, in, n, out);
+void launch_scan_u64(const unsigned long long *in, uint64_t n, unsigned long long *out, unsigned long long *part,
+                     hipStream_t s) {
+    launch_scan("scan_u64", in, n, out, part, s);
+}
+
+void launch_scan_u32(const uint32_t *in, uint64_t n, unsigned long long *out, unsigned long long *part, hipStream_t s) {
+    launch_scan("scan_u32", in, n, out, part, s);
 }
 
 void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint64_t *per_tile, uint64_t *out,
@@ -1192,7 +1343,10 @@ void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint6
     CRX_LAUNCH("tensor_sums", k_tensor_sums, n_tensors, 256, s, descs, per_tile, out);
 }
 
-void launch_decode(const DecodeArgs &a, hipStream_t s) { CRX_LAUNCH("decode", k_decode, grid1(a.n_blocks, 64), 64, s, a); }
+void launch_decode(const DecodeArgs &a, hipStream_t s) {
+    if (a.n_syms <= kDecSyms) CRX_LAUNCH("decode", k_decode<true>, grid1(a.n_blocks, 64), 64, s, a);
+    else CRX_LAUNCH("decode", k_decode<false>, grid1(a.n_blocks, 64), 64, s, a);
+}
 
 void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
     CRX_LAUNCH("local_fix", k_local_fix, (uint32_t)n_blocks, 256, s, a);
@@ -1201,8 +1355,8 @@ void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
 void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("locate", k_locate, tiles, 256, s, a); }
 
 void launch_select(const SelectArgs &a, uint32_t tiles, hipStream_t s) {
-    CRX_LAUNCH("select", k_select<kWin>, tiles, 64, s, a);
-    CRX_LAUNCH("select_wide", k_select<256>, tiles, 64, s, a);
+    CRX_LAUNCH("select", k_select, tiles, 64, s, a);
+    CRX_LAUNCH("select_wide", k_select_wide, min(tiles, 2048u), 64, s, a);
 }
 
 void launch_verify(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
