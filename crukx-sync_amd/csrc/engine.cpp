@@ -294,6 +294,9 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
 
     uint64_t *sorted = ar.get<uint64_t>(C);
     launch_place(chunks, (uint32_t)h[1], rec, sd.tile_tensor, hall, hchg, gbase, sorted, C, s);
+    const uint64_t n_thr = (C + kElemsPerThread - 1) / kElemsPerThread;  // threads of the walking kernels
+    uint32_t *cmap = ar.get<uint32_t>(n_thr);
+    launch_chunk_map(d_groups, (uint32_t)G, cmap, s);
     launch_r0(d_groups, (uint32_t)G, sorted, s);
     uint32_t *dense = ar.get<uint32_t>(256 * kDense);
     uint32_t *rare = ar.get<uint32_t>(C);
@@ -303,7 +306,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     zero(dense, 256 * kDense, s);
     zero(scnt, 2, s);
     zero(cost, G * 3, s);
-    StatsArgs st{sorted, C, d_groups, (uint32_t)G, dense, rare, C, scnt, cost};
+    StatsArgs st{sorted, C, d_groups, (uint32_t)G, cmap, dense, rare, C, scnt, cost};
     launch_stats(st, s);
     launch_tensor_sums(d_descs, T, delta, t_delta, s);
     launch_tensor_sums(d_descs, T, full, t_full, s);
@@ -392,13 +395,13 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     h2d(d_lut, lut.data(), lut.size(), s);
     h2d(d_rk, rkeys.data(), rkeys.size(), s);
     h2d(d_rv, rvals.data(), rvals.size(), s);
-    const uint64_t n_wg = (C + kElemsPerWG - 1) / kElemsPerWG;
-    unsigned long long *wsum = ar.get<unsigned long long>(n_wg), *woff = ar.get<unsigned long long>(n_wg + 1);
-    CodeArgs ca{sorted, C, d_groups2, (uint32_t)G, d_lut, d_rk, d_rv, (uint32_t)rkeys.size(), wsum, woff, nullptr, nullptr};
+    unsigned long long *tsum = ar.get<unsigned long long>(n_thr), *toff = ar.get<unsigned long long>(n_thr + 1);
+    CodeArgs ca{sorted, C, d_groups2, (uint32_t)G, d_lut, d_rk, d_rv, (uint32_t)rkeys.size(), cmap, tsum, toff,
+                nullptr, nullptr};
     launch_code_lengths(ca, s);
-    launch_scan_u64(wsum, n_wg, woff, ar.get<unsigned long long>(scan_parts(n_wg)), s);
+    launch_scan_u64(tsum, n_thr, toff, ar.get<unsigned long long>(scan_parts(n_thr)), s);
     unsigned long long total_bits = 0;
-    d2h(&total_bits, woff + n_wg, 1, s);
+    d2h(&total_bits, toff + n_thr, 1, s);
     sync(s);
 
     const uint64_t n_words = (total_bits + 31) / 32 + 4;
@@ -408,7 +411,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     unsigned int *ovf = ar.get<unsigned int>(1);
     zero(words, n_words, s);
     zero(ovf, 1, s);
-    HIP_OK(hipMemcpyAsync(bstart + B, woff + n_wg, sizeof(unsigned long long), hipMemcpyDeviceToDevice, s));
+    HIP_OK(hipMemcpyAsync(bstart + B, toff + n_thr, sizeof(unsigned long long), hipMemcpyDeviceToDevice, s));
     ca.words = words;
     ca.bstart = bstart;
     launch_pack(ca, s);
@@ -504,6 +507,8 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     uint64_t *pay = ar.get<uint64_t>(pay_words);
     h2d(d_groups, groups.data(), G, s);
     h2d(d_gof, group_of.data(), group_of.size(), s);
+    uint32_t *bmap = ar.get<uint32_t>(B);
+    launch_block_map(d_groups, (uint32_t)G, bmap, s);
     h2d(d_lim, lim.data(), lim.size(), s);
     h2d(d_off, off.data(), off.size(), s);
     h2d(d_syms, syms.data(), syms.size(), s);
@@ -531,11 +536,11 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     uint32_t *lb = ar.get<uint32_t>((uint64_t)(tiles + 1) * 256);  // row tiles: read, never used
     zero(bad, 1, s);
     zero(tdelta, T, s);
-    DecodeArgs da{pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, sizes, d_lim, d_off, d_syms, (uint32_t)syms.size(),
+    DecodeArgs da{pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, bmap, sizes, d_lim, d_off, d_syms, (uint32_t)syms.size(),
                   zz, local, blk_sum, bad};
     launch_decode(da, s);
     launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), s);
-    BlockArgs ba{d_groups, (uint32_t)G, d_descs, sizes, blk_prefix, local, zz, pv, tdelta, bad};
+    BlockArgs ba{d_groups, (uint32_t)G, bmap, d_descs, sizes, blk_prefix, local, zz, pv, tdelta, bad};
     launch_local_fix(ba, B, s);
     uint32_t *wide = ar.get<uint32_t>(tiles);
     unsigned int *n_wide = ar.get<unsigned int>(1);

@@ -84,6 +84,7 @@ struct StatsArgs {
     uint64_t n;
     const GroupDev *groups;
     uint32_t n_groups;
+    const uint32_t *cmap;           // [n / kElemsPerThread] group of every thread's first change
     uint32_t *dense;                // [256][kDense]
     uint32_t *rare;                 // (exponent << 17) | zz for zz >= kDense
     uint64_t rare_cap;
@@ -100,8 +101,9 @@ struct CodeArgs {
     const uint32_t *rare_keys;      // sorted (exponent << 17) | zz
     const uint32_t *rare_vals;
     uint32_t n_rare;
-    unsigned long long *wsum;       // [workgroups] bits per workgroup
-    const unsigned long long *woff; // [workgroups] exclusive bit offsets
+    const uint32_t *cmap;           // [n / kElemsPerThread] group of every thread's first change
+    unsigned long long *tsum;       // [threads] bits per thread (kElemsPerThread changes)
+    const unsigned long long *toff; // [threads] exclusive bit offsets
     uint32_t *words;                // payload as big-endian bytes in 32-bit words
     unsigned long long *bstart;     // [blocks + 1] bit offset of each block
 };
@@ -114,6 +116,7 @@ struct DecodeArgs {
     uint64_t n_blocks;
     const GroupDev *groups;
     uint32_t n_groups;
+    const uint32_t *bmap;           // [blocks] group of every block
     const uint32_t *sizes;          // [tensor][256] group sizes of the receiver
     const uint32_t *lim;            // [tables][17]: end of length l's codes, left-justified to 17 bits
     const uint32_t *off;            // [tables][17]: symbol index of code 0 of length l (mod 2^32)
@@ -143,6 +146,7 @@ struct SelectArgs {
 struct BlockArgs {                  // per-block kernels over the change list (one workgroup per block)
     const GroupDev *groups;
     uint32_t n_groups;
+    const uint32_t *bmap;           // [blocks] group of every block
     const TensorDesc *descs;
     const uint32_t *sizes;
     const unsigned long long *blk_prefix;
@@ -165,6 +169,9 @@ void launch_place(const Chunk *chunks, uint32_t n_chunks, const uint64_t *rec, c
 void launch_r0(GroupDev *groups, uint32_t n_groups, const uint64_t *sorted, hipStream_t s);
 void launch_stats(const StatsArgs &a, hipStream_t s);
 void launch_code_lengths(const CodeArgs &a, hipStream_t s);
+// cmap[c] = group of change kElemsPerThread * c; bmap[b] = group of block b
+void launch_chunk_map(const GroupDev *groups, uint32_t n_groups, uint32_t *cmap, hipStream_t s);
+void launch_block_map(const GroupDev *groups, uint32_t n_groups, uint32_t *bmap, hipStream_t s);
 void launch_pack(const CodeArgs &a, hipStream_t s);
 void launch_block_bits(const unsigned long long *bstart, uint64_t n_blocks, uint32_t *out, unsigned int *overflow,
                        hipStream_t s);

@@ -51,6 +51,20 @@ __global__ __launch_bounds__(256) void k_tile_map(const TensorDesc *descs, uint3
     for (uint32_t i = threadIdx.x; i < d.n_tiles; i += 256) tile_tensor[d.tile_begin + i] = blockIdx.x;
 }
 
+// One workgroup per group: the group of every kElemsPerThread-th change and of every block.
+__global__ __launch_bounds__(256) void k_chunk_map(const GroupDev *groups, uint32_t *cmap) {
+    const GroupDev g = groups[blockIdx.x];
+    const uint64_t c0 = ((uint64_t)g.elem_base + kElemsPerThread - 1) / kElemsPerThread;
+    const uint64_t c1 = ((uint64_t)g.elem_base + g.count + kElemsPerThread - 1) / kElemsPerThread;
+    for (uint64_t c = c0 + threadIdx.x; c < c1; c += 256) cmap[c] = blockIdx.x;
+}
+
+__global__ __launch_bounds__(256) void k_block_map(const GroupDev *groups, uint32_t *bmap) {
+    const GroupDev g = groups[blockIdx.x];
+    const uint32_t nb = (g.count + 255) / 256;
+    for (uint32_t i = threadIdx.x; i < nb; i += 256) bmap[g.blk_base + i] = blockIdx.x;
+}
+
 // last group whose first change is <= i
 __device__ uint32_t group_of_elem(const GroupDev *g, uint32_t n, uint64_t i) {
     uint32_t lo = 0, hi = n;
@@ -438,6 +452,24 @@ __global__ __launch_bounds__(256) void k_r0(GroupDev *groups, uint32_t n_groups,
     groups[g].r0 = r0;
 }
 
+// Records of a workgroup's changes in LDS: thread t's kElemsPerThread records at t * kRecPad (the pad
+// spreads one wavefront's reads of its threads' k-th records over the banks).
+constexpr uint32_t kRecPad = kElemsPerThread + 1;
+
+__device__ __forceinline__ void stage_records(const uint64_t *sorted, uint64_t n, uint64_t wbase, uint64_t *rec) {
+    for (uint32_t j = threadIdx.x; j < (uint32_t)kElemsPerWG; j += 256) {
+        const uint64_t i = wbase + j;
+        rec[(j / kElemsPerThread) * kRecPad + (j % kElemsPerThread)] = i < n ? sorted[i] : 0ULL;
+    }
+    __syncthreads();
+}
+
+// group-local index of the change before this thread's first one (0 if it starts its group)
+__device__ __forceinline__ uint64_t prev_index(const uint64_t *sorted, const uint64_t *rec, uint64_t ib, uint32_t elem_base) {
+    if (ib <= elem_base) return 0;
+    return (uint32_t)(threadIdx.x ? rec[(threadIdx.x - 1) * kRecPad + kElemsPerThread - 1] : sorted[ib - 1]);
+}
+
 __device__ __forceinline__ void rice_cands(uint32_t r0, uint32_t c[3]) {
     c[0] = r0 ? r0 - 1 : 0;
     c[1] = r0;
@@ -450,21 +482,20 @@ __device__ __forceinline__ void rice_cands(uint32_t r0, uint32_t c[3]) {
 __global__ __launch_bounds__(256) void k_stats(StatsArgs a) {
     __shared__ uint32_t lhist[kLocalGroups * kDense];
     __shared__ unsigned long long lcost[kLocalGroups * 3];
-    __shared__ uint32_t s_gfirst;
+    __shared__ uint64_t rec[256 * kRecPad];
     const uint32_t tid = threadIdx.x;
     const uint64_t wbase = (uint64_t)blockIdx.x * kElemsPerWG;
     for (uint32_t x = tid; x < kLocalGroups * kDense; x += 256) lhist[x] = 0;
     for (uint32_t x = tid; x < kLocalGroups * 3; x += 256) lcost[x] = 0;
-    if (tid == 0) s_gfirst = group_of_elem(a.groups, a.n_groups, wbase);
-    __syncthreads();
-    const uint32_t gf = s_gfirst;
+    stage_records(a.sorted, a.n, wbase, rec);
+    const uint32_t gf = a.cmap[wbase / kElemsPerThread];
     const uint64_t ib = wbase + (uint64_t)tid * kElemsPerThread;
     const bool any = ib < a.n;
-    uint32_t g = any ? group_of_elem(a.groups, a.n_groups, ib) : 0;
+    uint32_t g = any ? a.cmap[ib / kElemsPerThread] : 0;
     GroupDev gr = a.groups[g];
     uint32_t c[3];
     rice_cands(gr.r0, c);
-    uint64_t prev = (any && ib > gr.elem_base) ? (uint32_t)a.sorted[ib - 1] : 0;
+    uint64_t prev = any ? prev_index(a.sorted, rec, ib, gr.elem_base) : 0;
     unsigned long long s0 = 0, s1 = 0, s2 = 0;
     auto flush_cost = [&](uint32_t gg) {
         if (!(s0 | s1 | s2)) return;
@@ -490,7 +521,7 @@ __global__ __launch_bounds__(256) void k_stats(StatsArgs a) {
                 gr = a.groups[++g];
                 rice_cands(gr.r0, c);
             }
-            const uint64_t v = a.sorted[i];
+            const uint64_t v = rec[tid * kRecPad + k];
             const uint64_t gidx = (uint32_t)v;
             zz = (uint32_t)(v >> 32);
             e = gr.exponent;
@@ -532,59 +563,68 @@ __global__ __launch_bounds__(256) void k_stats(StatsArgs a) {
 }
 
 // ================================================================== encode: code lengths and packing
-struct Code {
-    uint64_t len;   // total bits
-    uint64_t q;     // unary run
-    uint32_t rice, hl, hc;
-    uint64_t gap;
+// The change-order kernels give each thread kElemsPerThread consecutive changes.  A workgroup's
+// records are first staged in LDS with coalesced loads (thread t's records at t * kRecPad: the pad
+// spreads one wavefront's reads of its threads' k-th records over the banks); each thread then walks
+// its records from LDS and issues its table lookups together.
+// A thread's codes: gap, key = exponent << 22 | rice << 17 | zz, the Huffman entry and, when the
+// change opens a block, the block index.
+struct ThreadCodes {
+    uint64_t gap[kElemsPerThread];
+    uint32_t key[kElemsPerThread];
+    uint32_t hv[kElemsPerThread];   // (code << 5) | length
+    uint32_t blk[kElemsPerThread];  // block opened by the change, else kNone
+    uint32_t n;
 };
 
-__device__ __forceinline__ Code code_of(const CodeArgs &a, uint64_t gap, uint32_t zz, uint32_t e, uint32_t rice) {
-    uint32_t v;
-    if (zz < kDense) {
-        v = a.lut[e * kDense + zz];
-    } else {
-        const uint32_t key = (e << 17) | zz;
-        uint32_t lo = 0, hi = a.n_rare;
-        while (lo < hi) {
-            uint32_t mid = (lo + hi) >> 1;
-            if (a.rare_keys[mid] < key) lo = mid + 1;
-            else hi = mid;
-        }
-        v = lo < a.n_rare ? a.rare_vals[lo] : 0u;
+__device__ __forceinline__ uint32_t huff_entry(const CodeArgs &a, uint32_t e, uint32_t zz) {
+    if (zz < kDense) return a.lut[e * kDense + zz];
+    const uint32_t key = (e << 17) | zz;
+    uint32_t lo = 0, hi = a.n_rare;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (a.rare_keys[mid] < key) lo = mid + 1;
+        else hi = mid;
     }
-    Code c;
-    c.gap = gap;
-    c.rice = rice;
-    c.q = gap >> rice;
-    c.hl = v & 31;
-    c.hc = v >> 5;
-    c.len = c.q + 1 + rice + c.hl;
-    return c;
+    return lo < a.n_rare ? a.rare_vals[lo] : 0u;
 }
 
-// Walks a thread's contiguous changes in update order, tracking the group and the previous index.
-struct Walk {
-    uint32_t g;
-    GroupDev gr;
-    uint64_t prev;
-};
-
-__device__ __forceinline__ Walk walk_start(const CodeArgs &a, uint64_t ib) {
-    Walk w;
-    w.g = group_of_elem(a.groups, a.n_groups, ib);
-    w.gr = a.groups[w.g];
-    w.prev = ib > w.gr.elem_base ? (uint32_t)a.sorted[ib - 1] : 0;
-    return w;
+__device__ void thread_codes(const CodeArgs &a, const uint64_t *rec, uint64_t wbase, ThreadCodes &tc) {
+    const uint32_t t = threadIdx.x;
+    const uint64_t ib = wbase + (uint64_t)t * kElemsPerThread;
+    tc.n = ib < a.n ? (uint32_t)min<uint64_t>(kElemsPerThread, a.n - ib) : 0u;
+    uint32_t g = tc.n ? a.cmap[ib / kElemsPerThread] : 0u;
+    GroupDev gr = a.groups[g];
+    uint64_t gend = (uint64_t)gr.elem_base + gr.count;
+    uint64_t prev = tc.n ? prev_index(a.sorted, rec, ib, gr.elem_base) : 0;
+#pragma unroll
+    for (int k = 0; k < kElemsPerThread; ++k) {
+        const uint64_t i = ib + k;
+        tc.gap[k] = 0;
+        tc.key[k] = 0;
+        tc.blk[k] = kNone;
+        if ((uint32_t)k < tc.n) {
+            while (i >= gend) {
+                gr = a.groups[++g];
+                gend = (uint64_t)gr.elem_base + gr.count;
+            }
+            const uint64_t v = rec[t * kRecPad + k];
+            const uint64_t gidx = (uint32_t)v;
+            tc.gap[k] = i == gr.elem_base ? gidx : gidx - prev - 1;
+            prev = gidx;
+            tc.key[k] = (gr.exponent << 22) | (gr.rice << 17) | (uint32_t)(v >> 32);
+            const uint64_t rel = i - gr.elem_base;
+            if ((rel & 255) == 0) tc.blk[k] = gr.blk_base + (uint32_t)(rel >> 8);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kElemsPerThread; ++k)
+        tc.hv[k] = (uint32_t)k < tc.n ? huff_entry(a, tc.key[k] >> 22, tc.key[k] & 0x1FFFF) : 0u;
 }
 
-__device__ __forceinline__ Code walk_next(const CodeArgs &a, Walk &w, uint64_t i) {
-    while (i >= (uint64_t)w.gr.elem_base + w.gr.count) w.gr = a.groups[++w.g];
-    const uint64_t v = a.sorted[i];
-    const uint64_t gidx = (uint32_t)v;
-    const uint64_t gap = i == w.gr.elem_base ? gidx : gidx - w.prev - 1;
-    w.prev = gidx;
-    return code_of(a, gap, (uint32_t)(v >> 32), w.gr.exponent, w.gr.rice);
+__device__ __forceinline__ uint64_t code_len(const ThreadCodes &tc, int k) {
+    const uint32_t rice = (tc.key[k] >> 17) & 31;
+    return (tc.gap[k] >> rice) + 1 + rice + (tc.hv[k] & 31);
 }
 
 // Exclusive sum over a 256-thread workgroup (4 wavefronts): wavefront scans by shuffles, then the
@@ -611,75 +651,95 @@ __device__ unsigned long long block_exclusive_sum(unsigned long long v, unsigned
 }
 
 __global__ __launch_bounds__(256) void k_code_lengths(CodeArgs a) {
-    __shared__ unsigned long long sh[256];
-    const uint64_t ib = (uint64_t)blockIdx.x * kElemsPerWG + (uint64_t)threadIdx.x * kElemsPerThread;
+    __shared__ uint64_t rec[256 * kRecPad];
+    const uint64_t wbase = (uint64_t)blockIdx.x * kElemsPerWG;
+    stage_records(a.sorted, a.n, wbase, rec);
+    ThreadCodes tc;
+    thread_codes(a, rec, wbase, tc);
+    if (!tc.n) return;
     unsigned long long sum = 0;
-    if (ib < a.n) {
-        Walk w = walk_start(a, ib);
-        for (int k = 0; k < kElemsPerThread && ib + k < a.n; ++k) sum += walk_next(a, w, ib + k).len;
+#pragma unroll
+    for (int k = 0; k < kElemsPerThread; ++k)
+        if ((uint32_t)k < tc.n) sum += code_len(tc, k);
+    a.tsum[(uint64_t)blockIdx.x * 256 + threadIdx.x] = sum;
+}
+
+// A thread's codes fill the contiguous bit range [off, off + its total): words wholly inside the
+// range are written with plain stores; the first word (when the range starts inside it) and the
+// last partial word are shared with the neighbouring threads and are ORed in.  The stream is
+// big-endian bytes in 32-bit words and starts zeroed.
+struct BitWriter {
+    uint32_t *words;
+    uint64_t w;       // next word to write
+    uint64_t acc;     // pending bits, right-aligned
+    uint32_t n;       // number of pending bits (< 32 between calls)
+    bool shared;      // the next word is shared with the previous thread
+
+    __device__ BitWriter(uint32_t *words_, uint64_t off) : words(words_), w(off >> 5), acc(0), n((uint32_t)(off & 31)), shared((off & 31) != 0) {}
+
+    __device__ __forceinline__ void emit(uint32_t v) {
+        if (shared) atomicOr(&words[w], __builtin_bswap32(v));
+        else words[w] = __builtin_bswap32(v);
+        shared = false;
+        ++w;
     }
-    unsigned long long total;
-    block_exclusive_sum(sum, sh, &total);
-    if (threadIdx.x == 0) a.wsum[blockIdx.x] = total;
-}
+    // len <= 32 bits of v (right-aligned, no bits above len)
+    __device__ __forceinline__ void put(uint64_t v, uint32_t len) {
+        acc = (acc << len) | v;
+        n += len;
+        if (n >= 32) {
+            n -= 32;
+            emit((uint32_t)(acc >> n));
+            acc &= (1ULL << n) - 1;
+        }
+    }
+    __device__ void ones(uint64_t q) {
+        for (; q >= 32; q -= 32) put(0xFFFFFFFFULL, 32);
+        if (q) put((1ULL << q) - 1, (uint32_t)q);
+    }
+    __device__ __forceinline__ void finish() {
+        if (n) atomicOr(&words[w], __builtin_bswap32((uint32_t)(acc << (32 - n))));
+    }
+};
 
-// OR `len` (<= 64) bits of `val` (right-aligned) into the big-endian bit stream at bit `off`.
-__device__ __forceinline__ void put_bits(uint32_t *words, uint64_t off, uint64_t val, uint32_t len) {
-    if (!len) return;
-    const uint32_t sh = (uint32_t)(off & 31);
-    const uint64_t w = off >> 5;
-    const unsigned __int128 X = (unsigned __int128)val << (96 - sh - len);
-    const uint32_t w0 = (uint32_t)(X >> 64), w1 = (uint32_t)(X >> 32), w2 = (uint32_t)X;
-    if (w0) atomicOr(&words[w], __builtin_bswap32(w0));
-    if (w1) atomicOr(&words[w + 1], __builtin_bswap32(w1));
-    if (w2) atomicOr(&words[w + 2], __builtin_bswap32(w2));
-}
-
-// q one-bits at bit `off`; whole 32-bit words inside the run belong to this code alone.
-__device__ void put_ones(uint32_t *words, uint64_t off, uint64_t q) {
-    const uint64_t end = off + q;
-    const uint32_t head = (uint32_t)min<uint64_t>((32 - (off & 31)) & 31, q);  // up to the next word
-    if (head) put_bits(words, off, (1ULL << head) - 1, head);
-    uint64_t w = (off + head) >> 5;
-    const uint64_t wend = end >> 5;  // whole words
-    for (; w < wend; ++w) words[w] = 0xFFFFFFFFu;
-    const uint32_t tail = (uint32_t)(end & 31);
-    if (w == wend && tail && (w << 5) >= off + head) put_bits(words, w << 5, (1ULL << tail) - 1, tail);
-}
-
-__device__ __forceinline__ void put_code(uint32_t *words, uint64_t off, const Code &c) {
-    const uint64_t tail = ((c.gap & ((1ULL << c.rice) - 1)) << c.hl) | c.hc;  // 0, r bits, Huffman code
-    const uint32_t tail_len = 1 + c.rice + c.hl;
-    if (c.len <= 64) {
-        const uint64_t ones = c.q ? (((1ULL << c.q) - 1) << tail_len) : 0ULL;
-        put_bits(words, off, ones | tail, (uint32_t)c.len);
+// 1^q 0 r-bit remainder, then the Huffman code (codec.py:214-257)
+__device__ __forceinline__ void put_code(BitWriter &bw, uint64_t gap, uint32_t rice, uint32_t hv) {
+    const uint64_t q = gap >> rice;
+    const uint32_t hl = hv & 31;
+    const uint64_t tail = ((gap & ((1ULL << rice) - 1)) << hl) | (hv >> 5);  // 0, r bits, Huffman code
+    const uint32_t tail_len = 1 + rice + hl;                                  // <= 48
+    if (q + tail_len <= 32) {
+        bw.put(q ? (((1ULL << q) - 1) << tail_len) | tail : tail, (uint32_t)(q + tail_len));
     } else {
-        put_ones(words, off, c.q);
-        put_bits(words, off + c.q, tail, tail_len);
+        bw.ones(q);
+        if (tail_len > 32) {
+            bw.put(tail >> 32, tail_len - 32);
+            bw.put(tail & 0xFFFFFFFFULL, 32);
+        } else {
+            bw.put(tail, tail_len);
+        }
     }
 }
 
 __global__ __launch_bounds__(256) void k_pack(CodeArgs a) {
-    __shared__ unsigned long long sh[256];
-    const uint64_t ib = (uint64_t)blockIdx.x * kElemsPerWG + (uint64_t)threadIdx.x * kElemsPerThread;
-    unsigned long long sum = 0;
-    if (ib < a.n) {
-        Walk w = walk_start(a, ib);
-        for (int k = 0; k < kElemsPerThread && ib + k < a.n; ++k) sum += walk_next(a, w, ib + k).len;
-    }
-    unsigned long long total;
-    unsigned long long off = a.woff[blockIdx.x] + block_exclusive_sum(sum, sh, &total);
-    if (ib < a.n) {
-        Walk w = walk_start(a, ib);
-        for (int k = 0; k < kElemsPerThread && ib + k < a.n; ++k) {
-            const uint64_t i = ib + k;
-            const Code c = walk_next(a, w, i);
-            const uint64_t rel = i - w.gr.elem_base;
-            if ((rel & 255) == 0) a.bstart[w.gr.blk_base + (rel >> 8)] = off;
-            put_code(a.words, off, c);
-            off += c.len;
+    __shared__ uint64_t rec[256 * kRecPad];
+    const uint64_t wbase = (uint64_t)blockIdx.x * kElemsPerWG;
+    stage_records(a.sorted, a.n, wbase, rec);
+    ThreadCodes tc;
+    thread_codes(a, rec, wbase, tc);
+    if (!tc.n) return;
+    unsigned long long off = a.toff[(uint64_t)blockIdx.x * 256 + threadIdx.x];
+    BitWriter bw(a.words, off);
+#pragma unroll
+    for (int k = 0; k < kElemsPerThread; ++k) {
+        if ((uint32_t)k < tc.n) {
+            if (tc.blk[k] != kNone) a.bstart[tc.blk[k]] = off;
+            const uint32_t rice = (tc.key[k] >> 17) & 31;
+            put_code(bw, tc.gap[k], rice, tc.hv[k]);
+            off += code_len(tc, k);
         }
     }
+    bw.finish();
 }
 
 __global__ __launch_bounds__(256) void k_block_bits(const unsigned long long *bstart, uint64_t n_blocks, uint32_t *out,
@@ -831,7 +891,7 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
     uint64_t eb = 0, size = 0, qmax = 0, cur = 0, end = 0;
     bool bad = false;
     if (b < a.n_blocks) {
-        const uint32_t g = group_of_block(a.groups, a.n_groups, b);
+        const uint32_t g = a.bmap[b];
         const GroupDev gr = a.groups[g];
         const uint64_t kb = b - gr.blk_base;
         cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
@@ -933,7 +993,7 @@ __global__ __launch_bounds__(64) void k_decode(DecodeArgs a) {
 __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
     if (*a.bad) return;
     const uint64_t b = blockIdx.x;
-    const uint32_t g = group_of_block(a.groups, a.n_groups, b);
+    const uint32_t g = a.bmap[b];
     const GroupDev gr = a.groups[g];
     const uint64_t kb = b - gr.blk_base;
     const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
@@ -1215,7 +1275,7 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
     __shared__ unsigned long long sh[256];
     if (*a.bad) return;
     const uint64_t b = blockIdx.x;
-    const uint32_t g = group_of_block(a.groups, a.n_groups, b);
+    const uint32_t g = a.bmap[b];
     const GroupDev gr = a.groups[g];
     const uint64_t kb = b - gr.blk_base;
     const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
@@ -1244,7 +1304,7 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
 
 __global__ __launch_bounds__(256) void k_scatter(BlockArgs a) {
     const uint64_t b = blockIdx.x;
-    const uint32_t g = group_of_block(a.groups, a.n_groups, b);
+    const uint32_t g = a.bmap[b];
     const GroupDev gr = a.groups[g];
     const uint64_t kb = b - gr.blk_base;
     const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
@@ -1302,6 +1362,14 @@ void launch_r0(GroupDev *groups, uint32_t n_groups, const uint64_t *sorted, hipS
 }
 
 void launch_stats(const StatsArgs &a, hipStream_t s) { CRX_LAUNCH("stats", k_stats, grid1(a.n, kElemsPerWG), 256, s, a); }
+
+void launch_chunk_map(const GroupDev *groups, uint32_t n_groups, uint32_t *cmap, hipStream_t s) {
+    CRX_LAUNCH("chunk_map", k_chunk_map, n_groups, 256, s, groups, cmap);
+}
+
+void launch_block_map(const GroupDev *groups, uint32_t n_groups, uint32_t *bmap, hipStream_t s) {
+    CRX_LAUNCH("block_map", k_block_map, n_groups, 256, s, groups, bmap);
+}
 
 void launch_code_lengths(const CodeArgs &a, hipStream_t s) {
     CRX_LAUNCH("code_lengths", k_code_lengths, grid1(a.n, kElemsPerWG), 256, s, a);
