@@ -49,6 +49,7 @@ SIGNATURES = {
     "crx_encode": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, ALLOC_FN, _vp, ctypes.POINTER(_vp), _cp, _u64]),
     "crx_encoded_present": (_i32, [_vp, _i32]),
     "crx_encoded_checksum": (_u64, [_vp, _i32]),
+    "crx_encoded_checksums": (None, [_vp, _vp, _vp]),
     "crx_encoded_total_changes": (_u64, [_vp]),
     "crx_encoded_size": (_u64, [_vp, _vp, _vp]),
     "crx_encoded_write": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _cp, _u64]),

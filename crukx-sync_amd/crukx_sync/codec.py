@@ -38,6 +38,18 @@ def bits16(name: str, t: torch.Tensor) -> torch.Tensor:
     return t.view(torch.int16).view(-1)
 
 
+_DTYPES16 = (torch.bfloat16, torch.int16)
+
+
+def _check16(name: str, t) -> torch.Tensor:
+    """bits16's checks without the views: the kernels take the storage address and element count."""
+    if type(t) is not torch.Tensor and not isinstance(t, torch.Tensor) or t.dtype not in _DTYPES16:
+        raise ValueError(f"{name}: expected a bfloat16 or int16 torch tensor, got {getattr(t, 'dtype', type(t))}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: tensor must be contiguous")
+    return t
+
+
 def exponents(a: torch.Tensor) -> torch.Tensor:
     return ((a >> 7) & 0xFF).long()
 
@@ -215,42 +227,48 @@ def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
            checksums: dict[str, int] | None = None) -> tuple[Update, dict[str, int]]:
     """The update, and the new checksums for the caller to commit once the update is serialized
     (codec.py:278-420)."""
-    pairs = {}
-    for name in old:
-        a, b = bits16(name, old[name]), bits16(name, new[name])
+    names = list(old)
+    if not names:
+        return Update([], []), {}
+    A, B = [], []
+    for name in names:
+        a, b = _check16(name, old[name]), _check16(name, new[name])
         if a.shape != b.shape:
             raise ValueError(f"{name}: old and new differ in shape")
-        pairs[name] = (a, b)
-    if not pairs:
-        return Update([], []), {}
-    if len({t.device for ab in pairs.values() for t in ab}) != 1:
+        A.append(a)
+        B.append(b)
+    src = A[0].device
+    if any(t.device != src for t in A) or any(t.device != src for t in B):
         raise ValueError("all tensors must be on one device")
-    src = next(iter(pairs.values()))[0].device
     dev = _hip_device(src)
-    names = list(pairs)
-    A, B = [], []
-    for a, b in pairs.values():
-        if a.device != dev:
-            a, b = a.to(dev), b.to(dev)
-        A.append(_aligned(a))
-        B.append(_aligned(b))
-    has = [1 if checksums is not None and n in checksums else 0 for n in names]
-    vals = [(checksums[n] & _MASK64) if h else 0 for n, h in zip(names, has)]
+    if src != dev:
+        A, B = [a.to(dev) for a in A], [b.to(dev) for b in B]
+    A = [a if a.data_ptr() & 3 == 0 else a.clone() for a in A]  # the kernels read 32-bit words
+    B = [b if b.data_ptr() & 3 == 0 else b.clone() for b in B]
+    numels = [a.numel() for a in A]
+    if checksums is None:
+        has, vals = [0] * len(names), [0] * len(names)
+    else:
+        cached = [checksums.get(n) for n in names]
+        has = [0 if c is None else 1 for c in cached]
+        vals = [0 if c is None else c & _MASK64 for c in cached]
+    n = len(names)
     L = _native.lib()
     ws = _native.Workspace(dev)
     err = _native.errbuf()
     h = ctypes.c_void_p()
     with torch.cuda.device(dev):
-        rc = L.crx_encode(len(names), _native.ptr_array([a.data_ptr() for a in A]),
-                          _native.ptr_array([b.data_ptr() for b in B]), _native.u64_array([a.numel() for a in A]),
+        rc = L.crx_encode(n, _native.ptr_array([a.data_ptr() for a in A]),
+                          _native.ptr_array([b.data_ptr() for b in B]), _native.u64_array(numels),
                           _native.i32_array(has), _native.u64_array(vals), int(_SLAB),
                           _native.stream_of(dev), ws.fn, None, ctypes.byref(h), err, 512)
     ws.check()
     _native.raise_for(rc, err)
     upd = EncodedUpdate(h.value, names, dev, ws)
-    upd._numels = [a.numel() for a in A]
-    new_checksums = {n: L.crx_encoded_checksum(h.value, t) for t, n in enumerate(names)
-                     if L.crx_encoded_present(h.value, t)}
+    upd._numels = numels
+    present, chk = (ctypes.c_int32 * n)(), (ctypes.c_uint64 * n)()
+    L.crx_encoded_checksums(h.value, present, chk)
+    new_checksums = {name: chk[t] for t, name in enumerate(names) if present[t]}
     return upd, new_checksums
 
 
@@ -273,9 +291,10 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
         return 0
     targets = []
     for name, numel in zip(names, numels):
-        if name not in weights:
+        t = weights.get(name) if isinstance(weights, dict) else (weights[name] if name in weights else None)
+        if t is None:
             raise ValueError(f"update has tensor {name!r} that the receiver does not have")
-        a = bits16(name, weights[name])
+        a = _check16(name, t)
         if a.numel() != numel:
             raise ValueError(f"{name}: update is for {numel} elements, receiver has {a.numel()}")
         targets.append(a)
@@ -284,7 +303,7 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
         raise ValueError("all updated tensors must be on one device")
     dev = _hip_device(src)
     staged = [a.to(dev) for a in targets] if src != dev else targets
-    cache = [_cache_get(checksums, name, weights[name]) for name in names]
+    cache = [_cache_get(checksums, name, t) for name, t in zip(names, targets)] if checksums is not None else [None] * len(names)
     has = [0 if c is None else 1 for c in cache]
     vals = [0 if c is None else c & _MASK64 for c in cache]
     payload_dev = 0
@@ -305,11 +324,11 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     ws.check()
     ws.release()
     _native.raise_for(rc, err)
-    for name, a, s in zip(names, targets, staged):
-        if s is not a:
-            a.copy_(s)  # an in-place op: bumps the tensor's version like index_put_ does
-        else:
-            torch.autograd.graph.increment_version(weights[name])
+    if staged is targets:
+        torch.autograd.graph.increment_version(targets)  # in place, like index_put_: bumps _version
+    else:
+        for a, s in zip(targets, staged):
+            a.copy_(s)  # an in-place op: bumps the tensor's version
     if checksums is not None:  # record the version after our own write
-        checksums.update({name: (c, weights[name]._version) for name, c in zip(names, header_chk)})
+        checksums.update({name: (c, t._version) for name, c, t in zip(names, header_chk, targets)})
     return changed.value

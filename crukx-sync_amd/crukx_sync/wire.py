@@ -269,6 +269,9 @@ def parse(data) -> ParsedUpdate:
     return ParsedUpdate(h.value, buf)
 
 
+_prefix_hint = [0]
+
+
 def _parse_tensor(t, L, err):
     import torch
     from . import _native
@@ -279,16 +282,20 @@ def _parse_tensor(t, L, err):
     total = t.numel()
     if total == 0:
         return parse(b"")
-    last = int(t[-1].item())
-    have = min(total, 1 << 16)
+    have = min(total, max(1 << 16, _prefix_hint[0]))
     while True:
-        prefix = t[:have].cpu().numpy().tobytes()
+        # the leading bytes and the last byte, through pinned host memory
+        host = torch.empty(have + 1, dtype=torch.uint8, pin_memory=True)
+        host[:have].copy_(t[:have])
+        host[have:].copy_(t[total - 1:])
         h = ctypes.c_void_p()
         need = ctypes.c_uint64()
-        rc = L.crx_parse_prefix(prefix, len(prefix), total, last, ctypes.byref(h), ctypes.byref(need), err, 512)
+        rc = L.crx_parse_prefix(ctypes.c_void_p(host.data_ptr()), have, total, int(host[have]), ctypes.byref(h),
+                                ctypes.byref(need), err, 512)
         if rc == _native.INVALID and need.value > have:
-            have = min(total, max(need.value, 2 * have))
+            have = min(total, max(need.value + 64, 2 * have))
             continue
         _native.raise_for(rc, err)
+        _prefix_hint[0] = have  # updates of a run have headers of about the same size
         off = L.crx_update_payload_offset(h.value)
-        return ParsedUpdate(h.value, prefix, payload_dev=t[off:])
+        return ParsedUpdate(h.value, host, payload_dev=t[off:])

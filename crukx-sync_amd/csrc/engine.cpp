@@ -75,16 +75,34 @@ void timing_end(const char *name, hipStream_t s) {
 }
 
 // ------------------------------------------------------------------ workspace
+// Device buffers of one call.  Small buffers are carved from chunks of kArenaChunk bytes so that a
+// call makes few trips through the caller's allocator; large ones are allocated on their own.
+constexpr uint64_t kArenaChunk = 8ULL << 20;
+
 struct Arena {
     crx_alloc_fn fn;
     void *ctx;
+    uint8_t *chunk = nullptr;
+    uint64_t used = 0, size = 0;
+
+    void *raw(uint64_t bytes) {
+        void *p = fn(ctx, bytes);
+        if (!p) throw std::bad_alloc();
+        return p;
+    }
     template <typename T>
     T *get(uint64_t count) {
         uint64_t bytes = std::max<uint64_t>(count * sizeof(T), 16);
         bytes = (bytes + 255) & ~uint64_t(255);
-        void *p = fn(ctx, bytes);
-        if (!p) throw std::bad_alloc();
-        return static_cast<T *>(p);
+        if (bytes > kArenaChunk / 4) return static_cast<T *>(raw(bytes));
+        if (used + bytes > size) {
+            chunk = static_cast<uint8_t *>(raw(kArenaChunk));
+            used = 0;
+            size = kArenaChunk;
+        }
+        T *p = reinterpret_cast<T *>(chunk + used);
+        used += bytes;
+        return p;
     }
 };
 
@@ -769,6 +787,12 @@ int32_t crx_encode(int32_t n, const uint16_t *const *olds, const uint16_t *const
 
 int32_t crx_encoded_present(const crx_encoded *e, int32_t t) { return (t >= 0 && t < e->n) ? e->present[t] : 0; }
 uint64_t crx_encoded_checksum(const crx_encoded *e, int32_t t) { return (t >= 0 && t < e->n) ? e->checksum[t] : 0; }
+void crx_encoded_checksums(const crx_encoded *e, int32_t *present, uint64_t *checksums) {
+    for (int32_t t = 0; t < e->n; ++t) {
+        present[t] = e->present[t];
+        checksums[t] = e->checksum[t];
+    }
+}
 uint64_t crx_encoded_total_changes(const crx_encoded *e) { return e->total_changes; }
 
 uint64_t crx_encoded_size(const crx_encoded *e, const char *const *names, const uint64_t *name_lens) {

@@ -107,6 +107,8 @@ int32_t crx_encode(int32_t n, const uint16_t *const *olds, const uint16_t *const
 int32_t crx_encoded_present(const crx_encoded *e, int32_t t);
 /* New checksum of tensor t (valid when present). */
 uint64_t crx_encoded_checksum(const crx_encoded *e, int32_t t);
+/* Both of the above for every tensor of the encode call (n entries each). */
+void crx_encoded_checksums(const crx_encoded *e, int32_t *present, uint64_t *checksums);
 uint64_t crx_encoded_total_changes(const crx_encoded *e);
 /* Serialized size (wire.serialize, wire.py:64-89) given the names of the encode call's tensors. */
 uint64_t crx_encoded_size(const crx_encoded *e, const char *const *names, const uint64_t *name_lens);
