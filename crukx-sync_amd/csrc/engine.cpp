@@ -255,7 +255,6 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     E.numel.assign(numels, numels + n);
     E.groups.assign(n, {});
     Layout L;
-    uint64_t total_elems = 0;
     for (int32_t t = 0; t < n; ++t) {
         if (!numels[t]) continue;
         TensorDesc d = make_desc(olds[t], numels[t]);
@@ -265,7 +264,6 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
         d.cold = (has_cache && has_cache[t]) ? 0u : 1u;
         L.descs.push_back(d);
         L.call_index.push_back(t);
-        total_elems += numels[t];
     }
     if (L.descs.empty()) return;
     finish_layout(L, slab);
@@ -275,29 +273,34 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     h2d(d_descs, L.descs.data(), T, s);
     uint32_t *hall = ar.get<uint32_t>((uint64_t)tiles * 256), *hchg = ar.get<uint32_t>((uint64_t)tiles * 256);
     uint64_t *delta = ar.get<uint64_t>(tiles), *full = ar.get<uint64_t>(tiles);
-    unsigned long long *cnt = ar.get<unsigned long long>(8);
     ScanDev sd = upload_scan(ar, L, d_descs, s);
     uint32_t *tot_all = ar.get<uint32_t>((uint64_t)T * 256), *tot_chg = ar.get<uint32_t>((uint64_t)T * 256);
     GroupDev *d_groups = ar.get<GroupDev>((uint64_t)T * 256);
     uint32_t *gbase = ar.get<uint32_t>((uint64_t)T * 256);
     unsigned long long *gcnt = ar.get<unsigned long long>(2);
 
-    uint64_t rec_cap = total_elems / 24 + 65536;
-    uint64_t *rec = nullptr;
-    Chunk *chunks = nullptr;
-    unsigned long long h[8];
-    for (int attempt = 0;; ++attempt) {
-        const uint64_t chunk_cap = tiles + rec_cap / (kChgCap - kRow) + 16;  // one flush per slab + full ones
-        rec = ar.get<uint64_t>(rec_cap);
-        chunks = ar.get<Chunk>(chunk_cap);
-        zero(cnt, 8, s);
-        EncRankArgs a{d_descs, sd.tile_tensor, T, slab, hall, hchg, rec, rec_cap, chunks, chunk_cap, cnt, delta, full};
-        launch_enc_rank(a, tiles, s);
-        d2h(h, cnt, 3, s);
+    // Each slab stores its change records in a region of its own, sized for 1/24 of its elements
+    // (+64).  If one overflows, the exact counts of that pass give exact regions for a second pass.
+    const uint64_t per_slab = slab / 24 + 64;
+    uint32_t *rec_count = ar.get<uint32_t>(tiles);
+    unsigned int *ovf = ar.get<unsigned int>(1);
+    zero(ovf, 1, s);
+    EncRankArgs a{d_descs, sd.tile_tensor, T, slab, hall, hchg, ar.get<uint64_t>((uint64_t)tiles * per_slab), nullptr,
+                  per_slab, rec_count, ovf, delta, full};
+    launch_enc_rank(a, tiles, s);
+    unsigned int hovf1 = 0;
+    d2h(&hovf1, ovf, 1, s);
+    sync(s);
+    if (hovf1) {
+        unsigned long long *rec_base = ar.get<unsigned long long>(tiles + 1);
+        launch_scan_u32(rec_count, tiles, rec_base, ar.get<unsigned long long>(scan_parts(tiles)), s);
+        unsigned long long total = 0;
+        d2h(&total, rec_base + tiles, 1, s);
         sync(s);
-        if (!h[2]) break;
-        if (attempt) throw DeviceError("change records overflowed twice");
-        rec_cap = h[0] + 1;  // exact count of the first attempt
+        a.rec = ar.get<uint64_t>(total);
+        a.rec_base = rec_base;
+        zero(ovf, 1, s);
+        launch_enc_rank(a, tiles, s);
     }
     launch_scan_tables(hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_all, s);
     launch_scan_tables(hchg, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_chg, s);
@@ -311,7 +314,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     if (C >= (1ULL << 32)) throw Invalid("2^32 or more changes in one update are not supported");
 
     uint64_t *sorted = ar.get<uint64_t>(C);
-    launch_place(chunks, (uint32_t)h[1], rec, sd.tile_tensor, hall, hchg, gbase, sorted, C, s);
+    launch_place(a, tiles, sd.tile_tensor, hall, hchg, gbase, sorted, C, s);
     const uint64_t n_thr = (C + kElemsPerThread - 1) / kElemsPerThread;  // threads of the walking kernels
     uint32_t *cmap = ar.get<uint32_t>(n_thr);
     launch_chunk_map(d_groups, (uint32_t)G, cmap, s);
@@ -426,16 +429,16 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     uint32_t *words = ar.get<uint32_t>(n_words);
     unsigned long long *bstart = ar.get<unsigned long long>(B + 1);
     uint32_t *bb = ar.get<uint32_t>(B);
-    unsigned int *ovf = ar.get<unsigned int>(1);
+    unsigned int *bovf = ar.get<unsigned int>(1);
     zero(words, n_words, s);
-    zero(ovf, 1, s);
+    zero(bovf, 1, s);
     HIP_OK(hipMemcpyAsync(bstart + B, toff + n_thr, sizeof(unsigned long long), hipMemcpyDeviceToDevice, s));
     ca.words = words;
     ca.bstart = bstart;
     launch_pack(ca, s);
-    launch_block_bits(bstart, B, bb, ovf, s);
+    launch_block_bits(bstart, B, bb, bovf, s);
     unsigned int hovf = 0;
-    d2h(&hovf, ovf, 1, s);
+    d2h(&hovf, bovf, 1, s);
     sync(s);
     if (hovf) throw Invalid("a block exceeds 2^32 bits; the update cannot be represented");
     E.d_block_bits = bb;

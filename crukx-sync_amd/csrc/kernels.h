@@ -8,7 +8,7 @@
 namespace crx {
 
 constexpr int kRow = 128;             // elements per wavefront row: 64 lanes x one 32-bit word
-constexpr int kChgCap = 384;          // changes a wavefront buffers in LDS; a flush leaves room for a row
+constexpr int kChgCap = 256;          // changes a wavefront buffers in LDS; a flush leaves room for a row
 constexpr int kDense = 32;            // residual symbols below this are counted in a dense table
 constexpr int kLocalGroups = 64;      // groups a statistics workgroup accumulates in LDS
 constexpr uint32_t kScanTiles = 32;   // slabs per chunk of the per-tensor histogram scan
@@ -34,13 +34,6 @@ struct TensorDesc {
     uint32_t cold;              // 1: a full checksum is needed (new for encode, old for apply)
 };
 
-// A run of change records one wavefront flushed: records [base, base + count) of slab `tile`.
-struct Chunk {
-    uint32_t tile;
-    uint32_t count;
-    uint64_t base;
-};
-
 // One (tensor, exponent) group.  Encode fills r0/rice/blk_base after the statistics pass;
 // apply fills everything from the parsed header.
 struct GroupDev {
@@ -59,11 +52,11 @@ struct EncRankArgs {
     const uint32_t *tile_tensor;    // [tiles] tensor of each slab
     uint32_t n_tensors, slab;
     uint32_t *hall, *hchg;          // [tiles][256]
-    uint64_t *rec;
-    uint64_t rec_cap;
-    Chunk *chunks;
-    uint64_t chunk_cap;
-    unsigned long long *counters;   // [0] records, [1] chunks, [2] overflow bits
+    uint64_t *rec;                  // change records, slab by slab
+    const unsigned long long *rec_base;  // [tiles] first record of each slab, or null: slab t at t * rec_per_slab
+    uint64_t rec_per_slab;          // records a slab may store when rec_base is null
+    uint32_t *rec_count;            // [tiles] changes of each slab (counted past the capacity too)
+    unsigned int *overflow;         // set when a slab has more changes than it may store
     uint64_t *delta, *full;         // [tiles]
 };
 
@@ -163,7 +156,7 @@ void launch_scan_tables(uint32_t *h, const ScanChunk *chunks, uint32_t n_chunks,
                         uint32_t n_tensors, uint32_t *csum, uint32_t *totals, hipStream_t s);
 void launch_enc_groups(const uint32_t *totals_chg, uint32_t n_tensors, GroupDev *groups, uint32_t *gbase,
                        unsigned long long *counters, hipStream_t s);
-void launch_place(const Chunk *chunks, uint32_t n_chunks, const uint64_t *rec, const uint32_t *tile_tensor,
+void launch_place(const EncRankArgs &a, uint32_t tiles, const uint32_t *tile_tensor,
                   const uint32_t *hall_pre, const uint32_t *hchg_pre, const uint32_t *gbase,
                   uint64_t *sorted, uint64_t n_sorted, hipStream_t s);
 void launch_r0(GroupDev *groups, uint32_t n_groups, const uint64_t *sorted, hipStream_t s);

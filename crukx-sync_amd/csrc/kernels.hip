@@ -162,30 +162,21 @@ __device__ __forceinline__ void stream_rows(const Slab &sl, const Rsrc (&src)[S]
 // exponent (`rc`): the running per-exponent counts in LDS give the part before the row, ballots and
 // mbcnt the stable part inside the row.  Changed elements are buffered in LDS as (rank, rc, exponent,
 // offset, old, new) and finished in dense batches: zigzag residual, checksum delta, 64-bit record.
-__device__ void flush_changes(const EncRankArgs &a, uint32_t tau, const Slab &sl, const uint64_t *meta,
-                              const uint32_t *vals, uint32_t cnt, uint64_t &dacc) {
+// Records go to the slab's own region, [base, base + cap): no shared counter.
+__device__ void flush_changes(const EncRankArgs &a, const Slab &sl, const uint64_t *meta, const uint32_t *vals,
+                              uint32_t cnt, uint64_t base, uint64_t cap, uint64_t &written, uint64_t &dacc) {
     wave_fence();
-    unsigned long long base = 0;
-    if (lane() == 0) base = atomicAdd(&a.counters[0], (unsigned long long)cnt);
-    base = __shfl(base, 0, 64);
-    const bool fits = base + cnt <= a.rec_cap;
+    const bool fits = written + cnt <= cap;
     for (uint32_t j = lane(); j < cnt; j += 64) {
         const uint64_t m = meta[j];
         const uint32_t v = vals[j];
         const uint32_t o16 = v & 0xFFFF, n16 = v >> 16;
         const uint32_t f = (uint32_t)(m >> 42);
         dacc += (uint64_t)((int64_t)n16 - (int64_t)o16) * weight(sl.base + f);
-        if (fits) a.rec[base + j] = (m & ((1ULL << 42) - 1)) | ((uint64_t)zigzag(o16, n16) << 42);
+        if (fits) a.rec[base + written + j] = (m & ((1ULL << 42) - 1)) | ((uint64_t)zigzag(o16, n16) << 42);
     }
-    if (lane() == 0) {
-        if (fits) {
-            const unsigned long long ci = atomicAdd(&a.counters[1], 1ULL);
-            if (ci < a.chunk_cap) a.chunks[ci] = Chunk{tau, cnt, base};
-            else atomicOr(&a.counters[2], 2ULL);
-        } else {
-            atomicOr(&a.counters[2], 1ULL);
-        }
-    }
+    if (!fits && lane() == 0) *a.overflow = 1u;
+    written += cnt;
     wave_fence();
 }
 
@@ -194,45 +185,56 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
                               uint32_t *hall, uint32_t *hchg, uint64_t *meta, uint32_t *vals) {
     const uint32_t ln = lane(), rep = ln & 3;
     const Rsrc src[2] = {slab_rsrc(td.frame, sl), slab_rsrc(td.frame_new, sl)};
+    const uint64_t rbase = a.rec_base ? a.rec_base[tau] : (uint64_t)tau * a.rec_per_slab;
+    const uint64_t rcap = a.rec_base ? ~0ULL : a.rec_per_slab;
+    uint64_t written = 0;
     uint32_t cnt = 0;
     uint64_t dacc = 0, facc = 0;
-    stream_rows<kRankRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t n) {
-        const uint32_t f = r * kRow + 2 * ln;
-        bool v0 = true, v1 = true;
+    stream_rows<kRankRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t nw) {
+        // exponents; lanes outside the slab count into slot 256 and never change
+        uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF, x = o ^ nw, n = nw;
         if (!row_full(sl, r)) {
-            v0 = f >= sl.f_lo && f < sl.f_hi;
-            v1 = f + 1 >= sl.f_lo && f + 1 < sl.f_hi;
+            const uint32_t f = r * kRow + 2 * ln;
+            if (f < sl.f_lo || f >= sl.f_hi) {
+                k0 = 256;
+                x &= 0xFFFF0000u;
+                n &= 0xFFFF0000u;
+            }
+            if (f + 1 < sl.f_lo || f + 1 >= sl.f_hi) {
+                k1 = 256;
+                x &= 0xFFFFu;
+                n &= 0xFFFFu;
+            }
         }
-        const uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF;
-        const uint32_t x = o ^ n;
-        const bool c0 = v0 && (x & 0xFFFF), c1 = v1 && x > 0xFFFF;
+        const bool c0 = (x & 0xFFFF) != 0, c1 = x > 0xFFFF;
         const uint64_t C0 = ballot(c0), C1 = ballot(c1);
         if (C0 | C1) {
             uint32_t rk0 = 0, rc0 = 0, rk1 = 0, rc1 = 0;
             uint64_t P0 = C0, P1 = C1;
-            while (P0 | P1) {  // once per distinct exponent among this row's changes
-                const uint32_t k = P0 ? rdlane(k0, (uint32_t)__builtin_ctzll(P0))
-                                      : rdlane(k1, (uint32_t)__builtin_ctzll(P1));
-                const bool m0 = v0 && k0 == k, m1 = v1 && k1 == k;
-                const uint64_t M0 = ballot(m0), M1 = ballot(m1);
+            do {  // once per distinct exponent among this row's changes
+                const uint32_t l = (uint32_t)__builtin_ctzll(P0 | P1);
+                const uint32_t k = rdlane((P0 >> l) & 1 ? k0 : k1, l);
+                const bool m0 = k0 == k, m1 = k1 == k;
+                const uint64_t M0 = ballot(m0), M1 = ballot(m1), D0 = M0 & C0, D1 = M1 & C1;
                 const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
-                const uint32_t R = h.x + h.y + h.z + h.w;
-                const uint32_t Rc = hchg[k];
-                const uint32_t before = mbcnt(M0) + mbcnt(M1);
-                const uint32_t beforec = mbcnt(M0 & C0) + mbcnt(M1 & C1);
-                if (c0 && m0) {
-                    rk0 = R + before;
-                    rc0 = Rc + beforec;
+                const uint32_t R = h.x + h.y + h.z + h.w;  // exponent-k elements before this row
+                const uint32_t Rc = hchg[k];               // ... of them changed
+                const uint32_t before = R + mbcnt(M0) + mbcnt(M1), beforec = Rc + mbcnt(D0) + mbcnt(D1);
+                const bool d0 = c0 && m0, d1 = c1 && m1;
+                if (d0) {
+                    rk0 = before;
+                    rc0 = beforec;
                 }
-                if (c1 && m1) {
-                    rk1 = R + before + (m0 ? 1u : 0u);
-                    rc1 = Rc + beforec + ((c0 && m0) ? 1u : 0u);
+                if (d1) {
+                    rk1 = before + (m0 ? 1u : 0u);
+                    rc1 = beforec + (d0 ? 1u : 0u);
                 }
                 wave_fence();
-                if (ln == 0) hchg[k] = Rc + (uint32_t)__popcll(M0 & C0) + (uint32_t)__popcll(M1 & C1);
+                if (ln == 0) hchg[k] = Rc + (uint32_t)(__popcll(D0) + __popcll(D1));
                 P0 &= ~M0;
                 P1 &= ~M1;
-            }
+            } while (P0 | P1);
+            const uint32_t f = r * kRow + 2 * ln;
             const uint32_t cb = cnt + mbcnt(C0) + mbcnt(C1);  // buffer slot of this lane's first change
             if (c0) {
                 meta[cb] = (uint64_t)rk0 | ((uint64_t)rc0 << 17) | ((uint64_t)k0 << 34) | ((uint64_t)f << 42);
@@ -246,18 +248,18 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
             cnt += (uint32_t)(__popcll(C0) + __popcll(C1));
             wave_fence();
         }
-        if (v0) atomicAdd(&hall[4 * k0 + rep], 1u);
-        if (v1) atomicAdd(&hall[4 * k1 + rep], 1u);
+        atomicAdd(&hall[4 * k0 + rep], 1u);
+        atomicAdd(&hall[4 * k1 + rep], 1u);
         if (COLD) {
-            if (v0) facc += (uint64_t)(n & 0xFFFF) * weight(sl.base + f);
-            if (v1) facc += (uint64_t)(n >> 16) * weight(sl.base + f + 1);
+            const uint32_t f = r * kRow + 2 * ln;
+            facc += (uint64_t)(n & 0xFFFF) * weight(sl.base + f) + (uint64_t)(n >> 16) * weight(sl.base + f + 1);
         }
         if (cnt > kChgCap - kRow) {
-            flush_changes(a, tau, sl, meta, vals, cnt, dacc);
+            flush_changes(a, sl, meta, vals, cnt, rbase, rcap, written, dacc);
             cnt = 0;
         }
     });
-    if (cnt) flush_changes(a, tau, sl, meta, vals, cnt, dacc);
+    if (cnt) flush_changes(a, sl, meta, vals, cnt, rbase, rcap, written, dacc);
     wave_fence();
     for (uint32_t k = ln; k < 256; k += 64) {
         const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
@@ -269,18 +271,19 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
     if (ln == 0) {
         a.delta[tau] = dacc;
         a.full[tau] = facc;
+        a.rec_count[tau] = (uint32_t)written;
     }
 }
 
 __global__ __launch_bounds__(64) void k_enc_rank(EncRankArgs a) {
-    __shared__ __attribute__((aligned(16))) uint32_t hall[256 * 4];  // 4 copies per exponent
+    __shared__ __attribute__((aligned(16))) uint32_t hall[257 * 4];  // 4 copies per exponent; 256: outside
     __shared__ uint32_t hchg[256];
     __shared__ uint64_t meta[kChgCap];
     __shared__ uint32_t vals[kChgCap];
     const uint32_t tau = blockIdx.x;
     const TensorDesc td = a.descs[a.tile_tensor[tau]];
     const Slab sl = slab_of(td, tau - td.tile_begin, a.slab);
-    for (uint32_t i = lane(); i < 1024; i += 64) hall[i] = 0;
+    for (uint32_t i = lane(); i < 257 * 4; i += 64) hall[i] = 0;
     for (uint32_t i = lane(); i < 256; i += 64) hchg[i] = 0;
     wave_fence();
     if (td.cold) enc_rank_slab<true>(a, td, tau, sl, hall, hchg, meta, vals);
@@ -425,17 +428,20 @@ __global__ __launch_bounds__(1024) void k_enc_groups(const uint32_t *tot, uint32
 
 // Records -> update order: position = group start + changes of the group in earlier slabs + rank
 // among the slab's changes of that exponent; value = zz and the group-local index.
-__global__ __launch_bounds__(64) void k_place(const Chunk *chunks, const uint64_t *rec, const uint32_t *tile_tensor,
-                                              const uint32_t *hall_pre, const uint32_t *hchg_pre,
-                                              const uint32_t *gbase, uint64_t *sorted, uint64_t n_sorted) {
-    const Chunk c = chunks[blockIdx.x];
-    const uint32_t t = tile_tensor[c.tile];
-    for (uint32_t j = lane(); j < c.count; j += 64) {
-        const uint64_t r = rec[c.base + j];
+// One wavefront per slab: its records -> (zz << 32 | group-local index) at the change's place in
+// update order.
+__global__ __launch_bounds__(64) void k_place(EncRankArgs a, const uint32_t *tile_tensor, const uint32_t *hall_pre,
+                                              const uint32_t *hchg_pre, const uint32_t *gbase, uint64_t *sorted,
+                                              uint64_t n_sorted) {
+    const uint32_t tau = blockIdx.x;
+    const uint32_t t = tile_tensor[tau], count = a.rec_count[tau];
+    const uint64_t base = a.rec_base ? a.rec_base[tau] : (uint64_t)tau * a.rec_per_slab;
+    for (uint32_t j = lane(); j < count; j += 64) {
+        const uint64_t r = a.rec[base + j];
         const uint32_t rank = (uint32_t)(r & 0x1FFFF), rc = (uint32_t)((r >> 17) & 0x1FFFF);
         const uint32_t k = (uint32_t)((r >> 34) & 0xFF), zz = (uint32_t)(r >> 42);
-        const uint32_t gidx = hall_pre[(uint64_t)c.tile * 256 + k] + rank;
-        const uint32_t dest = gbase[(uint64_t)t * 256 + k] + hchg_pre[(uint64_t)c.tile * 256 + k] + rc;
+        const uint32_t gidx = hall_pre[(uint64_t)tau * 256 + k] + rank;
+        const uint32_t dest = gbase[(uint64_t)t * 256 + k] + hchg_pre[(uint64_t)tau * 256 + k] + rc;
         if (dest < n_sorted) sorted[dest] = ((uint64_t)zz << 32) | gidx;
     }
 }
@@ -1347,10 +1353,9 @@ void launch_enc_groups(const uint32_t *totals_chg, uint32_t n_tensors, GroupDev 
     CRX_LAUNCH("enc_groups", k_enc_groups, 1, 1024, s, totals_chg, n_tensors, groups, gbase, counters);
 }
 
-void launch_place(const Chunk *chunks, uint32_t n_chunks, const uint64_t *rec, const uint32_t *tile_tensor,
-                  const uint32_t *hall_pre, const uint32_t *hchg_pre, const uint32_t *gbase,
-                  uint64_t *sorted, uint64_t n_sorted, hipStream_t s) {
-    CRX_LAUNCH("place", k_place, n_chunks, 64, s, chunks, rec, tile_tensor, hall_pre, hchg_pre, gbase, sorted, n_sorted);
+void launch_place(const EncRankArgs &a, uint32_t tiles, const uint32_t *tile_tensor, const uint32_t *hall_pre,
+                  const uint32_t *hchg_pre, const uint32_t *gbase, uint64_t *sorted, uint64_t n_sorted, hipStream_t s) {
+    CRX_LAUNCH("place", k_place, tiles, 64, s, a, tile_tensor, hall_pre, hchg_pre, gbase, sorted, n_sorted);
 }
 
 void launch_tile_map(const TensorDesc *descs, uint32_t n_tensors, uint32_t *tile_tensor, hipStream_t s) {
