@@ -454,7 +454,8 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     *changed = 0;
     const uint32_t T = (uint32_t)u.tensors.size();
     if (!T) return;
-    const uint32_t slab = slab_size(slab_req);
+    // the select pass keeps slab ranks in 16 bits: apply cuts slabs of at most 65536 elements
+    const uint32_t slab = std::min<uint32_t>(slab_size(slab_req), 65536);
     const uint64_t C = u.total_changes;
     if (C >= (1ULL << 32)) throw Invalid("2^32 or more changes in one update are not supported");
     Layout L;

@@ -15,7 +15,8 @@ constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ULL;
 constexpr uint64_t kMix1 = 0xBF58476D1CE4E5B9ULL;
 constexpr uint64_t kMix2 = 0x94D049BB133111EBULL;
 constexpr int kRankRows = 8;    // rows per batch of the encode rank pass (two streams)
-constexpr int kScanRows = 16;   // rows per batch of the apply histogram and select passes
+constexpr int kScanRows = 16;   // rows per batch of the apply histogram pass
+constexpr int kSelectRows = 12; // ... of the select pass (fewer registers: occupancy)
 
 // splitmix64(i) | 1: the per-position checksum weight (docs/FORMAT.md:61-64).
 __device__ __forceinline__ uint64_t weight(uint64_t i) {
@@ -1062,7 +1063,7 @@ struct SelectLds {
     uint2 next[W + kSpare];          // per exponent: {rank of the next target, its list index}
     uint2 range[W];                  // per exponent: {end of its list, group-local index - list index}
     uint32_t pre[W];                 // exponent count before the slab (targets read from HBM only)
-    alignas(16) uint32_t list[kTgtCap];  // slab ranks of the targets, per exponent in order
+    alignas(16) uint16_t list[kTgtCap];  // slab ranks of the targets (slab <= 65536), per exponent in order
     uint32_t slot[2 * kRow];         // in-row rank -> (in-row offset << 16) | bits; [kRow, 2 kRow): per lane, unused
 };
 
@@ -1071,7 +1072,7 @@ __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Sla
                             SelectLds<W> &S) {
     const uint32_t ln = lane(), rep = ln & 3, spare = W + (ln >> 2);
     const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
-    stream_rows<kScanRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
+    stream_rows<kSelectRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
         // window index of each exponent; outside the window (or the slab): a spare counter
         uint32_t c0 = min(((o >> 7) & 0xFF) - kbase, spare), c1 = min(((o >> 23) & 0xFF) - kbase, spare);
         if (!row_full(sl, r)) {
@@ -1108,7 +1109,7 @@ __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Sla
             do {  // this row's targets of exponent k, one per lane (64 more if all lanes take one)
                 const uint32_t j = i + ln;
                 if (LDS_LIST) {
-                    const uint32_t lv = S.list[min(j, kTgtCap - 1)];
+                    const uint32_t lv = S.list[min(j, kTgtCap - 1)];  // u16: slab ranks
                     tc = j < rg.x ? lv : (uint32_t)kFar;
                 } else {
                     tc = j < rg.x ? a.local[rg.y + j] - S.pre[k] : (uint32_t)kFar;
@@ -1203,21 +1204,23 @@ __device__ void select_tile(const SelectArgs &a, uint32_t tau, SelectLds<W> &S) 
     if (in_lds) {
         // list entry x belongs to the last exponent whose list starts at or before x: mark the starts
         // of the non-empty lists, then a running maximum over the entries (16 per lane, in order)
-        uint32_t *mark = S.list;  // read into registers before the list overwrites it
+        uint16_t *mark = S.list;  // read into registers before the list overwrites it
         for (uint32_t x = ln; x < kTgtCap; x += 64) mark[x] = 0;
         wave_fence();
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            if (n4[q]) mark[start[q]] = 4 * ln + q - kbase + 1;
+            if (n4[q]) mark[start[q]] = (uint16_t)(4 * ln + q - kbase + 1);
         wave_fence();
         uint32_t v[16], run = 0;
 #pragma unroll
-        for (int i = 0; i < 16; i += 4) {
+        for (int i = 0; i < 16; i += 8) {
             const uint4 m = *reinterpret_cast<const uint4 *>(&mark[16 * ln + i]);
-            v[i] = run = max(run, m.x);
-            v[i + 1] = run = max(run, m.y);
-            v[i + 2] = run = max(run, m.z);
-            v[i + 3] = run = max(run, m.w);
+            const uint32_t w4[4] = {m.x, m.y, m.z, m.w};
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                v[i + 2 * h] = run = max(run, w4[h] & 0xFFFF);
+                v[i + 2 * h + 1] = run = max(run, w4[h] >> 16);
+            }
         }
         uint32_t before = run;  // inclusive max-scan of the lane maxima, then shifted by one lane
         for (int o = 1; o < 64; o <<= 1) {
@@ -1237,7 +1240,7 @@ __device__ void select_tile(const SelectArgs &a, uint32_t tau, SelectLds<W> &S) 
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const uint32_t x = 16 * ln + i;
-            if (x < total) S.list[x] = a.local[idx[i]] - sub[i];
+            if (x < total) S.list[x] = (uint16_t)(a.local[idx[i]] - sub[i]);
         }
     }
     wave_fence();
