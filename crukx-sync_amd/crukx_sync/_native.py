@@ -46,6 +46,8 @@ SIGNATURES = {
     "crx_update_payload_len": (_u64, [_vp]),
     "crx_update_total_changes": (_u64, [_vp]),
     "crx_apply": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, ALLOC_FN, _vp, _u64p, _cp, _u64]),
+    "crx_apply_cached": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, ALLOC_FN, _vp, _u64p, _cp, _u64]),
+    "crx_apply_hist_words": (_u64, [_u64, _i32]),
     "crx_encode": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, ALLOC_FN, _vp, ctypes.POINTER(_vp), _cp, _u64]),
     "crx_encoded_present": (_i32, [_vp, _i32]),
     "crx_encoded_checksum": (_u64, [_vp, _i32]),

@@ -12,6 +12,7 @@ device (there is no CPU implementation in the product, and without a HIP device 
 from __future__ import annotations
 
 import ctypes
+import weakref
 from collections.abc import Mapping
 
 import torch
@@ -274,6 +275,25 @@ def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
 
 # ---------------------------------------------------------------- apply
 
+# Receiver-side exponent counts per slab, kept on the device across updates of the same tensors:
+# id(tensor) -> (weakref, _version after our last write, device buffer).  They are used only with a
+# checksum-cache hit for the tensor (the same trust rule), and let apply skip its full read of
+# those weights (crx_apply_cached).
+_hist = {}
+
+
+def _hist_lookup(t):
+    e = _hist.get(id(t))
+    if e is None or e[0]() is not t:
+        return None
+    return e
+
+
+def _hist_store(t, buf):
+    key = id(t)
+    _hist[key] = (weakref.ref(t, lambda _r, key=key: _hist.pop(key, None)), t._version, buf)
+
+
 def _cache_get(checksums, name, t):
     """A cached checksum, trusted only if the tensor was not modified since it was recorded
     (codec.py:457-460)."""
@@ -316,19 +336,40 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     ws = _native.Workspace(dev)
     err = _native.errbuf()
     changed = ctypes.c_uint64()
+    # exponent counts carried across updates: only for tensors updated in place with a trusted cache
+    keep = checksums is not None and staged is targets
+    hist_in, hist_out, bufs = [], [], []
+    if keep:
+        for a, c in zip(targets, cache):
+            e = _hist_lookup(a)
+            if c is not None and e is not None and e[1] == a._version and e[2].device == dev:
+                buf = e[2]
+                hist_in.append(buf.data_ptr())
+            else:
+                buf = torch.empty(L.crx_apply_hist_words(a.numel(), int(_SLAB)), dtype=torch.int32, device=dev)
+                hist_in.append(0)
+            hist_out.append(buf.data_ptr())
+            bufs.append(buf)
     with torch.cuda.device(dev):
-        rc = L.crx_apply(u.handle, payload_dev or None, _native.ptr_array([a.data_ptr() for a in staged]),
-                         _native.u64_array([a.numel() for a in staged]), _native.i32_array(has),
-                         _native.u64_array(vals), int(_SLAB), _native.stream_of(dev), ws.fn, None,
-                         ctypes.byref(changed), err, 512)
+        rc = L.crx_apply_cached(u.handle, payload_dev or None, _native.ptr_array([a.data_ptr() for a in staged]),
+                                _native.u64_array([a.numel() for a in staged]), _native.i32_array(has),
+                                _native.u64_array(vals),
+                                _native.ptr_array(hist_in) if keep else None,
+                                _native.ptr_array(hist_out) if keep else None,
+                                int(_SLAB), _native.stream_of(dev), ws.fn, None, ctypes.byref(changed), err, 512)
     ws.check()
     ws.release()
+    if rc != _native.OK:
+        for a in targets:  # their counts may be half-updated
+            _hist.pop(id(a), None)
     _native.raise_for(rc, err)
     if staged is targets:
         torch.autograd.graph.increment_version(targets)  # in place, like index_put_: bumps _version
     else:
         for a, s in zip(targets, staged):
             a.copy_(s)  # an in-place op: bumps the tensor's version
+    for a, buf in zip(targets, bufs):
+        _hist_store(a, buf)
     if checksums is not None:  # record the version after our own write
         checksums.update({name: (c, t._version) for name, c, t in zip(names, header_chk, targets)})
     return changed.value

@@ -448,14 +448,18 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
 
 // ------------------------------------------------------------------ apply
 // codec.apply (codec.py:578-717) on the device: decode, locate, verify, then write.
+uint32_t apply_slab(int32_t slab_req) {
+    // the select pass keeps slab ranks in 16 bits: apply cuts slabs of at most 65536 elements
+    return std::min<uint32_t>(slab_size(slab_req), 65536);
+}
+
 void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets, const uint64_t *numels,
-           const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab_req, hipStream_t s, Arena &ar,
-           uint64_t *changed) {
+           const int32_t *has_cache, const uint64_t *cache_vals, uint32_t *const *hist_in, uint32_t *const *hist_out,
+           int32_t slab_req, hipStream_t s, Arena &ar, uint64_t *changed) {
     *changed = 0;
     const uint32_t T = (uint32_t)u.tensors.size();
     if (!T) return;
-    // the select pass keeps slab ranks in 16 bits: apply cuts slabs of at most 65536 elements
-    const uint32_t slab = std::min<uint32_t>(slab_size(slab_req), 65536);
+    const uint32_t slab = apply_slab(slab_req);
     const uint64_t C = u.total_changes;
     if (C >= (1ULL << 32)) throw Invalid("2^32 or more changes in one update are not supported");
     Layout L;
@@ -463,6 +467,8 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
         if (numels[t] != u.tensors[t].numel) throw Invalid(u.tensors[t].name + ": numel mismatch");
         TensorDesc d = make_desc(targets[t], numels[t]);
         d.cold = (has_cache && has_cache[t]) ? 0u : 1u;
+        d.hist_in = hist_in ? hist_in[t] : nullptr;
+        d.hist_out = hist_out ? hist_out[t] : nullptr;
         L.descs.push_back(d);
         L.call_index.push_back((int32_t)t);
     }
@@ -562,7 +568,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
                   zz, local, blk_sum, bad};
     launch_decode(da, s);
     launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), s);
-    BlockArgs ba{d_groups, (uint32_t)G, bmap, d_descs, sizes, blk_prefix, local, zz, pv, tdelta, bad};
+    BlockArgs ba{d_groups, (uint32_t)G, slab, bmap, d_descs, sizes, blk_prefix, local, zz, pv, tdelta, bad};
     launch_local_fix(ba, B, s);
     uint32_t *wide = ar.get<uint32_t>(tiles);
     unsigned int *n_wide = ar.get<unsigned int>(1);
@@ -768,8 +774,27 @@ int32_t crx_apply(const crx_update *u, const uint8_t *payload_dev, uint16_t *con
     return guarded(err, errlen, [&] {
         if (!payload_dev && u->u.payload_len && !u->u.payload_host) throw Invalid("payload is not on the host");
         Arena ar{alloc, alloc_ctx};
-        apply(u->u, payload_dev, targets, numels, has_cache, cache_vals, slab, (hipStream_t)stream, ar, changed);
+        apply(u->u, payload_dev, targets, numels, has_cache, cache_vals, nullptr, nullptr, slab, (hipStream_t)stream, ar,
+              changed);
     });
+}
+
+int32_t crx_apply_cached(const crx_update *u, const uint8_t *payload_dev, uint16_t *const *targets,
+                         const uint64_t *numels, const int32_t *has_cache, const uint64_t *cache_vals,
+                         uint32_t *const *hist_in, uint32_t *const *hist_out, int32_t slab, void *stream,
+                         crx_alloc_fn alloc, void *alloc_ctx, uint64_t *changed, char *err, uint64_t errlen) {
+    *changed = 0;
+    return guarded(err, errlen, [&] {
+        if (!payload_dev && u->u.payload_len && !u->u.payload_host) throw Invalid("payload is not on the host");
+        Arena ar{alloc, alloc_ctx};
+        apply(u->u, payload_dev, targets, numels, has_cache, cache_vals, hist_in, hist_out, slab, (hipStream_t)stream,
+              ar, changed);
+    });
+}
+
+uint64_t crx_apply_hist_words(uint64_t numel, int32_t slab) {
+    const uint32_t sl = apply_slab(slab);
+    return (numel + sl - 1) / sl * 256;
 }
 
 int32_t crx_encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news, const uint64_t *numels,

@@ -32,6 +32,8 @@ struct TensorDesc {
     uint32_t tile_begin;        // first slab (global index)
     uint32_t n_tiles;
     uint32_t cold;              // 1: a full checksum is needed (new for encode, old for apply)
+    const uint32_t *hist_in;    // apply: [n_tiles][256] exponent counts of these weights, or null
+    uint32_t *hist_out;         // apply: receives the counts after the update, or null
 };
 
 // One (tensor, exponent) group.  Encode fills r0/rice/blk_base after the statistics pass;
@@ -138,7 +140,7 @@ struct SelectArgs {
 
 struct BlockArgs {                  // per-block kernels over the change list (one workgroup per block)
     const GroupDev *groups;
-    uint32_t n_groups;
+    uint32_t n_groups, slab;
     const uint32_t *bmap;           // [blocks] group of every block
     const TensorDesc *descs;
     const uint32_t *sizes;

@@ -322,6 +322,7 @@ __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau,
         }
     });
     wave_fence();
+    uint32_t *out = td.hist_out ? td.hist_out + (uint64_t)(tau - td.tile_begin) * 256 : nullptr;
     for (uint32_t k = ln; k < 256; k += 64) {
         uint32_t sum = 0;
 #pragma unroll
@@ -330,6 +331,7 @@ __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau,
             sum += h.x + h.y + h.z + h.w;
         }
         a.hall[(uint64_t)tau * 256 + k] = sum;
+        if (out) out[k] = sum;
     }
     facc = wave_sum(facc);
     if (ln == 0) a.full[tau] = facc;
@@ -339,6 +341,16 @@ __global__ __launch_bounds__(64) void k_hist(HistArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t hall[257 * kHistCopies];
     const uint32_t tau = blockIdx.x;
     const TensorDesc td = a.descs[a.tile_tensor[tau]];
+    if (td.hist_in && !td.cold) {  // counts recorded by the previous update of these weights
+        const uint64_t at = (uint64_t)(tau - td.tile_begin) * 256;
+        for (uint32_t k = lane(); k < 256; k += 64) {
+            const uint32_t v = td.hist_in[at + k];
+            a.hall[(uint64_t)tau * 256 + k] = v;
+            if (td.hist_out && td.hist_out != td.hist_in) td.hist_out[at + k] = v;
+        }
+        if (lane() == 0) a.full[tau] = 0;
+        return;
+    }
     const Slab sl = slab_of(td, tau - td.tile_begin, a.slab);
     for (uint32_t i = lane(); i < 257 * kHistCopies; i += 64) hall[i] = 0;
     wave_fence();
@@ -1304,6 +1316,15 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
             const uint32_t nu = (uint32_t)((int32_t)old + delta) & 0xFFFF;
             d = (uint64_t)((int64_t)nu - (int64_t)old) * weight(p);
             a.pv[j] = p | ((unsigned long long)nu << 32);
+            const uint32_t eo = (old >> 7) & 0xFF, en = (nu >> 7) & 0xFF;
+            if (eo != en) {  // the element moves between exponent counts of its slab
+                uint32_t *h = a.descs[gr.tensor].hist_out;
+                if (h) {
+                    h += (uint64_t)(p / a.slab) * 256;
+                    atomicSub(&h[eo], 1u);
+                    atomicAdd(&h[en], 1u);
+                }
+            }
         }
     }
     unsigned long long total;

@@ -94,6 +94,21 @@ int32_t crx_apply(const crx_update *u, const uint8_t *payload_dev, uint16_t *con
                   void *stream, crx_alloc_fn alloc, void *alloc_ctx, uint64_t *changed, char *err,
                   uint64_t errlen);
 
+/* crx_apply with the receiver's per-slab exponent counts kept across updates.  These counts change
+ * only when an element crosses a power of two, so the histogram pass (a full read of the weights)
+ * is skipped for tensors whose counts are known.  hist_in[i] (device, crx_apply_hist_words(numel,
+ * slab) u32, or NULL) holds tensor i's counts, valid only while its weights are unchanged since they
+ * were recorded and only with a trusted cached checksum (has_cache[i]); hist_out[i] (or NULL)
+ * receives the counts after this update (it may equal hist_in[i]).  On any status but CRX_OK the
+ * weights are untouched but hist_out may hold partial results: discard them.  No counterpart in
+ * the reference (its analogue is the checksum cache, codec.py:457-460,713-716). */
+int32_t crx_apply_cached(const crx_update *u, const uint8_t *payload_dev, uint16_t *const *targets,
+                         const uint64_t *numels, const int32_t *has_cache, const uint64_t *cache_vals,
+                         uint32_t *const *hist_in, uint32_t *const *hist_out, int32_t slab, void *stream,
+                         crx_alloc_fn alloc, void *alloc_ctx, uint64_t *changed, char *err, uint64_t errlen);
+/* Size in u32 of one tensor's counts for crx_apply_cached. */
+uint64_t crx_apply_hist_words(uint64_t numel, int32_t slab);
+
 /* ------------------------------------------------------------------ encode (device)
  * Replaces codec.encode (src/crukx_sync/codec.py:278-420): rank changes in stable exponent order,
  * gaps and residuals, per-group Rice parameters, one canonical Huffman table per exponent, bit

@@ -190,3 +190,48 @@ def test_qwen_layer_sized_round_trip_properties():
     assert send == {k: v[0] for k, v in rc.items()}
     for k in ("model.layers.0.mlp.down_proj.weight", "model.norm.weight"):
         assert send[k] == codec.checksum(prev[k])
+
+
+def test_receiver_exponent_counts_carried_across_updates():
+    """apply keeps per-slab exponent counts of the receiver's weights between updates (used only
+    with a checksum-cache hit): a chain with many binade crossings stays exact, an in-place edit of
+    one tensor drops its counts, and a rejected update drops them too."""
+    g = torch.Generator().manual_seed(7)
+    shapes = [("a", (300, 4097)), ("b", (70001,)), ("c", (64, 1024))]
+    cur = {n: (torch.randn(s, generator=g) * 0.02).to(torch.bfloat16) for n, s in shapes}
+    cur["c"][:, :8] = 0  # zeros step to subnormals: exponent moves from 0
+    recv = _cuda(cur)
+    send_chk, recv_chk = {}, {}
+    old_slab = codec._SLAB
+    codec._SLAB = 4096  # many slabs per tensor
+    try:
+        for step in range(8):
+            nxt = {}
+            for n, t in cur.items():
+                bits = t.view(torch.int16).clone()
+                m = torch.rand(bits.shape, generator=g) < 0.05
+                k = torch.randint(1, 300, bits.shape, generator=g, dtype=torch.int16)  # large steps: crossings
+                bits[m] = bits[m] + k[m]
+                nxt[n] = bits.view(torch.bfloat16)
+            upd = crukx_sync.encode_update(_cuda(cur), _cuda(nxt), send_chk)
+            crukx_sync.apply_update(recv, upd, recv_chk)
+            for n in nxt:
+                assert torch.equal(recv[n].cpu().view(torch.int16), nxt[n].view(torch.int16)), (step, n)
+            if step == 3:  # edit one receiver tensor in place: its counts and checksum are stale
+                recv["b"].add_(0)  # bumps the version, values unchanged
+            cur = nxt
+        assert send_chk == {k: v[0] for k, v in recv_chk.items()}
+        # an update made against other old weights fails verification in the device pass: the weights
+        # stay as they were and the counts of its tensors are forgotten
+        alt = {n: t.clone() for n, t in cur.items()}
+        alt["a"].view(torch.int16)[0, 0] += 1
+        nxt = {n: (t.view(torch.int16) + 1).view(torch.bfloat16) for n, t in alt.items()}
+        upd = crukx_sync.encode_update(_cuda(alt), _cuda(nxt), {})
+        before = {n: t.clone() for n, t in recv.items()}
+        with pytest.raises(crukx_sync.CorruptUpdate):
+            crukx_sync.apply_update(recv, upd, recv_chk)
+        for n in recv:
+            assert torch.equal(recv[n], before[n])
+            assert codec._hist_lookup(recv[n]) is None
+    finally:
+        codec._SLAB = old_slab
