@@ -340,16 +340,24 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     keep = checksums is not None and staged is targets
     hist_in, hist_out, bufs = [], [], []
     if keep:
-        for a, c in zip(targets, cache):
+        fresh = []  # tensors without usable counts: one allocation, sliced per tensor
+        for i, (a, c) in enumerate(zip(targets, cache)):
             e = _hist_lookup(a)
             if c is not None and e is not None and e[1] == a._version and e[2].device == dev:
-                buf = e[2]
-                hist_in.append(buf.data_ptr())
+                bufs.append(e[2])
             else:
-                buf = torch.empty(L.crx_apply_hist_words(a.numel(), int(_SLAB)), dtype=torch.int32, device=dev)
-                hist_in.append(0)
+                bufs.append(None)
+                fresh.append((i, L.crx_apply_hist_words(a.numel(), int(_SLAB))))
+        if fresh:
+            block = torch.empty(sum(w for _, w in fresh), dtype=torch.int32, device=dev)
+            at = 0
+            for i, w in fresh:
+                bufs[i] = block[at:at + w]
+                at += w
+        fresh_set = {i for i, _ in fresh}
+        for i, buf in enumerate(bufs):
+            hist_in.append(0 if i in fresh_set else buf.data_ptr())
             hist_out.append(buf.data_ptr())
-            bufs.append(buf)
     with torch.cuda.device(dev):
         rc = L.crx_apply_cached(u.handle, payload_dev or None, _native.ptr_array([a.data_ptr() for a in staged]),
                                 _native.u64_array([a.numel() for a in staged]), _native.i32_array(has),

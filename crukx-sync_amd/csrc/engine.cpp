@@ -518,6 +518,9 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
             blk += n_blocks(g.count);
         }
     const uint64_t G = groups.size(), B = blk;
+    std::vector<uint32_t> tensor_blk(T + 1, (uint32_t)B);  // first block of each tensor (its changes are contiguous)
+    for (int64_t gi = (int64_t)G - 1; gi >= 0; --gi) tensor_blk[groups[gi].tensor] = groups[gi].blk_base;
+    for (int64_t t = (int64_t)T - 1; t >= 0; --t) tensor_blk[t] = std::min(tensor_blk[t], tensor_blk[t + 1]);
 
     TensorDesc *d_descs = ar.get<TensorDesc>(T);
     h2d(d_descs, L.descs.data(), T, s);
@@ -559,16 +562,17 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     uint32_t *zz = ar.get<uint32_t>(C), *local = ar.get<uint32_t>(C);
     unsigned long long *pv = ar.get<unsigned long long>(C);
     unsigned long long *blk_sum = ar.get<unsigned long long>(B), *blk_prefix = ar.get<unsigned long long>(B + 1);
-    unsigned long long *tdelta = ar.get<unsigned long long>(T);
+    unsigned long long *tdelta = ar.get<unsigned long long>(T), *bdelta = ar.get<unsigned long long>(B);
+    uint32_t *tblk = ar.get<uint32_t>(T + 1);
+    h2d(tblk, tensor_blk.data(), T + 1, s);
     unsigned int *bad = ar.get<unsigned int>(1);
     uint32_t *lb = ar.get<uint32_t>((uint64_t)(tiles + 1) * 256);  // row tiles: read, never used
     zero(bad, 1, s);
-    zero(tdelta, T, s);
     DecodeArgs da{pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, bmap, sizes, d_lim, d_off, d_syms, (uint32_t)syms.size(),
                   zz, local, blk_sum, bad};
     launch_decode(da, s);
     launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), s);
-    BlockArgs ba{d_groups, (uint32_t)G, slab, bmap, d_descs, sizes, blk_prefix, local, zz, pv, tdelta, bad};
+    BlockArgs ba{d_groups, (uint32_t)G, slab, bmap, d_descs, sizes, blk_prefix, local, zz, pv, bdelta, bad};
     launch_local_fix(ba, B, s);
     uint32_t *wide = ar.get<uint32_t>(tiles);
     unsigned int *n_wide = ar.get<unsigned int>(1);
@@ -577,6 +581,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     launch_locate(sa, tiles, s);
     launch_select(sa, tiles, s);
     launch_verify(ba, B, s);
+    launch_range_sums(bdelta, tblk, T, tdelta, s);
 
     unsigned int hbad = 0;
     std::vector<unsigned long long> hdelta(T);

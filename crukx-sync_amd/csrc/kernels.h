@@ -148,7 +148,7 @@ struct BlockArgs {                  // per-block kernels over the change list (o
     uint32_t *local;
     const uint32_t *zz;
     unsigned long long *pv;         // [changes] element index | bits << 32
-    unsigned long long *tdelta;     // [tensors]
+    unsigned long long *bdelta;     // [blocks] checksum delta of each block's changes
     unsigned int *bad;
 };
 
@@ -175,6 +175,9 @@ uint64_t scan_parts(uint64_t n);
 void launch_scan_u64(const unsigned long long *in, uint64_t n, unsigned long long *out, unsigned long long *part,
                      hipStream_t s);
 void launch_scan_u32(const uint32_t *in, uint64_t n, unsigned long long *out, unsigned long long *part, hipStream_t s);
+// out[t] = sum of v[begin[t] .. begin[t + 1])
+void launch_range_sums(const unsigned long long *v, const uint32_t *begin, uint32_t n, unsigned long long *out,
+                       hipStream_t s);
 void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint64_t *per_tile, uint64_t *out,
                         hipStream_t s);
 void launch_decode(const DecodeArgs &a, hipStream_t s);

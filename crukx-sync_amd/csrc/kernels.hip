@@ -841,6 +841,17 @@ __global__ __launch_bounds__(256) void k_tensor_sums(const TensorDesc *descs, co
     if (threadIdx.x == 0) out[blockIdx.x] = total;
 }
 
+__global__ __launch_bounds__(256) void k_range_sums(const unsigned long long *v, const uint32_t *begin,
+                                                   unsigned long long *out) {
+    __shared__ unsigned long long sh[4];
+    const uint32_t b = begin[blockIdx.x], e = begin[blockIdx.x + 1];
+    unsigned long long s = 0;
+    for (uint32_t i = b + threadIdx.x; i < e; i += 256) s += v[i];
+    unsigned long long total;
+    block_exclusive_sum(s, sh, &total);
+    if (threadIdx.x == 0) out[blockIdx.x] = total;
+}
+
 // Full checksum of one tensor: each workgroup sums a contiguous range.
 __global__ __launch_bounds__(256) void k_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial,
                                                   uint32_t n_parts) {
@@ -1329,7 +1340,7 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
     }
     unsigned long long total;
     block_exclusive_sum(d, sh, &total);
-    if (s == 0) atomicAdd(&a.tdelta[gr.tensor], total);
+    if (s == 0) a.bdelta[b] = total;
 }
 
 __global__ __launch_bounds__(256) void k_scatter(BlockArgs a) {
@@ -1433,6 +1444,11 @@ void launch_scan_u64(const unsigned long long *in, uint64_t n, unsigned long lon
 
 void launch_scan_u32(const uint32_t *in, uint64_t n, unsigned long long *out, unsigned long long *part, hipStream_t s) {
     launch_scan("scan_u32", in, n, out, part, s);
+}
+
+void launch_range_sums(const unsigned long long *v, const uint32_t *begin, uint32_t n, unsigned long long *out,
+                       hipStream_t s) {
+    CRX_LAUNCH("range_sums", k_range_sums, n, 256, s, v, begin, out);
 }
 
 void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint64_t *per_tile, uint64_t *out,
