@@ -872,28 +872,17 @@ __global__ __launch_bounds__(256) void k_checksum(const uint32_t *frame, uint32_
 }
 
 // ================================================================== apply: block decode
-// One lane per block of up to 256 changes (blocks are independent: docs/FORMAT.md:41-44).  Per
-// change: unary run (count of leading ones, continued across 64-bit windows but never past the
-// block end or the group's bound q_max), a zero, `rice` remainder bits, then the canonical Huffman
-// code found by length with the first/count/base tables (codec.py:434-454).  Bits past the payload
-// read as zero.  Any violation raises the shared `bad` flag; nothing here can read out of bounds.
-// ================================================================== apply: block decode
 // One lane per 256-change block (codec.py:504-575), 64 consecutive blocks per wavefront.  The
 // wavefront's payload bits (contiguous: blocks are stored in order) are staged in LDS as
-// host-order 64-bit words, and so are the decoding symbols when they fit; every change then costs
-// two LDS reads of the stream and one of the symbol.  Code lengths come from comparisons of the
-// 17-bit peek with the canonical limits held in registers.  Outputs are staged per 16 changes and
-// written as 64-byte runs per block.
-constexpr uint32_t kDecPayWords = 4096;  // 32 KiB of payload per wavefront; more is read from HBM
-constexpr uint32_t kDecStage = 16;
+// host-order 64-bit words, and so are the decoding symbols when they fit.  A change normally costs
+// one 64-bit window of the stream (unary run, remainder and Huffman peek together) and one LDS read
+// of its symbol; code lengths come from comparisons of the 17-bit peek with the canonical limits
+// held in registers.  Each lane writes its block's outputs in order, so the lines fill in L2.
+constexpr uint32_t kDecPayWords = 3584;  // 28 KiB of payload per wavefront; more is read from HBM
 
 struct DecodeLds {
     uint64_t pay[kDecPayWords];
     uint32_t syms[kDecSyms];
-    uint32_t zz[64][kDecStage + 1];
-    uint32_t loc[64][kDecStage + 1];
-    uint32_t cnt[64];
-    unsigned long long eb[64];
 };
 
 // 64 bits of the stream from bit `pos`: LDS words [w0, ...) when staged, else HBM.
@@ -917,86 +906,68 @@ template <bool LDS_PAY, bool LDS_SYMS>
 __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
     const uint32_t ln = lane();
     const uint64_t b = (uint64_t)blockIdx.x * 64 + ln;
-    uint32_t cnt = 0, rice = 0, lim[17], off[17];
-    uint64_t eb = 0, size = 0, qmax = 0, cur = 0, end = 0;
-    bool bad = false;
-    if (b < a.n_blocks) {
-        const uint32_t g = a.bmap[b];
-        const GroupDev gr = a.groups[g];
-        const uint64_t kb = b - gr.blk_base;
-        cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
-        eb = (uint64_t)gr.elem_base + kb * 256;
-        size = a.sizes[(uint64_t)gr.tensor * 256 + gr.exponent];
-        rice = gr.rice;
-        qmax = size >> rice;
-        cur = a.block_off[b];
-        end = cur + a.block_bits[b];
-        bad = kb == 0 && gr.count > size;  // a group with more changes than elements
+    if (b >= a.n_blocks) return;
+    uint32_t lim[17], off[17];
+    const uint32_t g = a.bmap[b];
+    const GroupDev gr = a.groups[g];
+    const uint64_t kb = b - gr.blk_base;
+    const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
+    const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
+    const uint64_t size = a.sizes[(uint64_t)gr.tensor * 256 + gr.exponent];
+    const uint32_t rice = gr.rice;
+    const uint64_t qmax = size >> rice;
+    uint64_t cur = a.block_off[b];
+    const uint64_t end = cur + a.block_bits[b];
+    bool bad = kb == 0 && gr.count > size;  // a group with more changes than elements
 #pragma unroll
-        for (int l = 0; l < 17; ++l) {
-            lim[l] = a.lim[(uint64_t)gr.table * 17 + l];
-            off[l] = a.off[(uint64_t)gr.table * 17 + l];
-        }
-    } else {
-#pragma unroll
-        for (int l = 0; l < 17; ++l) lim[l] = off[l] = 0;
+    for (int l = 0; l < 17; ++l) {
+        lim[l] = a.lim[(uint64_t)gr.table * 17 + l];
+        off[l] = a.off[(uint64_t)gr.table * 17 + l];
     }
-    S.cnt[ln] = cnt;
-    S.eb[ln] = eb;
     uint64_t rel = 0;  // sum of (gap + 1) so far in this block
-    for (uint32_t s = 0; s < 256; ++s) {  // the same trip count on every lane: flushes are wave-wide
-        if (s < cnt && !bad) {
-            uint64_t q = 0;
+    for (uint32_t s = 0; s < cnt && !bad; ++s) {
+        uint64_t x = bits64<LDS_PAY>(a, S.pay, w0, cur);
+        uint64_t q;
+        if (~x) {  // the unary run ends inside this window
+            q = (uint64_t)__builtin_clzll(~x);
+        } else {
+            q = 64;
             for (;;) {
+                if (q > qmax || cur + q >= end) break;
                 const uint64_t y = ~bits64<LDS_PAY>(a, S.pay, w0, cur + q);
                 if (y) {
                     q += (uint64_t)__builtin_clzll(y);
                     break;
                 }
                 q += 64;
-                if (q > qmax || cur + q >= end) break;
-            }
-            const uint64_t c = cur + q + 1;
-            const uint64_t x = bits64<LDS_PAY>(a, S.pay, w0, c);
-            const uint64_t rem = rice ? x >> (64 - rice) : 0ULL;
-            const uint32_t peek = (uint32_t)((x << rice) >> (64 - 17));
-            uint32_t L = 1, o = 0;
-#pragma unroll
-            for (int l = 0; l < 17; ++l) L += lim[l] <= peek ? 1u : 0u;  // lim is non-decreasing
-#pragma unroll
-            for (int l = 0; l < 17; ++l) o = L == (uint32_t)(l + 1) ? off[l] : o;
-            const uint32_t idx = o + (L <= 17 ? peek >> (17 - L) : 0u);
-            const uint64_t gap = (q << rice) | rem;
-            if (q > qmax || cur + q >= end || L > 17 || gap >= size) {
-                bad = true;
-            } else {
-                rel += gap + 1;
-                const uint32_t si = min(idx, a.n_syms - 1);
-                S.zz[ln][s & (kDecStage - 1)] = LDS_SYMS ? S.syms[si] : a.syms[si];
-                S.loc[ln][s & (kDecStage - 1)] = (uint32_t)min<uint64_t>(rel - 1, 0xFFFFFFFFULL);
-                cur = c + rice + L;
             }
         }
-        if ((s & (kDecStage - 1)) == kDecStage - 1) {  // write 16 changes of every block: 4 blocks per store
-            wave_fence();
-            const uint32_t s0 = s + 1 - kDecStage, e = ln & (kDecStage - 1);
-#pragma unroll 4
-            for (uint32_t i = 0; i < 64; i += 4) {
-                const uint32_t blk = i + (ln >> 4);
-                if (s0 + e < S.cnt[blk]) {
-                    const uint64_t j = S.eb[blk] + s0 + e;
-                    a.zz[j] = S.zz[blk][e];
-                    a.local[j] = S.loc[blk][e];
-                }
-            }
-            wave_fence();
+        const uint64_t c = cur + q + 1;
+        // remainder and Huffman peek: from the same window when they fit in it, else a new read
+        if (q + 1 + rice + 17 <= 64) x <<= (q + 1);
+        else x = bits64<LDS_PAY>(a, S.pay, w0, c);
+        const uint64_t rem = rice ? x >> (64 - rice) : 0ULL;
+        const uint32_t peek = (uint32_t)((x << rice) >> (64 - 17));
+        uint32_t L = 1, o = 0;
+#pragma unroll
+        for (int l = 0; l < 17; ++l) L += lim[l] <= peek ? 1u : 0u;  // lim is non-decreasing
+#pragma unroll
+        for (int l = 0; l < 17; ++l) o = L == (uint32_t)(l + 1) ? off[l] : o;
+        const uint32_t idx = o + (L <= 17 ? peek >> (17 - L) : 0u);
+        const uint64_t gap = (q << rice) | rem;
+        if (q > qmax || cur + q >= end || L > 17 || gap >= size) {
+            bad = true;
+        } else {
+            rel += gap + 1;
+            const uint32_t si = min(idx, a.n_syms - 1);
+            a.zz[eb + s] = LDS_SYMS ? S.syms[si] : a.syms[si];
+            a.local[eb + s] = (uint32_t)min<uint64_t>(rel - 1, 0xFFFFFFFFULL);
+            cur = c + rice + L;
         }
     }
-    if (b < a.n_blocks) {
-        if (!bad && cur != end) bad = true;
-        a.blk_sum[b] = rel;
-        if (bad) atomicOr(a.bad, kBadDecode);
-    }
+    if (!bad && cur != end) bad = true;
+    a.blk_sum[b] = rel;
+    if (bad) atomicOr(a.bad, kBadDecode);
 }
 
 template <bool LDS_SYMS>
@@ -1080,9 +1051,26 @@ constexpr uint32_t kTgtCap = 1024;  // targets per slab held in LDS; more are re
 constexpr uint32_t kWin = 32;       // exponent window of the common kernel
 constexpr uint32_t kSpare = 16;     // spare counters for elements outside the window
 
+constexpr uint32_t kSelCopies = 4;  // copies of each running count (power of two, 2..8; 4 measured best)
+
+// sum of the copies of count c
+__device__ __forceinline__ uint32_t sel_count(const uint32_t *cnt, uint32_t c) {
+    if (kSelCopies == 2) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(&cnt[2 * c]);
+        return v.x + v.y;
+    }
+    uint32_t s = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < kSelCopies; q += 4) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(&cnt[kSelCopies * c + q]);
+        s += v.x + v.y + v.z + v.w;
+    }
+    return s;
+}
+
 template <uint32_t W>
 struct SelectLds {
-    uint32_t cnt[(W + kSpare) * 4];  // running counts, 4 copies (lane & 3)
+    uint32_t cnt[(W + kSpare) * kSelCopies];  // running counts, kSelCopies copies (by lane)
     uint2 next[W + kSpare];          // per exponent: {rank of the next target, its list index}
     uint2 range[W];                  // per exponent: {end of its list, group-local index - list index}
     uint32_t pre[W];                 // exponent count before the slab (targets read from HBM only)
@@ -1093,7 +1081,7 @@ struct SelectLds {
 template <uint32_t W, bool LDS_LIST>
 __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase,
                             SelectLds<W> &S) {
-    const uint32_t ln = lane(), rep = ln & 3, spare = W + (ln >> 2);
+    const uint32_t ln = lane(), rep = ln & (kSelCopies - 1), spare = W + (ln >> 2);
     const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
     stream_rows<kSelectRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
         // window index of each exponent; outside the window (or the slab): a spare counter
@@ -1103,12 +1091,10 @@ __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Sla
             if (f < sl.f_lo || f >= sl.f_hi) c0 = spare;
             if (f + 1 < sl.f_lo || f + 1 >= sl.f_hi) c1 = spare;
         }
-        atomicAdd(&S.cnt[4 * c0 + rep], 1u);
-        atomicAdd(&S.cnt[4 * c1 + rep], 1u);
-        const uint4 a0 = *reinterpret_cast<const uint4 *>(&S.cnt[4 * c0]);
-        const uint4 a1 = *reinterpret_cast<const uint4 *>(&S.cnt[4 * c1]);
+        atomicAdd(&S.cnt[kSelCopies * c0 + rep], 1u);
+        atomicAdd(&S.cnt[kSelCopies * c1 + rep], 1u);
+        const uint32_t s0 = sel_count(S.cnt, c0), s1 = sel_count(S.cnt, c1);
         const uint2 q0 = S.next[c0], q1 = S.next[c1];
-        const uint32_t s0 = a0.x + a0.y + a0.z + a0.w, s1 = a1.x + a1.y + a1.z + a1.w;
         uint64_t H0 = ballot(s0 > q0.x), H1 = ballot(s1 > q1.x);
         if (!(H0 | H1)) return;
         wave_fence();
@@ -1278,7 +1264,7 @@ __device__ void select_tile(const SelectArgs &a, uint32_t tau, SelectLds<W> &S) 
     }
     if (ln < kSpare) S.next[W + ln] = make_uint2((uint32_t)kFar, 0u);
     wave_fence();
-    for (uint32_t i = ln; i < (W + kSpare) * 4; i += 64) S.cnt[i] = 0;
+    for (uint32_t i = ln; i < (W + kSpare) * kSelCopies; i += 64) S.cnt[i] = 0;
     wave_fence();
     const Slab sl = slab_of(td, local_tile, a.slab);
     if (in_lds) select_slab<W, true>(a, td, sl, kbase, S);
