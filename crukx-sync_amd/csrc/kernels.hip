@@ -27,6 +27,8 @@ __device__ __forceinline__ uint64_t weight(uint64_t i) {
 }
 
 __device__ __forceinline__ uint32_t lane() { return __lane_id(); }
+// 64-bit integer min (the generic min template of the HIP headers goes through double precision)
+__device__ __forceinline__ uint64_t min64(uint64_t a, uint64_t b) { return a < b ? a : b; }
 // Orders this wavefront's LDS accesses in the compiler's view without waiting on outstanding memory
 // operations (LDS instructions of one wavefront execute in order).  The streaming kernels run one
 // wavefront per workgroup, so a workgroup barrier would only drain the rows loaded ahead.
@@ -611,7 +613,7 @@ __device__ __forceinline__ uint32_t huff_entry(const CodeArgs &a, uint32_t e, ui
 __device__ void thread_codes(const CodeArgs &a, const uint64_t *rec, uint64_t wbase, ThreadCodes &tc) {
     const uint32_t t = threadIdx.x;
     const uint64_t ib = wbase + (uint64_t)t * kElemsPerThread;
-    tc.n = ib < a.n ? (uint32_t)min<uint64_t>(kElemsPerThread, a.n - ib) : 0u;
+    tc.n = ib < a.n ? (uint32_t)min64(kElemsPerThread, a.n - ib) : 0u;
     uint32_t g = tc.n ? a.cmap[ib / kElemsPerThread] : 0u;
     GroupDev gr = a.groups[g];
     uint64_t gend = (uint64_t)gr.elem_base + gr.count;
@@ -891,7 +893,7 @@ __device__ __forceinline__ uint64_t bits64(const DecodeArgs &a, const uint64_t *
     const uint32_t s = (uint32_t)(pos & 63);
     uint64_t hi, lo;
     if (LDS) {
-        const uint32_t w = (uint32_t)min<uint64_t>((pos >> 6) - w0, kDecPayWords - 2);
+        const uint32_t w = (uint32_t)min64((pos >> 6) - w0, kDecPayWords - 2);
         hi = W[w];
         lo = W[w + 1];
     } else {
@@ -911,7 +913,7 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
     const uint32_t g = a.bmap[b];
     const GroupDev gr = a.groups[g];
     const uint64_t kb = b - gr.blk_base;
-    const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
+    const uint32_t cnt = (uint32_t)min64(256, gr.count - kb * 256);
     const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
     const uint64_t size = a.sizes[(uint64_t)gr.tensor * 256 + gr.exponent];
     const uint32_t rice = gr.rice;
@@ -948,12 +950,24 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
         else x = bits64<LDS_PAY>(a, S.pay, w0, c);
         const uint64_t rem = rice ? x >> (64 - rice) : 0ULL;
         const uint32_t peek = (uint32_t)((x << rice) >> (64 - 17));
-        uint32_t L = 1, o = 0;
+        // code length: 1 + #{l : lim[l] <= peek} (lim is non-decreasing), summed as a tree; then the
+        // symbol index base off[L - 1] through a 5-level select tree (short dependency chains)
+        uint32_t t[17];
 #pragma unroll
-        for (int l = 0; l < 17; ++l) L += lim[l] <= peek ? 1u : 0u;  // lim is non-decreasing
+        for (int l = 0; l < 17; ++l) t[l] = lim[l] <= peek ? 1u : 0u;
 #pragma unroll
-        for (int l = 0; l < 17; ++l) o = L == (uint32_t)(l + 1) ? off[l] : o;
-        const uint32_t idx = o + (L <= 17 ? peek >> (17 - L) : 0u);
+        for (int w = 1; w < 17; w <<= 1)
+#pragma unroll
+            for (int l = 0; l + w < 17; l += 2 * w) t[l] += t[l + w];
+        const uint32_t L = 1 + t[0], li = L - 1;
+        uint32_t o[17];
+#pragma unroll
+        for (int l = 0; l < 17; ++l) o[l] = off[l];
+#pragma unroll
+        for (int w = 1; w < 17; w <<= 1)
+#pragma unroll
+            for (int l = 0; l + w < 17; l += 2 * w) o[l] = (li & w) ? o[l + w] : o[l];
+        const uint32_t idx = o[0] + (L <= 17 ? peek >> (17 - L) : 0u);
         const uint64_t gap = (q << rice) | rem;
         if (q > qmax || cur + q >= end || L > 17 || gap >= size) {
             bad = true;
@@ -961,7 +975,7 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
             rel += gap + 1;
             const uint32_t si = min(idx, a.n_syms - 1);
             a.zz[eb + s] = LDS_SYMS ? S.syms[si] : a.syms[si];
-            a.local[eb + s] = (uint32_t)min<uint64_t>(rel - 1, 0xFFFFFFFFULL);
+            a.local[eb + s] = (uint32_t)min64(rel - 1, 0xFFFFFFFFULL);
             cur = c + rice + L;
         }
     }
@@ -975,10 +989,10 @@ __global__ __launch_bounds__(64) void k_decode(DecodeArgs a) {
     __shared__ __attribute__((aligned(16))) DecodeLds S;
     const uint32_t ln = lane();
     const uint64_t b0 = (uint64_t)blockIdx.x * 64;
-    const uint64_t nb = min<uint64_t>(64, a.n_blocks - b0);
+    const uint64_t nb = min64(64, a.n_blocks - b0);
     // this wavefront's bits [block_off[b0], block_off[b0 + nb]) lie in words [w0, wend)
     const uint64_t w0 = a.block_off[b0] >> 6;
-    const uint64_t wend = min<uint64_t>(a.n_words, ((a.block_off[b0 + nb] + 63) >> 6) + 2);
+    const uint64_t wend = min64(a.n_words, ((a.block_off[b0 + nb] + 63) >> 6) + 2);
     const bool lds_pay = wend > w0 && wend - w0 <= kDecPayWords;
     if (lds_pay)
         for (uint64_t w = w0 + ln; w < wend; w += 64) S.pay[w - w0] = __builtin_bswap64(a.payload[w]);
@@ -997,7 +1011,7 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
     const uint32_t g = a.bmap[b];
     const GroupDev gr = a.groups[g];
     const uint64_t kb = b - gr.blk_base;
-    const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
+    const uint32_t cnt = (uint32_t)min64(256, gr.count - kb * 256);
     const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
     const uint64_t size = a.sizes[(uint64_t)gr.tensor * 256 + gr.exponent];
     const unsigned long long base = a.blk_prefix[b] - a.blk_prefix[gr.blk_base];
@@ -1005,7 +1019,7 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
     if (s < cnt) {
         const unsigned long long local = base + a.local[eb + s];
         if (local >= size) atomicOr(a.bad, kBadLocal);
-        a.local[eb + s] = (uint32_t)min<unsigned long long>(local, 0xFFFFFFFFULL);
+        a.local[eb + s] = (uint32_t)min64(local, 0xFFFFFFFFULL);
         a.pv[eb + s] = kNone;
     }
 }
@@ -1296,7 +1310,7 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
     const uint32_t g = a.bmap[b];
     const GroupDev gr = a.groups[g];
     const uint64_t kb = b - gr.blk_base;
-    const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
+    const uint32_t cnt = (uint32_t)min64(256, gr.count - kb * 256);
     const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
     const uint32_t s = threadIdx.x;
     unsigned long long d = 0;
@@ -1334,7 +1348,7 @@ __global__ __launch_bounds__(256) void k_scatter(BlockArgs a) {
     const uint32_t g = a.bmap[b];
     const GroupDev gr = a.groups[g];
     const uint64_t kb = b - gr.blk_base;
-    const uint32_t cnt = (uint32_t)min<uint64_t>(256, gr.count - kb * 256);
+    const uint32_t cnt = (uint32_t)min64(256, gr.count - kb * 256);
     const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
     const uint32_t s = threadIdx.x;
     if (s < cnt) {
