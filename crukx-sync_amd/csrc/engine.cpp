@@ -2,7 +2,6 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <cstdio>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -572,12 +571,13 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
                   zz, local, blk_sum, bad};
     launch_decode(da, s);
     launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), s);
-    BlockArgs ba{d_groups, (uint32_t)G, slab, bmap, d_descs, sizes, blk_prefix, local, zz, pv, bdelta, bad};
+    BlockArgs ba{d_groups, (uint32_t)G, slab, bmap, d_descs, sizes, blk_prefix, local, zz, pv, bdelta, bad, B};
     launch_local_fix(ba, B, s);
-    uint32_t *wide = ar.get<uint32_t>(tiles);
-    unsigned int *n_wide = ar.get<unsigned int>(1);
-    zero(n_wide, 1, s);
-    SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, pv, bad, wide, n_wide};
+    uint2 *more = ar.get<uint2>(3 * (uint64_t)tiles);  // at most 3 windows after the first per slab
+    unsigned int *n_more = ar.get<unsigned int>(1);
+    zero(n_more, 1, s);
+    SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, pv, bad, more, n_more,
+                  std::min(1024u, 3 * tiles)};
     launch_locate(sa, tiles, s);
     launch_select(sa, tiles, s);
     launch_verify(ba, B, s);

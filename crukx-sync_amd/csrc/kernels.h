@@ -134,8 +134,9 @@ struct SelectArgs {
     const uint32_t *local;          // group-local index of every change
     unsigned long long *pv;         // [changes] element index | bits << 32 (old, then new bits)
     const unsigned int *bad;
-    uint32_t *wide;                 // [tiles] slabs left to the all-exponent select kernel
-    unsigned int *n_wide;           // their number (zero before the select pass)
+    uint2 *more;                    // [3 tiles] (slab, first exponent) of windows after a slab's first
+    unsigned int *n_more;           // their number (zero before k_locate)
+    uint32_t n_front;               // listed windows taken by the front blocks of the select pass
 };
 
 struct BlockArgs {                  // per-block kernels over the change list (one workgroup per block)
@@ -150,6 +151,7 @@ struct BlockArgs {                  // per-block kernels over the change list (o
     unsigned long long *pv;         // [changes] element index | bits << 32
     unsigned long long *bdelta;     // [blocks] checksum delta of each block's changes
     unsigned int *bad;
+    uint64_t n_blocks;
 };
 
 void launch_enc_rank(const EncRankArgs &a, uint32_t tiles, hipStream_t s);

@@ -1003,76 +1003,142 @@ __global__ __launch_bounds__(64) void k_decode(DecodeArgs a) {
     else decode_blocks<false, LDS_SYMS>(a, S, w0);
 }
 
+// Change blocks handled by one workgroup of the per-block kernels (fewer, longer workgroups; their
+// loads are issued together).
+constexpr uint32_t kBlocksPerWG = 4;
+
+// Where the per-block kernels find block b's changes: [eb, eb + cnt) of its group g.
+struct BlockRef {
+    uint32_t g, cnt;
+    uint64_t eb;
+};
+__device__ __forceinline__ BlockRef block_ref(const BlockArgs &a, uint64_t b, GroupDev &gr) {
+    BlockRef r{0, 0, 0};
+    if (b < a.n_blocks) {
+        r.g = a.bmap[b];
+        gr = a.groups[r.g];
+        const uint64_t kb = b - gr.blk_base;
+        r.cnt = (uint32_t)min64(256, gr.count - kb * 256);
+        r.eb = (uint64_t)gr.elem_base + kb * 256;
+    }
+    return r;
+}
+
 // local = (sum of (gap + 1) over earlier blocks of the group) + block-relative local; must stay
 // below the group size (codec.py:640-642,696-697).
 __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
     if (*a.bad) return;
-    const uint64_t b = blockIdx.x;
-    const uint32_t g = a.bmap[b];
-    const GroupDev gr = a.groups[g];
-    const uint64_t kb = b - gr.blk_base;
-    const uint32_t cnt = (uint32_t)min64(256, gr.count - kb * 256);
-    const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
-    const uint64_t size = a.sizes[(uint64_t)gr.tensor * 256 + gr.exponent];
-    const unsigned long long base = a.blk_prefix[b] - a.blk_prefix[gr.blk_base];
     const uint32_t s = threadIdx.x;
-    if (s < cnt) {
-        const unsigned long long local = base + a.local[eb + s];
-        if (local >= size) atomicOr(a.bad, kBadLocal);
-        a.local[eb + s] = (uint32_t)min64(local, 0xFFFFFFFFULL);
-        a.pv[eb + s] = kNone;
+    GroupDev gr[kBlocksPerWG];
+    BlockRef r[kBlocksPerWG];
+    unsigned long long base[kBlocksPerWG];
+    uint64_t size[kBlocksPerWG];
+    uint32_t raw[kBlocksPerWG];
+#pragma unroll
+    for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
+        const uint64_t b = (uint64_t)blockIdx.x * kBlocksPerWG + u;
+        r[u] = block_ref(a, b, gr[u]);
+        if (r[u].cnt) {
+            size[u] = a.sizes[(uint64_t)gr[u].tensor * 256 + gr[u].exponent];
+            base[u] = a.blk_prefix[b] - a.blk_prefix[gr[u].blk_base];
+        }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kBlocksPerWG; ++u)
+        if (s < r[u].cnt) raw[u] = a.local[r[u].eb + s];
+#pragma unroll
+    for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
+        if (s < r[u].cnt) {
+            const unsigned long long local = base[u] + raw[u];
+            if (local >= size[u]) atomicOr(a.bad, kBadLocal);
+            a.local[r[u].eb + s] = (uint32_t)min64(local, 0xFFFFFFFFULL);
+            a.pv[r[u].eb + s] = kNone;
+        }
     }
 }
 
 // For every (slab, exponent): the first change of the group whose local index is at or after the
-// number of same-exponent elements before the slab.
+// number of same-exponent elements before the slab.  Also lists the slab's exponent windows after
+// its first one (the select pass streams the slab once per window): windows of kSelWin exponents,
+// each starting at the lowest exponent with targets past the previous window.
+constexpr uint32_t kSelWin = 64;
 __global__ __launch_bounds__(256) void k_locate(SelectArgs a) {
+    __shared__ uint64_t hasm[4];
     if (*a.bad) return;
     const uint32_t tau = blockIdx.x, k = threadIdx.x;
     const uint32_t t = a.tile_tensor[tau];
     const int32_t g = a.group_of[(uint64_t)t * 256 + k];
     uint32_t lb = kNone;
+    bool has = false;  // targets of exponent k in this slab
     if (g >= 0) {
         const GroupDev gr = a.groups[g];
         const uint32_t target = a.pre[(uint64_t)tau * 256 + k];
-        uint32_t lo = gr.elem_base, hi = gr.elem_base + gr.count;
+        const uint32_t tb = a.descs[t].tile_begin, nt = a.descs[t].n_tiles;
+        const bool last = tau + 1 >= tb + nt;
+        const uint32_t next = last ? kNone : a.pre[(uint64_t)(tau + 1) * 256 + k];
+        uint32_t lo = gr.elem_base, hi = gr.elem_base + gr.count, vhi = kNone;  // vhi = local[hi]
         while (lo < hi) {
-            uint32_t mid = lo + ((hi - lo) >> 1);
-            if (a.local[mid] < target) lo = mid + 1;
-            else hi = mid;
+            const uint32_t mid = lo + ((hi - lo) >> 1), v = a.local[mid];
+            if (v < target) {
+                lo = mid + 1;
+            } else {
+                hi = mid;
+                vhi = v;
+            }
         }
         lb = lo;
+        has = lo < gr.elem_base + gr.count && (last || vhi < next);
     }
     ((uint32_t *)a.lb)[(uint64_t)tau * 256 + k] = lb;
+    const uint64_t m = ballot(has);
+    if (lane() == 0) hasm[k >> 6] = m;
+    __syncthreads();
+    if (k == 0) {
+        // bit e of the 256-bit mask: exponent e has targets; windows greedy from the lowest
+        const uint64_t w[4] = {hasm[0], hasm[1], hasm[2], hasm[3]};
+        auto first_at = [&](uint32_t from) -> uint32_t {  // lowest set bit at or past `from` (256: none)
+            for (uint32_t q = from >> 6; q < 4; ++q) {
+                const uint64_t v = q == (from >> 6) ? w[q] & (~0ULL << (from & 63)) : w[q];
+                if (v) return 64 * q + (uint32_t)__builtin_ctzll(v);
+            }
+            return 256u;
+        };
+        uint32_t kb = first_at(0);
+        while (kb < 256 - kSelWin) {
+            kb = first_at(kb + kSelWin);
+            if (kb < 256) a.more[atomicAdd(a.n_more, 1u)] = make_uint2(tau, kb);
+        }
+    }
 }
 
 // ================================================================== apply: select pass
 // One wavefront per slab.  The slab's targets (group-local indices of its changes, minus the
 // exponent's count before the slab = ranks within the slab) are copied to LDS, per exponent in
-// order.  Streaming the slab, every element adds one to its exponent's count (4 copies by lane, few
-// same-address conflicts) and reads back the total with the exponent's next target: when the total
-// passes it, targets lie in this row.  The row's elements of that exponent are then published in
-// LDS by in-row rank (stable: ballots and mbcnt), and the targets, one per lane, read their element
-// there.
+// order.  The slab is streamed once per window of kWin consecutive exponents holding targets
+// (normally one window covers them all).  Every element adds one to its exponent's running count
+// (kSelCopies copies, by lane, so few lanes share an address); elements outside the window go to a
+// spare counter no other lane uses.  Lane e owns window exponent e: it sums that exponent's copies
+// and compares the total with the exponent's next target, so one ballot names the exponents with
+// targets in the row.  For each of them, ballots and mbcnt give every element of that exponent its
+// stable in-row rank, and the target's element is the one whose rank matches.  A row with more
+// targets of one exponent publishes that exponent's elements in LDS by rank and takes the rest of
+// its targets one per lane.
 //
-// The pass is bound by LDS latency, so the LDS footprint sets the speed through occupancy.  Only
-// exponents with targets in the slab need counting; they normally span a few consecutive values, so
-// the common kernel keeps state for a window of kWin exponents starting at the slab's lowest target
-// exponent and sends every other element to one of 16 spare counters (by lane, so the spare counts
-// never conflict).  Slabs whose target exponents span more than kWin values go to a second kernel
-// with state for all 256.
-constexpr uint32_t kTgtCap = 1024;  // targets per slab held in LDS; more are read from HBM
-constexpr uint32_t kWin = 32;       // exponent window of the common kernel
-constexpr uint32_t kSpare = 16;     // spare counters for elements outside the window
+// The pass is bound by instruction issue and LDS latency: per-row instructions and the LDS footprint
+// (occupancy) set its speed.  The per-row path is six packed-16-bit and address operations, two LDS
+// atomics, one LDS read and one compare.
+constexpr uint32_t kTgtCap = 1024;            // targets per window held in LDS; more are read from HBM
+constexpr uint32_t kWin = kSelWin;           // exponents per window: one per lane
+constexpr uint32_t kSelCopies = 4;            // copies of each running count (4 or 8)
+constexpr uint32_t kSpare = 64 / kSelCopies;  // spare counters: lane l uses copy l % kSelCopies of spare l / kSelCopies
+constexpr uint32_t kCntShift = kSelCopies == 4 ? 3 : 2;  // (window index << 7) >> kCntShift = counter byte offset
+static_assert(kSelCopies == 4 || kSelCopies == 8, "kSelCopies");
 
-constexpr uint32_t kSelCopies = 4;  // copies of each running count (power of two, 2..8; 4 measured best)
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u16x2 as16(uint32_t v) { return __builtin_bit_cast(u16x2, v); }
 
 // sum of the copies of count c
 __device__ __forceinline__ uint32_t sel_count(const uint32_t *cnt, uint32_t c) {
-    if (kSelCopies == 2) {
-        const uint2 v = *reinterpret_cast<const uint2 *>(&cnt[2 * c]);
-        return v.x + v.y;
-    }
     uint32_t s = 0;
 #pragma unroll
     for (uint32_t q = 0; q < kSelCopies; q += 4) {
@@ -1082,91 +1148,110 @@ __device__ __forceinline__ uint32_t sel_count(const uint32_t *cnt, uint32_t c) {
     return s;
 }
 
-template <uint32_t W>
 struct SelectLds {
-    uint32_t cnt[(W + kSpare) * kSelCopies];  // running counts, kSelCopies copies (by lane)
-    uint2 next[W + kSpare];          // per exponent: {rank of the next target, its list index}
-    uint2 range[W];                  // per exponent: {end of its list, group-local index - list index}
-    uint32_t pre[W];                 // exponent count before the slab (targets read from HBM only)
-    alignas(16) uint16_t list[kTgtCap];  // slab ranks of the targets (slab <= 65536), per exponent in order
-    uint32_t slot[2 * kRow];         // in-row rank -> (in-row offset << 16) | bits; [kRow, 2 kRow): per lane, unused
+    uint32_t cnt[(kWin + kSpare) * kSelCopies];  // running counts, kSelCopies copies (by lane)
+    alignas(16) uint16_t list[kTgtCap];            // slab ranks of the window's targets, per exponent in order
+    union {
+        uint32_t slot[2 * kRow];  // streaming: in-row rank -> (in-row offset << 16) | bits; [kRow, 2 kRow): per lane
+        uint4 info[kWin];         // set-up, per window exponent: {list begin, list end, change index - list
+                                  // index, exponent count before the slab}
+    };
 };
 
-template <uint32_t W, bool LDS_LIST>
-__device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase,
-                            SelectLds<W> &S) {
-    const uint32_t ln = lane(), rep = ln & (kSelCopies - 1), spare = W + (ln >> 2);
+template <bool LDS_LIST>
+__device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase, SelectLds &S,
+                            uint32_t nxt, uint32_t nix, const uint32_t end, const uint32_t jofs, const uint32_t pre_k) {
+    // lane e, for window exponent e: nxt = slab rank of its next target (kFar: none left), nix = that
+    // target's list index, end = end of its list, jofs = change index - list index, pre_k = its count
+    // before the slab (HBM list only)
+    const uint32_t ln = lane(), rep4 = (ln & (kSelCopies - 1)) * 4u;
+    const uint32_t kb = (kbase << 7) * 0x10001u, sp = ((kWin + ln / kSelCopies) << 7) * 0x10001u;
+    char *const cnt = reinterpret_cast<char *>(S.cnt);
+    // slab rank of list entry i of the exponent whose offsets are (jo, pr); i below the list's end
+    auto target = [&](uint32_t i, uint32_t jo, uint32_t pr) -> uint32_t {
+        if (LDS_LIST) return S.list[min(i, kTgtCap - 1)];
+        return a.local[jo + i] - pr;
+    };
     const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
     stream_rows<kSelectRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
-        // window index of each exponent; outside the window (or the slab): a spare counter
-        uint32_t c0 = min(((o >> 7) & 0xFF) - kbase, spare), c1 = min(((o >> 23) & 0xFF) - kbase, spare);
+        // window index << 7 of both elements (16-bit halves); outside the window or the slab: the spare
+        u16x2 c = __builtin_elementwise_min(as16(o & 0x7F807F80u) - as16(kb), as16(sp));
         if (!row_full(sl, r)) {
             const uint32_t f = r * kRow + 2 * ln;
-            if (f < sl.f_lo || f >= sl.f_hi) c0 = spare;
-            if (f + 1 < sl.f_lo || f + 1 >= sl.f_hi) c1 = spare;
+            if (f < sl.f_lo || f >= sl.f_hi) c.x = as16(sp).x;
+            if (f + 1 < sl.f_lo || f + 1 >= sl.f_hi) c.y = as16(sp).y;
         }
-        atomicAdd(&S.cnt[kSelCopies * c0 + rep], 1u);
-        atomicAdd(&S.cnt[kSelCopies * c1 + rep], 1u);
-        const uint32_t s0 = sel_count(S.cnt, c0), s1 = sel_count(S.cnt, c1);
-        const uint2 q0 = S.next[c0], q1 = S.next[c1];
-        uint64_t H0 = ballot(s0 > q0.x), H1 = ballot(s1 > q1.x);
-        if (!(H0 | H1)) return;
+        const u16x2 ad = c >> (unsigned short)kCntShift;
+        atomicAdd(reinterpret_cast<uint32_t *>(cnt + ((uint32_t)ad.x | rep4)), 1u);
+        atomicAdd(reinterpret_cast<uint32_t *>(cnt + ((uint32_t)ad.y | rep4)), 1u);
+        const uint32_t s = sel_count(S.cnt, ln);  // exponent ln's count up to the row's end
+        uint64_t H = ballot(s > nxt);
+        if (!H) return;
         wave_fence();
+        const uint32_t c0 = c.x, c1 = c.y;
         do {  // once per exponent with targets in this row
-            // a lane whose element of that exponent triggered: its count, and the next target's index
-            const uint32_t l = (uint32_t)__builtin_ctzll(H0 | H1);
-            const bool use0 = (H0 >> l) & 1;
-            const uint32_t k = rdlane(use0 ? c0 : c1, l);
-            const uint32_t after = rdlane(use0 ? s0 : s1, l);  // exponent-k count up to the row's end
-            uint32_t i = rdlane(use0 ? q0.y : q1.y, l);
-            const bool m0 = c0 == k, m1 = c1 == k;
+            const uint32_t k = (uint32_t)__builtin_ctzll(H);
+            const uint32_t after = rdlane(s, k), ke = rdlane(end, k), jo = rdlane(jofs, k);
+            const uint32_t pr = LDS_LIST ? 0u : rdlane(pre_k, k);
+            uint32_t tc = rdlane(nxt, k), i = rdlane(nix, k);
+            const bool m0 = c0 == (k << 7), m1 = c1 == (k << 7);
             const uint64_t M0 = ballot(m0), M1 = ballot(m1);
             const uint32_t seen = after - (uint32_t)(__popcll(M0) + __popcll(M1));  // ... before this row
-            const uint32_t rr0 = mbcnt(M0) + mbcnt(M1);
-            // publish by in-row rank; other lanes write a slot of their own past the ranks
-            S.slot[m0 ? rr0 : kRow + ln] = ((2 * ln) << 16) | (o & 0xFFFF);
-            S.slot[m1 ? rr0 + (m0 ? 1u : 0u) : kRow + ln] = ((2 * ln + 1) << 16) | (o >> 16);
-            const uint2 rg = S.range[k];
-            wave_fence();
-            uint32_t n, tc;
-            do {  // this row's targets of exponent k, one per lane (64 more if all lanes take one)
-                const uint32_t j = i + ln;
-                if (LDS_LIST) {
-                    const uint32_t lv = S.list[min(j, kTgtCap - 1)];  // u16: slab ranks
-                    tc = j < rg.x ? lv : (uint32_t)kFar;
-                } else {
-                    tc = j < rg.x ? a.local[rg.y + j] - S.pre[k] : (uint32_t)kFar;
-                }
-                const bool take = tc < after;
-                n = (uint32_t)__popcll(ballot(take));
-                if (take) {
-                    const uint32_t w = S.slot[tc - seen];
-                    a.pv[rg.y + j] = (unsigned long long)(sl.base + r * kRow + (w >> 16)) |
-                                     ((unsigned long long)(w & 0xFFFF) << 32);
-                }
-                i += n;
-            } while (n == 64);
-            const uint32_t nx = rdlane(tc, n);  // the first target not taken, or kFar
-            wave_fence();
-            if (ln == 0) S.next[k] = make_uint2(nx, i);
-            wave_fence();
-            H0 &= ~M0;
-            H1 &= ~M1;
-        } while (H0 | H1);
+            const uint32_t rr0 = __builtin_amdgcn_mbcnt_hi((uint32_t)(M1 >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)M1, mbcnt(M0)));
+            const uint32_t rr1 = rr0 + (m0 ? 1u : 0u);
+            {  // the first target: the element of in-row rank tc - seen
+                const uint32_t q = tc - seen;
+                const uint64_t E0 = ballot(m0 && rr0 == q), E1 = ballot(m1 && rr1 == q);
+                const uint32_t L = (uint32_t)__builtin_ctzll(E0 | E1) & 63u;
+                const uint32_t h = (uint32_t)(E1 >> L) & 1u, wv = rdlane(o, L);
+                if (ln == 0)
+                    a.pv[jo + i] = (unsigned long long)(sl.base + r * kRow + 2 * L + h) |
+                                   ((unsigned long long)(h ? wv >> 16 : wv & 0xFFFFu) << 32);
+                ++i;
+                tc = i < ke ? target(i, jo, pr) : (uint32_t)kFar;
+            }
+            if (tc < after) {  // more targets of exponent k in this row
+                // publish by in-row rank; other lanes write a slot of their own past the ranks
+                S.slot[m0 ? rr0 : kRow + ln] = ((2 * ln) << 16) | (o & 0xFFFFu);
+                S.slot[m1 ? rr1 : kRow + ln] = ((2 * ln + 1) << 16) | (o >> 16);
+                wave_fence();
+                uint32_t n, tl;
+                do {  // one target per lane (64 more if all lanes take one)
+                    const uint32_t j = i + ln;
+                    tl = j < ke ? target(j, jo, pr) : (uint32_t)kFar;
+                    const bool take = tl < after;
+                    n = (uint32_t)__popcll(ballot(take));
+                    if (take) {
+                        const uint32_t w = S.slot[tl - seen];
+                        a.pv[jo + j] = (unsigned long long)(sl.base + r * kRow + (w >> 16)) |
+                                       ((unsigned long long)(w & 0xFFFFu) << 32);
+                    }
+                    i += n;
+                } while (n == 64);
+                tc = rdlane(tl, n);  // the first target not taken, or kFar
+                wave_fence();
+            }
+            if (ln == k) {
+                nxt = tc;
+                nix = i;
+            }
+            H &= H - 1;
+        } while (H);
     });
 }
 
-// W == kWin: slabs whose target exponents lie within kWin consecutive values (the others are
-// listed for the W == 256 kernel); W == 256: a listed slab.
-template <uint32_t W>
-__device__ void select_tile(const SelectArgs &a, uint32_t tau, SelectLds<W> &S) {
+// One window of one slab: exponents [kfirst, kfirst + kWin), or from the slab's lowest exponent with
+// targets when kfirst is 256.  The slab's targets are the group changes [lb(slab), lb(next slab)) of
+// each exponent (to the group's end for a tensor's last slab).
+__device__ void select_window(const SelectArgs &a, uint32_t tau, uint32_t kfirst, SelectLds &S) {
     const uint32_t ln = lane();
     const uint32_t t = a.tile_tensor[tau];
     const TensorDesc td = a.descs[t];
     int32_t g4[4];
     uint32_t j0[4], j1[4], pr[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {  // independent loads, issued together
+    for (int q = 0; q < 4; ++q) {  // exponents 4 ln + q; independent loads, issued together
         const uint32_t k = 4 * ln + q;
         g4[q] = a.group_of[(uint64_t)t * 256 + k];
         j0[q] = a.lb[(uint64_t)tau * 256 + k];
@@ -1175,9 +1260,7 @@ __device__ void select_tile(const SelectArgs &a, uint32_t tau, SelectLds<W> &S) 
     }
     const uint32_t local_tile = tau - td.tile_begin;
     const bool last = local_tile + 1 >= td.n_tiles;
-
-    // targets of this slab: group changes [lb(slab), lb(next slab)) of each exponent
-    uint32_t n4[4], mine = 0, klo = 256, khi = 0;
+    uint32_t n4[4], klo = 256;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         n4[q] = 0;
@@ -1189,170 +1272,179 @@ __device__ void select_tile(const SelectArgs &a, uint32_t tau, SelectLds<W> &S) 
             }
             if (j0[q] < je) n4[q] = je - j0[q];
         }
-        mine += n4[q];
-        if (n4[q]) {
-            klo = min(klo, 4 * ln + q);
-            khi = max(khi, 4 * ln + q);
+        if (n4[q]) klo = min(klo, 4 * ln + q);
+    }
+    for (int o = 32; o > 0; o >>= 1) klo = min(klo, (uint32_t)__shfl_xor(klo, o, 64));
+    const uint32_t kbase = kfirst < 256 ? kfirst : klo;
+    if (kbase >= 256) return;  // no targets in this slab
+    const Slab sl = slab_of(td, local_tile, a.slab);
+    {
+        uint32_t nw[4], mine = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            nw[q] = 4 * ln + q - kbase < kWin ? n4[q] : 0u;
+            mine += nw[q];
         }
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-        klo = min(klo, (uint32_t)__shfl_xor(klo, o, 64));
-        khi = max(khi, (uint32_t)__shfl_xor(khi, o, 64));
-    }
-    if (klo > khi) return;  // no targets in this slab
-    if (W == kWin && khi - klo >= kWin) {
-        if (ln == 0) a.wide[atomicAdd(a.n_wide, 1u)] = tau;
-        return;
-    }
-    const uint32_t kbase = W == kWin ? klo : 0;
-
-    uint32_t incl = mine;  // inclusive scan of per-lane totals across the wave
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t v = __shfl_up(incl, o, 64);
-        if (ln >= (uint32_t)o) incl += v;
-    }
-    const uint32_t total = __shfl(incl, 63, 64);
-    const bool in_lds = total <= kTgtCap;
-    uint32_t start[4], off = incl - mine;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t c = 4 * ln + q - kbase;
-        start[q] = off;
-        if (c < W) {
-            S.range[c] = make_uint2(off + n4[q], j0[q] - off);
-            S.pre[c] = pr[q];
+        uint32_t incl = mine;  // inclusive scan of per-lane totals across the wave
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t v = __shfl_up(incl, o, 64);
+            if (ln >= (uint32_t)o) incl += v;
         }
-        off += n4[q];
-    }
-    if (in_lds) {
-        // list entry x belongs to the last exponent whose list starts at or before x: mark the starts
-        // of the non-empty lists, then a running maximum over the entries (16 per lane, in order)
-        uint16_t *mark = S.list;  // read into registers before the list overwrites it
-        for (uint32_t x = ln; x < kTgtCap; x += 64) mark[x] = 0;
+        const uint32_t total = __shfl(incl, 63, 64);
+        const bool in_lds = total <= kTgtCap;
+        S.info[ln] = make_uint4(0u, 0u, 0u, 0u);  // window exponents past 255
         wave_fence();
+        uint32_t start[4], off = incl - mine;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (n4[q]) mark[start[q]] = (uint16_t)(4 * ln + q - kbase + 1);
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t c = 4 * ln + q - kbase;
+            start[q] = off;
+            if (c < kWin) S.info[c] = make_uint4(off, off + nw[q], j0[q] - off, pr[q]);
+            off += nw[q];
+        }
         wave_fence();
-        uint32_t v[16], run = 0;
+        if (in_lds) {
+            // list entry x belongs to the last exponent whose list starts at or before x: mark the starts
+            // of the non-empty lists, then a running maximum over the entries (16 per lane, in order)
+            uint16_t *mark = S.list;  // read into registers before the list overwrites it
+            for (uint32_t x = ln; x < kTgtCap; x += 64) mark[x] = 0;
+            wave_fence();
 #pragma unroll
-        for (int i = 0; i < 16; i += 8) {
-            const uint4 m = *reinterpret_cast<const uint4 *>(&mark[16 * ln + i]);
-            const uint32_t w4[4] = {m.x, m.y, m.z, m.w};
+            for (int q = 0; q < 4; ++q)
+                if (nw[q]) mark[start[q]] = (uint16_t)(4 * ln + q - kbase + 1);
+            wave_fence();
+            uint32_t v[16], run = 0;
 #pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                v[i + 2 * h] = run = max(run, w4[h] & 0xFFFF);
-                v[i + 2 * h + 1] = run = max(run, w4[h] >> 16);
+            for (int i = 0; i < 16; i += 8) {
+                const uint4 m = *reinterpret_cast<const uint4 *>(&mark[16 * ln + i]);
+                const uint32_t w4[4] = {m.x, m.y, m.z, m.w};
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    v[i + 2 * h] = run = max(run, w4[h] & 0xFFFF);
+                    v[i + 2 * h + 1] = run = max(run, w4[h] >> 16);
+                }
+            }
+            uint32_t before = run;  // inclusive max-scan of the lane maxima, then shifted by one lane
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t w = __shfl_up(before, o, 64);
+                if (ln >= (uint32_t)o) before = max(before, w);
+            }
+            before = __shfl_up(before, 1, 64);
+            if (ln == 0) before = 0;
+            uint32_t idx[16], sub[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t c = max(before, v[i]);
+                const uint4 inf = S.info[c ? c - 1 : 0];
+                idx[i] = inf.z + 16 * ln + i;
+                sub[i] = inf.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t x = 16 * ln + i;
+                if (x < total) S.list[x] = (uint16_t)(a.local[idx[i]] - sub[i]);
             }
         }
-        uint32_t before = run;  // inclusive max-scan of the lane maxima, then shifted by one lane
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t w = __shfl_up(before, o, 64);
-            if (ln >= (uint32_t)o) before = max(before, w);
-        }
-        before = __shfl_up(before, 1, 64);
-        if (ln == 0) before = 0;
-        uint32_t idx[16], sub[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint32_t c = max(before, v[i]);
-            const uint32_t cc = c ? c - 1 : 0;
-            idx[i] = S.range[cc].y + 16 * ln + i;
-            sub[i] = S.pre[cc];
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint32_t x = 16 * ln + i;
-            if (x < total) S.list[x] = (uint16_t)(a.local[idx[i]] - sub[i]);
-        }
+        wave_fence();
+        const uint4 inf = S.info[ln];  // lane ln: window exponent ln
+        uint32_t first = (uint32_t)kFar;
+        if (inf.x < inf.y) first = in_lds ? S.list[inf.x] : a.local[inf.z + inf.x] - inf.w;
+        wave_fence();
+        for (uint32_t i = ln; i < (kWin + kSpare) * kSelCopies; i += 64) S.cnt[i] = 0;
+        wave_fence();
+        if (in_lds) select_slab<true>(a, td, sl, kbase, S, first, inf.x, inf.y, inf.z, inf.w);
+        else select_slab<false>(a, td, sl, kbase, S, first, inf.x, inf.y, inf.z, inf.w);
     }
-    wave_fence();
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t c = 4 * ln + q - kbase;
-        if (c < W) {
-            uint32_t first = (uint32_t)kFar;
-            if (n4[q]) first = in_lds ? S.list[start[q]] : a.local[j0[q]] - pr[q];
-            S.next[c] = make_uint2(first, start[q]);
-        }
-    }
-    if (ln < kSpare) S.next[W + ln] = make_uint2((uint32_t)kFar, 0u);
-    wave_fence();
-    for (uint32_t i = ln; i < (W + kSpare) * kSelCopies; i += 64) S.cnt[i] = 0;
-    wave_fence();
-    const Slab sl = slab_of(td, local_tile, a.slab);
-    if (in_lds) select_slab<W, true>(a, td, sl, kbase, S);
-    else select_slab<W, false>(a, td, sl, kbase, S);
 }
 
+// Blocks [0, n_front): the first n_front windows k_locate listed (started first, so they overlap
+// the rest); then one block per slab for its first window.
 __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
-    __shared__ __attribute__((aligned(16))) SelectLds<kWin> S;
+    __shared__ __attribute__((aligned(16))) SelectLds S;
     if (*a.bad) return;
-    select_tile<kWin>(a, blockIdx.x, S);
+    const uint32_t b = blockIdx.x;
+    if (b < a.n_front) {
+        if (b >= *a.n_more) return;
+        const uint2 m = a.more[b];
+        select_window(a, m.x, m.y, S);
+    } else {
+        select_window(a, b - a.n_front, 256u, S);
+    }
 }
 
-// The slabs k_select listed; a fixed grid walks the list.
-__global__ __launch_bounds__(64) void k_select_wide(SelectArgs a) {
-    __shared__ __attribute__((aligned(16))) SelectLds<256> S;
+// Listed windows past the first n_front (normally none); a fixed grid walks them.
+__global__ __launch_bounds__(64) void k_select_more(SelectArgs a) {
+    __shared__ __attribute__((aligned(16))) SelectLds S;
     if (*a.bad) return;
-    const uint32_t n = *a.n_wide;
-    for (uint32_t i = blockIdx.x; i < n; i += gridDim.x) {
-        select_tile<256>(a, a.wide[i], S);
+    const uint32_t n = *a.n_more;
+    for (uint32_t i = a.n_front + blockIdx.x; i < n; i += gridDim.x) {
+        const uint2 m = a.more[i];
+        select_window(a, m.x, m.y, S);
         wave_fence();
     }
 }
 
 // new = (old + unzigzag(zz)) mod 2^16; checksum delta per tensor (codec.py:698-700).
 __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
-    __shared__ unsigned long long sh[256];
+    __shared__ unsigned long long sh[kBlocksPerWG][256];
     if (*a.bad) return;
-    const uint64_t b = blockIdx.x;
-    const uint32_t g = a.bmap[b];
-    const GroupDev gr = a.groups[g];
-    const uint64_t kb = b - gr.blk_base;
-    const uint32_t cnt = (uint32_t)min64(256, gr.count - kb * 256);
-    const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
     const uint32_t s = threadIdx.x;
-    unsigned long long d = 0;
-    if (s < cnt) {
-        const uint64_t j = eb + s;
-        const unsigned long long pv = a.pv[j];
-        const uint32_t p = (uint32_t)pv;
-        if (p == kNone) {
-            atomicOr(a.bad, kBadUnplaced);
-        } else {
-            const uint32_t zz = a.zz[j];
-            const int32_t delta = (int32_t)(zz >> 1) ^ -(int32_t)(zz & 1);
-            const uint32_t old = (uint32_t)(pv >> 32);
-            const uint32_t nu = (uint32_t)((int32_t)old + delta) & 0xFFFF;
-            d = (uint64_t)((int64_t)nu - (int64_t)old) * weight(p);
-            a.pv[j] = p | ((unsigned long long)nu << 32);
-            const uint32_t eo = (old >> 7) & 0xFF, en = (nu >> 7) & 0xFF;
-            if (eo != en) {  // the element moves between exponent counts of its slab
-                uint32_t *h = a.descs[gr.tensor].hist_out;
-                if (h) {
-                    h += (uint64_t)(p / a.slab) * 256;
-                    atomicSub(&h[eo], 1u);
-                    atomicAdd(&h[en], 1u);
+    GroupDev gr[kBlocksPerWG];
+    BlockRef r[kBlocksPerWG];
+    unsigned long long pv[kBlocksPerWG];
+    uint32_t zz[kBlocksPerWG];
+#pragma unroll
+    for (uint32_t u = 0; u < kBlocksPerWG; ++u) r[u] = block_ref(a, (uint64_t)blockIdx.x * kBlocksPerWG + u, gr[u]);
+#pragma unroll
+    for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
+        if (s < r[u].cnt) {
+            pv[u] = a.pv[r[u].eb + s];
+            zz[u] = a.zz[r[u].eb + s];
+        }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
+        unsigned long long d = 0;
+        const uint32_t p = (uint32_t)pv[u];
+        if (s < r[u].cnt) {
+            if (p == kNone) {
+                atomicOr(a.bad, kBadUnplaced);
+            } else {
+                const int32_t delta = (int32_t)(zz[u] >> 1) ^ -(int32_t)(zz[u] & 1);
+                const uint32_t old = (uint32_t)(pv[u] >> 32);
+                const uint32_t nu = (uint32_t)((int32_t)old + delta) & 0xFFFF;
+                d = (uint64_t)((int64_t)nu - (int64_t)old) * weight(p);
+                a.pv[r[u].eb + s] = p | ((unsigned long long)nu << 32);
+                const uint32_t eo = (old >> 7) & 0xFF, en = (nu >> 7) & 0xFF;
+                if (eo != en) {  // the element moves between exponent counts of its slab
+                    uint32_t *h = a.descs[gr[u].tensor].hist_out;
+                    if (h) {
+                        h += (uint64_t)(p / a.slab) * 256;
+                        atomicSub(&h[eo], 1u);
+                        atomicAdd(&h[en], 1u);
+                    }
                 }
             }
         }
+        sh[u][s] = d;
     }
-    unsigned long long total;
-    block_exclusive_sum(d, sh, &total);
-    if (s == 0) a.bdelta[b] = total;
+    __syncthreads();
+    // wavefront u sums block u's deltas
+    const uint32_t w = s >> 6, ln = lane();
+    const unsigned long long *v = &sh[w][4 * ln];
+    const unsigned long long t = wave_sum(v[0] + v[1] + v[2] + v[3]);
+    const uint64_t b = (uint64_t)blockIdx.x * kBlocksPerWG + w;
+    if (ln == 0 && b < a.n_blocks) a.bdelta[b] = t;
 }
 
+// One workgroup per block: the stores are bound by HBM partial writes, and more blocks per workgroup
+// measured slower.
 __global__ __launch_bounds__(256) void k_scatter(BlockArgs a) {
-    const uint64_t b = blockIdx.x;
-    const uint32_t g = a.bmap[b];
-    const GroupDev gr = a.groups[g];
-    const uint64_t kb = b - gr.blk_base;
-    const uint32_t cnt = (uint32_t)min64(256, gr.count - kb * 256);
-    const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
+    GroupDev gr;
+    const BlockRef r = block_ref(a, blockIdx.x, gr);
     const uint32_t s = threadIdx.x;
-    if (s < cnt) {
-        const unsigned long long pv = a.pv[eb + s];
+    if (s < r.cnt) {
+        const unsigned long long pv = a.pv[r.eb + s];
         a.descs[gr.tensor].base[(uint32_t)pv] = (uint16_t)(pv >> 32);
     }
 }
@@ -1462,18 +1554,18 @@ void launch_decode(const DecodeArgs &a, hipStream_t s) {
 }
 
 void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
-    CRX_LAUNCH("local_fix", k_local_fix, (uint32_t)n_blocks, 256, s, a);
+    CRX_LAUNCH("local_fix", k_local_fix, grid1(n_blocks, kBlocksPerWG), 256, s, a);
 }
 
 void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("locate", k_locate, tiles, 256, s, a); }
 
 void launch_select(const SelectArgs &a, uint32_t tiles, hipStream_t s) {
-    CRX_LAUNCH("select", k_select, tiles, 64, s, a);
-    CRX_LAUNCH("select_wide", k_select_wide, min(tiles, 2048u), 64, s, a);
+    CRX_LAUNCH("select", k_select, a.n_front + tiles, 64, s, a);
+    CRX_LAUNCH("select_more", k_select_more, 256, 64, s, a);
 }
 
 void launch_verify(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
-    CRX_LAUNCH("verify", k_verify, (uint32_t)n_blocks, 256, s, a);
+    CRX_LAUNCH("verify", k_verify, grid1(n_blocks, kBlocksPerWG), 256, s, a);
 }
 
 void launch_scatter(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
