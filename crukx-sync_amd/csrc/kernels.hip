@@ -1197,12 +1197,14 @@ __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Sla
             const bool m0 = c0 == (k << 7), m1 = c1 == (k << 7);
             const uint64_t M0 = ballot(m0), M1 = ballot(m1);
             const uint32_t seen = after - (uint32_t)(__popcll(M0) + __popcll(M1));  // ... before this row
+            // in-row rank of this lane's first element among exponent k's (the second's is one more
+            // when the first is one of them)
             const uint32_t rr0 = __builtin_amdgcn_mbcnt_hi((uint32_t)(M1 >> 32),
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)M1, mbcnt(M0)));
-            const uint32_t rr1 = rr0 + (m0 ? 1u : 0u);
             {  // the first target: the element of in-row rank tc - seen
                 const uint32_t q = tc - seen;
-                const uint64_t E0 = ballot(m0 && rr0 == q), E1 = ballot(m1 && rr1 == q);
+                const uint64_t Q0 = ballot(rr0 == q), Q1 = ballot(rr0 == q - 1u);
+                const uint64_t E0 = Q0 & M0, E1 = M1 & ((Q1 & M0) | (Q0 & ~M0));
                 const uint32_t L = (uint32_t)__builtin_ctzll(E0 | E1) & 63u;
                 const uint32_t h = (uint32_t)(E1 >> L) & 1u, wv = rdlane(o, L);
                 if (ln == 0)
@@ -1214,7 +1216,7 @@ __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Sla
             if (tc < after) {  // more targets of exponent k in this row
                 // publish by in-row rank; other lanes write a slot of their own past the ranks
                 S.slot[m0 ? rr0 : kRow + ln] = ((2 * ln) << 16) | (o & 0xFFFFu);
-                S.slot[m1 ? rr1 : kRow + ln] = ((2 * ln + 1) << 16) | (o >> 16);
+                S.slot[m1 ? rr0 + (m0 ? 1u : 0u) : kRow + ln] = ((2 * ln + 1) << 16) | (o >> 16);
                 wave_fence();
                 uint32_t n, tl;
                 do {  // one target per lane (64 more if all lanes take one)
