@@ -1062,40 +1062,56 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
 // its first one (the select pass streams the slab once per window): windows of kSelWin exponents,
 // each starting at the lowest exponent with targets past the previous window.
 constexpr uint32_t kSelWin = 64;
-__global__ __launch_bounds__(256) void k_locate(SelectArgs a) {
-    __shared__ uint64_t hasm[4];
+__global__ __launch_bounds__(64) void k_locate(SelectArgs a) {
     if (*a.bad) return;
-    const uint32_t tau = blockIdx.x, k = threadIdx.x;
+    const uint32_t tau = blockIdx.x, ln = lane();
     const uint32_t t = a.tile_tensor[tau];
-    const int32_t g = a.group_of[(uint64_t)t * 256 + k];
-    uint32_t lb = kNone;
-    bool has = false;  // targets of exponent k in this slab
-    if (g >= 0) {
-        const GroupDev gr = a.groups[g];
-        const uint32_t target = a.pre[(uint64_t)tau * 256 + k];
-        const uint32_t tb = a.descs[t].tile_begin, nt = a.descs[t].n_tiles;
-        const bool last = tau + 1 >= tb + nt;
-        const uint32_t next = last ? kNone : a.pre[(uint64_t)(tau + 1) * 256 + k];
-        uint32_t lo = gr.elem_base, hi = gr.elem_base + gr.count, vhi = kNone;  // vhi = local[hi]
-        while (lo < hi) {
-            const uint32_t mid = lo + ((hi - lo) >> 1), v = a.local[mid];
-            if (v < target) {
-                lo = mid + 1;
-            } else {
-                hi = mid;
-                vhi = v;
+    const bool last = tau + 1 >= a.descs[t].tile_begin + a.descs[t].n_tiles;
+    // exponents ln + 64 q: four lower-bound searches per lane, advanced together
+    int32_t g[4];
+    uint32_t lo[4], hi[4], end[4], vhi[4], target[4], next[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t k = ln + 64 * q;
+        g[q] = a.group_of[(uint64_t)t * 256 + k];
+        target[q] = a.pre[(uint64_t)tau * 256 + k];
+        next[q] = last ? kNone : a.pre[(uint64_t)(tau + 1) * 256 + k];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        lo[q] = hi[q] = end[q] = 0;
+        vhi[q] = kNone;  // local[hi] once hi has moved
+        if (g[q] >= 0) {
+            const GroupDev gr = a.groups[g[q]];
+            lo[q] = gr.elem_base;
+            hi[q] = end[q] = gr.elem_base + gr.count;
+        }
+    }
+    for (;;) {
+        bool more = false;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) more |= lo[q] < hi[q];
+        if (!__any(more)) break;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (lo[q] < hi[q]) {
+                const uint32_t mid = lo[q] + ((hi[q] - lo[q]) >> 1), v = a.local[mid];
+                if (v < target[q]) {
+                    lo[q] = mid + 1;
+                } else {
+                    hi[q] = mid;
+                    vhi[q] = v;
+                }
             }
         }
-        lb = lo;
-        has = lo < gr.elem_base + gr.count && (last || vhi < next);
     }
-    ((uint32_t *)a.lb)[(uint64_t)tau * 256 + k] = lb;
-    const uint64_t m = ballot(has);
-    if (lane() == 0) hasm[k >> 6] = m;
-    __syncthreads();
-    if (k == 0) {
-        // bit e of the 256-bit mask: exponent e has targets; windows greedy from the lowest
-        const uint64_t w[4] = {hasm[0], hasm[1], hasm[2], hasm[3]};
+    uint64_t w[4];  // bit ln of w[q]: exponent ln + 64 q has targets in this slab
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        ((uint32_t *)a.lb)[(uint64_t)tau * 256 + ln + 64 * q] = g[q] >= 0 ? lo[q] : kNone;
+        w[q] = ballot(g[q] >= 0 && lo[q] < end[q] && (last || vhi[q] < next[q]));
+    }
+    if (ln == 0) {  // windows greedy from the lowest exponent with targets
         auto first_at = [&](uint32_t from) -> uint32_t {  // lowest set bit at or past `from` (256: none)
             for (uint32_t q = from >> 6; q < 4; ++q) {
                 const uint64_t v = q == (from >> 6) ? w[q] & (~0ULL << (from & 63)) : w[q];
@@ -1559,7 +1575,7 @@ void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
     CRX_LAUNCH("local_fix", k_local_fix, grid1(n_blocks, kBlocksPerWG), 256, s, a);
 }
 
-void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("locate", k_locate, tiles, 256, s, a); }
+void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("locate", k_locate, tiles, 64, s, a); }
 
 void launch_select(const SelectArgs &a, uint32_t tiles, hipStream_t s) {
     CRX_LAUNCH("select", k_select, a.n_front + tiles, 64, s, a);
