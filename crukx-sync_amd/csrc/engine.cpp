@@ -2,6 +2,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -72,6 +73,21 @@ void timing_end(const char *name, hipStream_t s) {
     g_pending.push_back(Pending{name, g_open, e});
     g_open = nullptr;
 }
+
+// Host phases of a call: wall time between marks, accumulated as "host:<name>" when timing is on.
+// A phase that ends at a stream synchronisation includes the wait for the device.
+struct HostClock {
+    std::chrono::steady_clock::time_point t = std::chrono::steady_clock::now();
+    void mark(const char *name) {
+        if (!g_timing) return;
+        const auto n = std::chrono::steady_clock::now();
+        std::lock_guard<std::mutex> lk(g_tmu);
+        Stat &st = g_stats[std::string("host:") + name];
+        st.calls++;
+        st.ms += std::chrono::duration<double, std::milli>(n - t).count();
+        t = n;
+    }
+};
 
 // ------------------------------------------------------------------ workspace
 // Device buffers of one call.  Small buffers are carved from chunks of kArenaChunk bytes so that a
@@ -253,6 +269,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     E.checksum.assign(n, 0);
     E.numel.assign(numels, numels + n);
     E.groups.assign(n, {});
+    HostClock hc;
     Layout L;
     for (int32_t t = 0; t < n; ++t) {
         if (!numels[t]) continue;
@@ -287,9 +304,11 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     EncRankArgs a{d_descs, sd.tile_tensor, T, slab, hall, hchg, ar.get<uint64_t>((uint64_t)tiles * per_slab), nullptr,
                   per_slab, rec_count, ovf, delta, full};
     launch_enc_rank(a, tiles, s);
+    hc.mark("enc_setup");
     unsigned int hovf1 = 0;
     d2h(&hovf1, ovf, 1, s);
     sync(s);
+    hc.mark("enc_wait_rank");
     if (hovf1) {
         unsigned long long *rec_base = ar.get<unsigned long long>(tiles + 1);
         launch_scan_u32(rec_count, tiles, rec_base, ar.get<unsigned long long>(scan_parts(tiles)), s);
@@ -307,6 +326,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     unsigned long long gc[2];
     d2h(gc, gcnt, 2, s);
     sync(s);
+    hc.mark("enc_wait_groups");
     const uint64_t G = gc[0], C = gc[1];
     E.total_changes = C;
     if (C == 0) return;
@@ -343,10 +363,12 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     d2h(hfull.data(), t_full, T, s);
     d2h(hs, scnt, 2, s);
     sync(s);
+    hc.mark("enc_wait_stats");
     if (hs[1]) throw DeviceError("rare symbol list overflowed");
     std::vector<uint32_t> hrare(hs[0]);
     d2h(hrare.data(), rare, hs[0], s);
     sync(s);
+    hc.mark("enc_wait_rare");
     std::sort(hrare.begin(), hrare.end());
 
     // checksums (codec.py:344-352) and groups / Rice parameters (codec.py:354-360)
@@ -408,6 +430,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
         E.tables.push_back(std::move(tb));
     }
 
+    hc.mark("enc_tables");
     GroupDev *d_groups2 = ar.get<GroupDev>(G);
     uint32_t *d_lut = ar.get<uint32_t>(256 * kDense);
     uint32_t *d_rk = ar.get<uint32_t>(rkeys.size()), *d_rv = ar.get<uint32_t>(rvals.size());
@@ -423,6 +446,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     unsigned long long total_bits = 0;
     d2h(&total_bits, toff + n_thr, 1, s);
     sync(s);
+    hc.mark("enc_wait_lengths");
 
     const uint64_t n_words = (total_bits + 31) / 32 + 4;
     uint32_t *words = ar.get<uint32_t>(n_words);
@@ -439,6 +463,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     unsigned int hovf = 0;
     d2h(&hovf, bovf, 1, s);
     sync(s);
+    hc.mark("enc_wait_pack");
     if (hovf) throw Invalid("a block exceeds 2^32 bits; the update cannot be represented");
     E.d_block_bits = bb;
     E.payload_len = (total_bits + 7) / 8;
@@ -458,6 +483,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     *changed = 0;
     const uint32_t T = (uint32_t)u.tensors.size();
     if (!T) return;
+    HostClock hc;
     const uint32_t slab = apply_slab(slab_req);
     const uint64_t C = u.total_changes;
     if (C >= (1ULL << 32)) throw Invalid("2^32 or more changes in one update are not supported");
@@ -521,6 +547,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     for (int64_t gi = (int64_t)G - 1; gi >= 0; --gi) tensor_blk[groups[gi].tensor] = groups[gi].blk_base;
     for (int64_t t = (int64_t)T - 1; t >= 0; --t) tensor_blk[t] = std::min(tensor_blk[t], tensor_blk[t + 1]);
 
+    hc.mark("apply_tables");
     TensorDesc *d_descs = ar.get<TensorDesc>(T);
     h2d(d_descs, L.descs.data(), T, s);
     uint32_t *hall = ar.get<uint32_t>((uint64_t)tiles * 256);
@@ -582,6 +609,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     launch_select(sa, tiles, s);
     launch_verify(ba, B, s);
     launch_range_sums(bdelta, tblk, T, tdelta, s);
+    hc.mark("apply_launch");
 
     unsigned int hbad = 0;
     std::vector<unsigned long long> hdelta(T);
@@ -590,6 +618,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     d2h(hdelta.data(), tdelta, T, s);
     d2h(hfull.data(), t_full, T, s);
     sync(s);
+    hc.mark("apply_wait_verify");
     if (hbad & kBadDecode) throw Corrupt("payload does not decode to its block table");
     if (hbad) throw Corrupt("payload positions outside their exponent groups");
     std::vector<std::string> wrong;
@@ -604,6 +633,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     }
     launch_scatter(ba, B, s);
     sync(s);
+    hc.mark("apply_wait_scatter");
     *changed = C;
 }
 

@@ -162,23 +162,46 @@ __device__ __forceinline__ void stream_rows(const Slab &sl, const Rsrc (&src)[S]
 // ================================================================== encode: rank pass
 // One wavefront per slab; reads old and new once.  For every changed element it needs its rank among
 // the slab's elements with the same old exponent (`rank`) and among the slab's changes with that
-// exponent (`rc`): the running per-exponent counts in LDS give the part before the row, ballots and
-// mbcnt the stable part inside the row.  Changed elements are buffered in LDS as (rank, rc, exponent,
-// offset, old, new) and finished in dense batches: zigzag residual, checksum delta, 64-bit record.
-// Records go to the slab's own region, [base, base + cap): no shared counter.
+// exponent (`rc`).  The running per-exponent counts in LDS give the part of `rank` before the row,
+// ballots and mbcnt the stable part inside the row.  Changed elements are buffered in LDS in slab
+// order as (rank, exponent, offset, old, new) and finished in dense batches: `rc` from per-exponent
+// change counts and ballots over the batch, zigzag residual, checksum delta, 64-bit record.  Records
+// go to the slab's own region, [base, base + cap): no shared counter.
 __device__ void flush_changes(const EncRankArgs &a, const Slab &sl, const uint64_t *meta, const uint32_t *vals,
-                              uint32_t cnt, uint64_t base, uint64_t cap, uint64_t &written, uint64_t &dacc) {
+                              uint32_t *hchg, uint32_t cnt, uint64_t base, uint64_t cap, uint64_t &written,
+                              uint64_t &dacc) {
     wave_fence();
     const bool fits = written + cnt <= cap;
-    for (uint32_t j = lane(); j < cnt; j += 64) {
-        const uint64_t m = meta[j];
-        const uint32_t v = vals[j];
-        const uint32_t o16 = v & 0xFFFF, n16 = v >> 16;
-        const uint32_t f = (uint32_t)(m >> 42);
-        dacc += (uint64_t)((int64_t)n16 - (int64_t)o16) * weight(sl.base + f);
-        if (fits) a.rec[base + written + j] = (m & ((1ULL << 42) - 1)) | ((uint64_t)zigzag(o16, n16) << 42);
+    const uint32_t ln = lane();
+    for (uint32_t j0 = 0; j0 < cnt; j0 += 64) {
+        const uint32_t j = j0 + ln;
+        const bool v = j < cnt;
+        const uint64_t m = v ? meta[j] : 0ULL;
+        const uint32_t val = v ? vals[j] : 0u;
+        const uint32_t k = v ? (uint32_t)(m >> 17) & 0xFF : 256u;
+        // rc: the exponent's changes in earlier batches plus the earlier lanes of this batch
+        uint32_t rc = 0;
+        uint64_t P = ballot(v);
+        while (P) {
+            const uint32_t kk = rdlane(k, (uint32_t)__builtin_ctzll(P));
+            const uint64_t M = ballot(k == kk);
+            const uint32_t before = hchg[kk];
+            if (k == kk) rc = before + mbcnt(M);
+            wave_fence();
+            if (ln == 0) hchg[kk] = before + (uint32_t)__popcll(M);
+            wave_fence();
+            P &= ~M;
+        }
+        if (v) {
+            const uint32_t o16 = val & 0xFFFF, n16 = val >> 16;
+            const uint32_t f = (uint32_t)(m >> 25) & 0x1FFFF;
+            dacc += (uint64_t)((int64_t)n16 - (int64_t)o16) * weight(sl.base + f);
+            if (fits)
+                a.rec[base + written + j] = (m & 0x1FFFFULL) | ((uint64_t)rc << 17) | ((uint64_t)k << 34) |
+                                            ((uint64_t)zigzag(o16, n16) << 42);
+        }
     }
-    if (!fits && lane() == 0) *a.overflow = 1u;
+    if (!fits && ln == 0) *a.overflow = 1u;
     written += cnt;
     wave_fence();
 }
@@ -212,40 +235,33 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
         const bool c0 = (x & 0xFFFF) != 0, c1 = x > 0xFFFF;
         const uint64_t C0 = ballot(c0), C1 = ballot(c1);
         if (C0 | C1) {
-            uint32_t rk0 = 0, rc0 = 0, rk1 = 0, rc1 = 0;
+            uint32_t rk0 = 0, rk1 = 0;  // meaningful for changed elements only
             uint64_t P0 = C0, P1 = C1;
             do {  // once per distinct exponent among this row's changes
                 const uint32_t l = (uint32_t)__builtin_ctzll(P0 | P1);
                 const uint32_t k = rdlane((P0 >> l) & 1 ? k0 : k1, l);
                 const bool m0 = k0 == k, m1 = k1 == k;
-                const uint64_t M0 = ballot(m0), M1 = ballot(m1), D0 = M0 & C0, D1 = M1 & C1;
+                const uint64_t M0 = ballot(m0), M1 = ballot(m1);
                 const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
-                const uint32_t R = h.x + h.y + h.z + h.w;  // exponent-k elements before this row
-                const uint32_t Rc = hchg[k];               // ... of them changed
-                const uint32_t before = R + mbcnt(M0) + mbcnt(M1), beforec = Rc + mbcnt(D0) + mbcnt(D1);
-                const bool d0 = c0 && m0, d1 = c1 && m1;
-                if (d0) {
-                    rk0 = before;
-                    rc0 = beforec;
-                }
-                if (d1) {
-                    rk1 = before + (m0 ? 1u : 0u);
-                    rc1 = beforec + (d0 ? 1u : 0u);
-                }
-                wave_fence();
-                if (ln == 0) hchg[k] = Rc + (uint32_t)(__popcll(D0) + __popcll(D1));
+                // exponent-k elements before this row, plus this row's before this lane
+                const uint32_t before = h.x + h.y + h.z + h.w +
+                                        __builtin_amdgcn_mbcnt_hi((uint32_t)(M1 >> 32),
+                                            __builtin_amdgcn_mbcnt_lo((uint32_t)M1, mbcnt(M0)));
+                if (m0) rk0 = before;
+                if (m1) rk1 = before + (m0 ? 1u : 0u);
                 P0 &= ~M0;
                 P1 &= ~M1;
             } while (P0 | P1);
             const uint32_t f = r * kRow + 2 * ln;
-            const uint32_t cb = cnt + mbcnt(C0) + mbcnt(C1);  // buffer slot of this lane's first change
+            const uint32_t cb = __builtin_amdgcn_mbcnt_hi((uint32_t)(C1 >> 32),
+                                    __builtin_amdgcn_mbcnt_lo((uint32_t)C1, cnt + mbcnt(C0)));  // buffer slot
             if (c0) {
-                meta[cb] = (uint64_t)rk0 | ((uint64_t)rc0 << 17) | ((uint64_t)k0 << 34) | ((uint64_t)f << 42);
+                meta[cb] = (uint64_t)(rk0 | (k0 << 17)) | ((uint64_t)f << 25);
                 vals[cb] = (o & 0xFFFF) | (n << 16);
             }
             if (c1) {
                 const uint32_t s = cb + (c0 ? 1u : 0u);
-                meta[s] = (uint64_t)rk1 | ((uint64_t)rc1 << 17) | ((uint64_t)k1 << 34) | ((uint64_t)(f + 1) << 42);
+                meta[s] = (uint64_t)(rk1 | (k1 << 17)) | ((uint64_t)(f + 1) << 25);
                 vals[s] = (o >> 16) | (n & 0xFFFF0000u);
             }
             cnt += (uint32_t)(__popcll(C0) + __popcll(C1));
@@ -258,11 +274,11 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
             facc += (uint64_t)(n & 0xFFFF) * weight(sl.base + f) + (uint64_t)(n >> 16) * weight(sl.base + f + 1);
         }
         if (cnt > kChgCap - kRow) {
-            flush_changes(a, sl, meta, vals, cnt, rbase, rcap, written, dacc);
+            flush_changes(a, sl, meta, vals, hchg, cnt, rbase, rcap, written, dacc);
             cnt = 0;
         }
     });
-    if (cnt) flush_changes(a, sl, meta, vals, cnt, rbase, rcap, written, dacc);
+    if (cnt) flush_changes(a, sl, meta, vals, hchg, cnt, rbase, rcap, written, dacc);
     wave_fence();
     for (uint32_t k = ln; k < 256; k += 64) {
         const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
