@@ -135,10 +135,11 @@ void zero(T *dst, uint64_t n, hipStream_t s) {
 }
 void sync(hipStream_t s) { HIP_OK(hipStreamSynchronize(s)); }
 
+// Elements per slab: a multiple of kRow, at most 65536 (slab ranks and offsets are kept in 16 bits).
 uint32_t slab_size(int32_t slab) {
     if (slab <= 0) return 65536;
     uint32_t s = (uint32_t)slab;
-    s = std::max<uint32_t>(kRow, std::min<uint32_t>(s, 1u << 17));
+    s = std::max<uint32_t>(kRow, std::min<uint32_t>(s, 65536u));
     return s / kRow * kRow;
 }
 
@@ -472,10 +473,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
 
 // ------------------------------------------------------------------ apply
 // codec.apply (codec.py:578-717) on the device: decode, locate, verify, then write.
-uint32_t apply_slab(int32_t slab_req) {
-    // the select pass keeps slab ranks in 16 bits: apply cuts slabs of at most 65536 elements
-    return std::min<uint32_t>(slab_size(slab_req), 65536);
-}
+uint32_t apply_slab(int32_t slab_req) { return slab_size(slab_req); }
 
 void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets, const uint64_t *numels,
            const int32_t *has_cache, const uint64_t *cache_vals, uint32_t *const *hist_in, uint32_t *const *hist_out,

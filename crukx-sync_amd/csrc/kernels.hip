@@ -15,6 +15,8 @@ constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ULL;
 constexpr uint64_t kMix1 = 0xBF58476D1CE4E5B9ULL;
 constexpr uint64_t kMix2 = 0x94D049BB133111EBULL;
 constexpr int kRankRows = 8;    // rows per batch of the encode rank pass (two streams)
+constexpr uint32_t kRankCopies = 4;  // copies of each exponent count in the encode rank pass (2 or 4)
+static_assert(kRankCopies == 2 || kRankCopies == 4, "kRankCopies");
 constexpr int kScanRows = 16;   // rows per batch of the apply histogram pass
 constexpr int kSelectRows = 12; // ... of the select pass (fewer registers: occupancy)
 
@@ -164,10 +166,10 @@ __device__ __forceinline__ void stream_rows(const Slab &sl, const Rsrc (&src)[S]
 // the slab's elements with the same old exponent (`rank`) and among the slab's changes with that
 // exponent (`rc`).  The running per-exponent counts in LDS give the part of `rank` before the row,
 // ballots and mbcnt the stable part inside the row.  Changed elements are buffered in LDS in slab
-// order as (rank, exponent, offset, old, new) and finished in dense batches: `rc` from per-exponent
+// order as (rank, offset, old, new) and finished in dense batches: `rc` from per-exponent
 // change counts and ballots over the batch, zigzag residual, checksum delta, 64-bit record.  Records
 // go to the slab's own region, [base, base + cap): no shared counter.
-__device__ void flush_changes(const EncRankArgs &a, const Slab &sl, const uint64_t *meta, const uint32_t *vals,
+__device__ void flush_changes(const EncRankArgs &a, const Slab &sl, const uint32_t *meta, const uint32_t *vals,
                               uint32_t *hchg, uint32_t cnt, uint64_t base, uint64_t cap, uint64_t &written,
                               uint64_t &dacc) {
     wave_fence();
@@ -176,9 +178,9 @@ __device__ void flush_changes(const EncRankArgs &a, const Slab &sl, const uint64
     for (uint32_t j0 = 0; j0 < cnt; j0 += 64) {
         const uint32_t j = j0 + ln;
         const bool v = j < cnt;
-        const uint64_t m = v ? meta[j] : 0ULL;
-        const uint32_t val = v ? vals[j] : 0u;
-        const uint32_t k = v ? (uint32_t)(m >> 17) & 0xFF : 256u;
+        const uint32_t m = v ? meta[j] : 0u;  // rank | (offset - f_lo) << 16
+        const uint32_t val = v ? vals[j] : 0u;  // old | new << 16
+        const uint32_t k = v ? (val >> 7) & 0xFF : 256u;
         // rc: the exponent's changes in earlier batches plus the earlier lanes of this batch
         uint32_t rc = 0;
         uint64_t P = ballot(v);
@@ -194,10 +196,10 @@ __device__ void flush_changes(const EncRankArgs &a, const Slab &sl, const uint64
         }
         if (v) {
             const uint32_t o16 = val & 0xFFFF, n16 = val >> 16;
-            const uint32_t f = (uint32_t)(m >> 25) & 0x1FFFF;
+            const uint32_t f = (m >> 16) + sl.f_lo;
             dacc += (uint64_t)((int64_t)n16 - (int64_t)o16) * weight(sl.base + f);
             if (fits)
-                a.rec[base + written + j] = (m & 0x1FFFFULL) | ((uint64_t)rc << 17) | ((uint64_t)k << 34) |
+                a.rec[base + written + j] = (uint64_t)(m & 0xFFFF) | ((uint64_t)rc << 17) | ((uint64_t)k << 34) |
                                             ((uint64_t)zigzag(o16, n16) << 42);
         }
     }
@@ -206,10 +208,20 @@ __device__ void flush_changes(const EncRankArgs &a, const Slab &sl, const uint64
     wave_fence();
 }
 
+// the exponent-k count of the encode rank pass: the sum of its copies
+__device__ __forceinline__ uint32_t rank_count(const uint32_t *hall, uint32_t k) {
+    if (kRankCopies == 2) {
+        const uint2 h = *reinterpret_cast<const uint2 *>(&hall[2 * k]);
+        return h.x + h.y;
+    }
+    const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
+    return h.x + h.y + h.z + h.w;
+}
+
 template <bool COLD>
 __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32_t tau, const Slab &sl,
-                              uint32_t *hall, uint32_t *hchg, uint64_t *meta, uint32_t *vals) {
-    const uint32_t ln = lane(), rep = ln & 3;
+                              uint32_t *hall, uint32_t *hchg, uint32_t *meta, uint32_t *vals) {
+    const uint32_t ln = lane(), rep = ln & (kRankCopies - 1);
     const Rsrc src[2] = {slab_rsrc(td.frame, sl), slab_rsrc(td.frame_new, sl)};
     const uint64_t rbase = a.rec_base ? a.rec_base[tau] : (uint64_t)tau * a.rec_per_slab;
     const uint64_t rcap = a.rec_base ? ~0ULL : a.rec_per_slab;
@@ -242,9 +254,8 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
                 const uint32_t k = rdlane((P0 >> l) & 1 ? k0 : k1, l);
                 const bool m0 = k0 == k, m1 = k1 == k;
                 const uint64_t M0 = ballot(m0), M1 = ballot(m1);
-                const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
                 // exponent-k elements before this row, plus this row's before this lane
-                const uint32_t before = h.x + h.y + h.z + h.w +
+                const uint32_t before = rank_count(hall, k) +
                                         __builtin_amdgcn_mbcnt_hi((uint32_t)(M1 >> 32),
                                             __builtin_amdgcn_mbcnt_lo((uint32_t)M1, mbcnt(M0)));
                 if (m0) rk0 = before;
@@ -255,20 +266,21 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
             const uint32_t f = r * kRow + 2 * ln;
             const uint32_t cb = __builtin_amdgcn_mbcnt_hi((uint32_t)(C1 >> 32),
                                     __builtin_amdgcn_mbcnt_lo((uint32_t)C1, cnt + mbcnt(C0)));  // buffer slot
+            const uint32_t fr = (f - sl.f_lo) << 16;  // slab offsets past f_lo fit 16 bits (slab <= 65536)
             if (c0) {
-                meta[cb] = (uint64_t)(rk0 | (k0 << 17)) | ((uint64_t)f << 25);
+                meta[cb] = rk0 | fr;
                 vals[cb] = (o & 0xFFFF) | (n << 16);
             }
             if (c1) {
                 const uint32_t s = cb + (c0 ? 1u : 0u);
-                meta[s] = (uint64_t)(rk1 | (k1 << 17)) | ((uint64_t)(f + 1) << 25);
+                meta[s] = rk1 | (fr + 0x10000u);
                 vals[s] = (o >> 16) | (n & 0xFFFF0000u);
             }
             cnt += (uint32_t)(__popcll(C0) + __popcll(C1));
             wave_fence();
         }
-        atomicAdd(&hall[4 * k0 + rep], 1u);
-        atomicAdd(&hall[4 * k1 + rep], 1u);
+        atomicAdd(&hall[kRankCopies * k0 + rep], 1u);
+        atomicAdd(&hall[kRankCopies * k1 + rep], 1u);
         if (COLD) {
             const uint32_t f = r * kRow + 2 * ln;
             facc += (uint64_t)(n & 0xFFFF) * weight(sl.base + f) + (uint64_t)(n >> 16) * weight(sl.base + f + 1);
@@ -281,8 +293,7 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
     if (cnt) flush_changes(a, sl, meta, vals, hchg, cnt, rbase, rcap, written, dacc);
     wave_fence();
     for (uint32_t k = ln; k < 256; k += 64) {
-        const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
-        a.hall[(uint64_t)tau * 256 + k] = h.x + h.y + h.z + h.w;
+        a.hall[(uint64_t)tau * 256 + k] = rank_count(hall, k);
         a.hchg[(uint64_t)tau * 256 + k] = hchg[k];
     }
     dacc = wave_sum(dacc);
@@ -295,14 +306,14 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
 }
 
 __global__ __launch_bounds__(64) void k_enc_rank(EncRankArgs a) {
-    __shared__ __attribute__((aligned(16))) uint32_t hall[257 * 4];  // 4 copies per exponent; 256: outside
+    __shared__ __attribute__((aligned(16))) uint32_t hall[257 * kRankCopies];  // copies by lane; 256: outside
     __shared__ uint32_t hchg[256];
-    __shared__ uint64_t meta[kChgCap];
+    __shared__ uint32_t meta[kChgCap];
     __shared__ uint32_t vals[kChgCap];
     const uint32_t tau = blockIdx.x;
     const TensorDesc td = a.descs[a.tile_tensor[tau]];
     const Slab sl = slab_of(td, tau - td.tile_begin, a.slab);
-    for (uint32_t i = lane(); i < 257 * 4; i += 64) hall[i] = 0;
+    for (uint32_t i = lane(); i < 257 * kRankCopies; i += 64) hall[i] = 0;
     for (uint32_t i = lane(); i < 256; i += 64) hchg[i] = 0;
     wave_fence();
     if (td.cold) enc_rank_slab<true>(a, td, tau, sl, hall, hchg, meta, vals);

@@ -18,7 +18,7 @@
  *     after the call (encode: when the crx_encoded handle is freed).  Work runs on `stream`
  *     (a hipStream_t); the calls are synchronous with respect to the host on return.
  *   - `slab` is the number of elements ranked by one wavefront (a multiple of 128, at most
- *     131072; 0 = default 65536).  It plays the role of codec._SLAB (codec.py:30): it changes
+ *     65536; 0 = default 65536).  It plays the role of codec._SLAB (codec.py:30): it changes
  *     how the work is cut, never the bytes.
  */
 #ifndef CRUKX_H
