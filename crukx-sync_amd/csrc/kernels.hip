@@ -1163,7 +1163,7 @@ __global__ __launch_bounds__(64) void k_locate(SelectArgs a) {
 // spare counter no other lane uses.  Lane e owns window exponent e: it sums that exponent's copies
 // and compares the total with the exponent's next target, so one ballot names the exponents with
 // targets in the row.  For each of them, ballots and mbcnt give every element of that exponent its
-// stable in-row rank, and the target's element is the one whose rank matches.  A row with more
+// stable in-row rank, and the lane holding the element whose rank matches the target records it.  A row with more
 // targets of one exponent publishes that exponent's elements in LDS by rank and takes the rest of
 // its targets one per lane.
 //
@@ -1244,22 +1244,24 @@ __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Sla
             // when the first is one of them)
             const uint32_t rr0 = __builtin_amdgcn_mbcnt_hi((uint32_t)(M1 >> 32),
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)M1, mbcnt(M0)));
-            {  // the first target: the element of in-row rank tc - seen
+            const uint32_t rr1 = rr0 + (m0 ? 1u : 0u);
+            // this lane's elements as published: (in-row offset << 16) | bits
+            const uint32_t w0 = ((2 * ln) << 16) | (o & 0xFFFFu), w1 = ((2 * ln + 1) << 16) | (o >> 16);
+            {  // the first target: the element of in-row rank tc - seen writes itself
                 const uint32_t q = tc - seen;
-                const uint64_t Q0 = ballot(rr0 == q), Q1 = ballot(rr0 == q - 1u);
-                const uint64_t E0 = Q0 & M0, E1 = M1 & ((Q1 & M0) | (Q0 & ~M0));
-                const uint32_t L = (uint32_t)__builtin_ctzll(E0 | E1) & 63u;
-                const uint32_t h = (uint32_t)(E1 >> L) & 1u, wv = rdlane(o, L);
-                if (ln == 0)
-                    a.pv[jo + i] = (unsigned long long)(sl.base + r * kRow + 2 * L + h) |
-                                   ((unsigned long long)(h ? wv >> 16 : wv & 0xFFFFu) << 32);
+                const bool t0 = m0 && rr0 == q, t1 = m1 && rr1 == q;  // one element of the row
+                if (t0 || t1) {
+                    const uint32_t w = t1 ? w1 : w0;
+                    a.pv[jo + i] = (unsigned long long)(sl.base + r * kRow + (w >> 16)) |
+                                   ((unsigned long long)(w & 0xFFFFu) << 32);
+                }
                 ++i;
                 tc = i < ke ? target(i, jo, pr) : (uint32_t)kFar;
             }
             if (tc < after) {  // more targets of exponent k in this row
                 // publish by in-row rank; other lanes write a slot of their own past the ranks
-                S.slot[m0 ? rr0 : kRow + ln] = ((2 * ln) << 16) | (o & 0xFFFFu);
-                S.slot[m1 ? rr0 + (m0 ? 1u : 0u) : kRow + ln] = ((2 * ln + 1) << 16) | (o >> 16);
+                S.slot[m0 ? rr0 : kRow + ln] = w0;
+                S.slot[m1 ? rr1 : kRow + ln] = w1;
                 wave_fence();
                 uint32_t n, tl;
                 do {  // one target per lane (64 more if all lanes take one)
