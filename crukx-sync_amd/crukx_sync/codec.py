@@ -120,6 +120,7 @@ class EncodedUpdate(Update):
         self._device = device
         self._ws = workspace  # keeps the device buffers alive
         self._tensors = None
+        self._nargs = None
 
     def __del__(self):
         h, self._h = getattr(self, "_h", None), None
@@ -127,9 +128,10 @@ class EncodedUpdate(Update):
             self._free(h)
 
     def _name_args(self):
-        arr = (ctypes.c_char_p * max(len(self._names), 1))(*self._names)
-        lens = _native.u64_array([len(n) for n in self._names])
-        return arr, lens
+        if self._nargs is None:
+            arr = (ctypes.c_char_p * max(len(self._names), 1))(*self._names)
+            self._nargs = (arr, _native.u64_array([len(n) for n in self._names]))
+        return self._nargs
 
     def nbytes(self) -> int:
         arr, lens = self._name_args()
@@ -291,7 +293,9 @@ def _hist_lookup(t):
 
 def _hist_store(t, buf):
     key = id(t)
-    _hist[key] = (weakref.ref(t, lambda _r, key=key: _hist.pop(key, None)), t._version, buf)
+    e = _hist.get(key)
+    ref = e[0] if e is not None and e[0]() is t else weakref.ref(t, lambda _r, key=key: _hist.pop(key, None))
+    _hist[key] = (ref, t._version, buf)
 
 
 def _cache_get(checksums, name, t):
@@ -326,13 +330,13 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     cache = [_cache_get(checksums, name, t) for name, t in zip(names, targets)] if checksums is not None else [None] * len(names)
     has = [0 if c is None else 1 for c in cache]
     vals = [0 if c is None else c & _MASK64 for c in cache]
-    payload_dev = 0
-    if u._payload_dev is not None:
-        pd = u._payload_dev
-        if pd.device != dev:
-            pd = pd.to(dev)
-        payload_dev = pd.data_ptr()
     L = _native.lib()
+    payload_dev = 0
+    if u._dev_bytes is not None:  # the whole update in device memory: payload and block table read there
+        db = u._dev_bytes
+        if db.device != dev:
+            db = db.to(dev)
+        payload_dev = db.data_ptr() + L.crx_update_payload_offset(u.handle)
     ws = _native.Workspace(dev)
     err = _native.errbuf()
     changed = ctypes.c_uint64()

@@ -125,13 +125,14 @@ def new_bytes(n: int) -> tuple[bytes, int]:
 class ParsedUpdate(Update):
     """An update parsed by the native library; fields are materialised on first access."""
 
-    def __init__(self, handle, source, payload_dev=None):
-        # `source` keeps the parsed buffer alive: the native handle reads the payload from it
+    def __init__(self, handle, source, dev_bytes=None):
+        # `source` keeps the parsed buffer alive: the native handle reads the payload from it;
+        # `dev_bytes`: the whole update in device memory (apply reads payload and block table there)
         from . import _native
         self._free = _native.lib().crx_update_free
         self._h = handle
         self._source = source
-        self._payload_dev = payload_dev
+        self._dev_bytes = dev_bytes
         self._tensors = None
         self._tables = None
 
@@ -227,8 +228,8 @@ class ParsedUpdate(Update):
         from . import _native
         L = _native.lib()
         off, n = L.crx_update_payload_offset(self._h), L.crx_update_payload_len(self._h)
-        if self._payload_dev is not None:
-            return self._payload_dev[:n].cpu().numpy().tobytes()
+        if self._dev_bytes is not None:
+            return self._dev_bytes[off:off + n].cpu().numpy().tobytes()
         return bytes(memoryview(self._source)[off:off + n])
 
     @payload.setter
@@ -297,5 +298,4 @@ def _parse_tensor(t, L, err):
             continue
         _native.raise_for(rc, err)
         _prefix_hint[0] = have  # updates of a run have headers of about the same size
-        off = L.crx_update_payload_offset(h.value)
-        return ParsedUpdate(h.value, host, payload_dev=t[off:])
+        return ParsedUpdate(h.value, host, dev_bytes=t)

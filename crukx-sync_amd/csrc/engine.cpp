@@ -567,7 +567,11 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     h2d(d_lim, lim.data(), lim.size(), s);
     h2d(d_off, off.data(), off.size(), s);
     h2d(d_syms, syms.data(), syms.size(), s);
-    h2d(d_bb, u.block_bits.data(), B, s);
+    if (payload_dev)  // the update is in device memory: its block table precedes the payload there
+        HIP_OK(hipMemcpyAsync(d_bb, payload_dev - (u.payload_offset - u.block_table_offset), 4 * B,
+                              hipMemcpyDeviceToDevice, s));
+    else
+        h2d(d_bb, u.block_bits.data(), B, s);
     zero(pay, pay_words, s);
     if (u.payload_len) {
         if (payload_dev)
@@ -873,20 +877,20 @@ int32_t crx_encoded_write(const crx_encoded *e, const char *const *names, const 
         write_header(*e, names, name_lens, hdr);
         put_varint(pl, e->payload_len);
         const hipMemcpyKind from_dev = dst_on_device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
-        uint64_t off = 0;
+        const uint64_t off_bt = hdr.size(), off_pl = off_bt + 4 * e->n_blocks, off_pay = off_pl + pl.size();
         if (dst_on_device) {
+            // host bytes first, waited for (their buffers end with this call); the device-to-device
+            // copies are left ordered on the stream
             HIP_OK(hipMemcpyAsync(dst, hdr.data(), hdr.size(), hipMemcpyHostToDevice, s));
+            HIP_OK(hipMemcpyAsync(dst + off_pl, pl.data(), pl.size(), hipMemcpyHostToDevice, s));
+            HIP_OK(hipStreamSynchronize(s));
         } else {
             std::memcpy(dst, hdr.data(), hdr.size());
+            std::memcpy(dst + off_pl, pl.data(), pl.size());
         }
-        off += hdr.size();
-        if (e->n_blocks) HIP_OK(hipMemcpyAsync(dst + off, e->d_block_bits, 4 * e->n_blocks, from_dev, s));
-        off += 4 * e->n_blocks;
-        if (dst_on_device) HIP_OK(hipMemcpyAsync(dst + off, pl.data(), pl.size(), hipMemcpyHostToDevice, s));
-        else std::memcpy(dst + off, pl.data(), pl.size());
-        off += pl.size();
-        if (e->payload_len) HIP_OK(hipMemcpyAsync(dst + off, e->d_payload, e->payload_len, from_dev, s));
-        HIP_OK(hipStreamSynchronize(s));
+        if (e->n_blocks) HIP_OK(hipMemcpyAsync(dst + off_bt, e->d_block_bits, 4 * e->n_blocks, from_dev, s));
+        if (e->payload_len) HIP_OK(hipMemcpyAsync(dst + off_pay, e->d_payload, e->payload_len, from_dev, s));
+        if (!dst_on_device) HIP_OK(hipStreamSynchronize(s));
     });
 }
 

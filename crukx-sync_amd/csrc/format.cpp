@@ -181,6 +181,7 @@ void parse(const uint8_t *data, uint64_t avail, uint64_t total, uint8_t last, Up
         if (t.symbols.size() > per_exp[t.exponent]) throw Corrupt("table unused or larger than its changes");
 
     if (total_blocks > r.remaining() / 4) throw Corrupt("block table longer than the update");
+    u.block_table_offset = r.pos;
     const uint8_t *bb = r.take(4 * total_blocks);
     u.block_bits.resize(total_blocks);
     uint64_t total_bits = 0;

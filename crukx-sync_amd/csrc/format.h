@@ -52,6 +52,7 @@ struct Update {
     std::vector<Table> tables;
     std::vector<TensorHeader> tensors;
     std::vector<uint32_t> block_bits;
+    uint64_t block_table_offset = 0;  // byte offset of the block table in the update
     uint64_t payload_offset = 0;
     uint64_t payload_len = 0;
     const uint8_t *payload_host = nullptr;  // null when the payload lives on the device

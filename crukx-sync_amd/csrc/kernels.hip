@@ -1283,7 +1283,7 @@ __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Sla
                 nxt = tc;
                 nix = i;
             }
-            H &= H - 1;
+            H &= ~(1ULL << k);
         } while (H);
     });
 }

@@ -86,8 +86,10 @@ uint64_t crx_update_total_changes(const crx_update *u);
  * exponent order of the receiver's old weights, verify each tensor's checksum, and only then
  * write.  `targets[i]` is the receiver tensor for update tensor i (crx_update_tensor order) with
  * `numels[i]` elements; `has_cache[i]`/`cache_vals[i]` give a trusted old checksum (else one is
- * computed from the weights).  `payload_dev` is NULL to upload the payload from the parsed host
- * bytes, or a device pointer to the payload bytes.  On any status but CRX_OK nothing is written.
+ * computed from the weights).  `payload_dev` is NULL to upload the payload (and block table) from
+ * the parsed host bytes, or the address of the payload inside a device-resident copy of the whole
+ * update (the block table, which precedes the payload, is read from there too).  On any status but
+ * CRX_OK nothing is written.
  * `*changed` receives the number of changed elements. */
 int32_t crx_apply(const crx_update *u, const uint8_t *payload_dev, uint16_t *const *targets,
                   const uint64_t *numels, const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab,
@@ -127,7 +129,8 @@ void crx_encoded_checksums(const crx_encoded *e, int32_t *present, uint64_t *che
 uint64_t crx_encoded_total_changes(const crx_encoded *e);
 /* Serialized size (wire.serialize, wire.py:64-89) given the names of the encode call's tensors. */
 uint64_t crx_encoded_size(const crx_encoded *e, const char *const *names, const uint64_t *name_lens);
-/* Writes the serialized update to `dst` (host memory, or device memory when dst_on_device). */
+/* Writes the serialized update to `dst`: host memory (complete on return), or device memory when
+ * dst_on_device (the copies are ordered on `stream`; the encoded handle must outlive them). */
 int32_t crx_encoded_write(const crx_encoded *e, const char *const *names, const uint64_t *name_lens, uint8_t *dst,
                           int32_t dst_on_device, void *stream, char *err, uint64_t errlen);
 /* Header pieces for wire.Update materialisation. */
