@@ -389,6 +389,10 @@ __global__ __launch_bounds__(64) void k_hist(HistArgs a) {
 
 // ================================================================== per-tensor histogram scan
 // h[tile][256] -> exclusive prefix over the tensor's slabs, in place; totals[tensor][256].
+// The loops below read a batch of values before writing any (the reads and writes alias as far as
+// the compiler knows), so a batch costs one memory latency instead of one per value.
+constexpr uint32_t kScanBatch = 16;
+
 __global__ __launch_bounds__(256) void k_scan_sum(const uint32_t *h, const ScanChunk *ch, uint32_t *csum) {
     const ScanChunk c = ch[blockIdx.x];
     const uint32_t k = threadIdx.x;
@@ -397,26 +401,33 @@ __global__ __launch_bounds__(256) void k_scan_sum(const uint32_t *h, const ScanC
     csum[(uint64_t)blockIdx.x * 256 + k] = s;
 }
 
+// exclusive running sums of v[(i0 + i) * 256 + k], i < n, in place; returns the total
+__device__ __forceinline__ uint32_t scan_column(uint32_t *v, uint64_t i0, uint32_t n, uint32_t k, uint32_t run) {
+    for (uint32_t b = 0; b < n; b += kScanBatch) {
+        uint32_t x[kScanBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kScanBatch; ++j)
+            if (b + j < n) x[j] = v[(i0 + b + j) * 256 + k];
+#pragma unroll
+        for (uint32_t j = 0; j < kScanBatch; ++j) {
+            if (b + j < n) {
+                v[(i0 + b + j) * 256 + k] = run;
+                run += x[j];
+            }
+        }
+    }
+    return run;
+}
+
 __global__ __launch_bounds__(256) void k_scan_mid(uint32_t *csum, const uint32_t *tcb, uint32_t *totals) {
     const uint32_t t = blockIdx.x, k = threadIdx.x;
-    uint32_t run = 0;
-    for (uint32_t c = tcb[t]; c < tcb[t + 1]; ++c) {
-        uint32_t v = csum[(uint64_t)c * 256 + k];
-        csum[(uint64_t)c * 256 + k] = run;
-        run += v;
-    }
-    totals[(uint64_t)t * 256 + k] = run;
+    totals[(uint64_t)t * 256 + k] = scan_column(csum, tcb[t], tcb[t + 1] - tcb[t], k, 0);
 }
 
 __global__ __launch_bounds__(256) void k_scan_fin(uint32_t *h, const ScanChunk *ch, const uint32_t *csum) {
     const ScanChunk c = ch[blockIdx.x];
     const uint32_t k = threadIdx.x;
-    uint32_t run = csum[(uint64_t)blockIdx.x * 256 + k];
-    for (uint32_t t = c.tile_begin; t < c.tile_end; ++t) {
-        uint32_t v = h[(uint64_t)t * 256 + k];
-        h[(uint64_t)t * 256 + k] = run;
-        run += v;
-    }
+    scan_column(h, c.tile_begin, c.tile_end - c.tile_begin, k, csum[(uint64_t)blockIdx.x * 256 + k]);
 }
 
 // ================================================================== encode: groups and placement
