@@ -434,48 +434,57 @@ __global__ __launch_bounds__(256) void k_scan_fin(uint32_t *h, const ScanChunk *
 // Groups are the non-empty (tensor, exponent) pairs in (tensor, exponent) order (codec.py:317-333).
 __global__ __launch_bounds__(1024) void k_enc_groups(const uint32_t *tot, uint32_t n_tensors, GroupDev *groups,
                                                      uint32_t *gbase, unsigned long long *counters) {
-    __shared__ uint32_t sv[1024], sz[1024];
-    __shared__ uint32_t carry_v, carry_z;
-    const uint32_t tid = threadIdx.x;
-    const uint64_t n = (uint64_t)n_tensors * 256;
-    if (tid == 0) carry_v = carry_z = 0;
+    // each thread owns a run of consecutive (tensor, exponent) totals: sums, a block scan of the
+    // sums, then the run again with its offsets
+    __shared__ unsigned long long wsum_v[16], wsum_z[16];
+    const uint32_t tid = threadIdx.x, ln = lane(), w = tid >> 6;
+    const uint64_t n = (uint64_t)n_tensors * 256, per = (n + 1023) / 1024;
+    const uint64_t lo = min64(tid * per, n), hi = min64(lo + per, n);
+    unsigned long long sv = 0, sz = 0;
+    for (uint64_t i = lo; i < hi; ++i) {
+        const uint32_t v = tot[i];
+        sv += v;
+        sz += v ? 1u : 0u;
+    }
+    unsigned long long iv = sv, iz = sz;  // inclusive scans within the wavefront
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long tv = __shfl_up(iv, o, 64), tz = __shfl_up(iz, o, 64);
+        if (ln >= (uint32_t)o) {
+            iv += tv;
+            iz += tz;
+        }
+    }
+    if (ln == 63) {
+        wsum_v[w] = iv;
+        wsum_z[w] = iz;
+    }
     __syncthreads();
-    for (uint64_t base = 0; base < n; base += 1024) {
-        const uint64_t idx = base + tid;
-        const uint32_t v = idx < n ? tot[idx] : 0u;
-        const uint32_t z = v ? 1u : 0u;
-        sv[tid] = v;
-        sz[tid] = z;
-        __syncthreads();
-        for (uint32_t off = 1; off < 1024; off <<= 1) {
-            uint32_t av = tid >= off ? sv[tid - off] : 0u, az = tid >= off ? sz[tid - off] : 0u;
-            __syncthreads();
-            sv[tid] += av;
-            sz[tid] += az;
-            __syncthreads();
+    unsigned long long ev = iv - sv, ez = iz - sz, tv = 0, tz = 0;
+    for (uint32_t q = 0; q < 16; ++q) {
+        if (q < w) {
+            ev += wsum_v[q];
+            ez += wsum_z[q];
         }
-        const uint32_t ev = carry_v + sv[tid] - v, ez = carry_z + sz[tid] - z;
-        if (idx < n) {
-            gbase[idx] = ev;
-            if (v) {
-                GroupDev g{};
-                g.tensor = (uint32_t)(idx >> 8);
-                g.exponent = (uint32_t)(idx & 255);
-                g.count = v;
-                g.elem_base = ev;
-                groups[ez] = g;
-            }
+        tv += wsum_v[q];
+        tz += wsum_z[q];
+    }
+    for (uint64_t i = lo; i < hi; ++i) {
+        const uint32_t v = tot[i];
+        gbase[i] = (uint32_t)ev;  // meaningful while the total stays below 2^32 (checked by the host)
+        if (v) {
+            GroupDev g{};
+            g.tensor = (uint32_t)(i >> 8);
+            g.exponent = (uint32_t)(i & 255);
+            g.count = v;
+            g.elem_base = (uint32_t)ev;
+            groups[ez] = g;
+            ++ez;
         }
-        __syncthreads();
-        if (tid == 1023) {
-            carry_v = ev + v;
-            carry_z = ez + z;
-        }
-        __syncthreads();
+        ev += v;
     }
     if (tid == 0) {
-        counters[0] = carry_z;  // groups
-        counters[1] = carry_v;  // changes
+        counters[0] = tz;  // groups
+        counters[1] = tv;  // changes
     }
 }
 
@@ -486,16 +495,34 @@ __global__ __launch_bounds__(1024) void k_enc_groups(const uint32_t *tot, uint32
 __global__ __launch_bounds__(64) void k_place(EncRankArgs a, const uint32_t *tile_tensor, const uint32_t *hall_pre,
                                               const uint32_t *hchg_pre, const uint32_t *gbase, uint64_t *sorted,
                                               uint64_t n_sorted) {
-    const uint32_t tau = blockIdx.x;
+    // per exponent of this slab: first group-local index, first place in update order
+    __shared__ uint32_t off_rank[256], off_dest[256];
+    const uint32_t tau = blockIdx.x, ln = lane();
     const uint32_t t = tile_tensor[tau], count = a.rec_count[tau];
     const uint64_t base = a.rec_base ? a.rec_base[tau] : (uint64_t)tau * a.rec_per_slab;
-    for (uint32_t j = lane(); j < count; j += 64) {
-        const uint64_t r = a.rec[base + j];
-        const uint32_t rank = (uint32_t)(r & 0x1FFFF), rc = (uint32_t)((r >> 17) & 0x1FFFF);
-        const uint32_t k = (uint32_t)((r >> 34) & 0xFF), zz = (uint32_t)(r >> 42);
-        const uint32_t gidx = hall_pre[(uint64_t)tau * 256 + k] + rank;
-        const uint32_t dest = gbase[(uint64_t)t * 256 + k] + hchg_pre[(uint64_t)tau * 256 + k] + rc;
-        if (dest < n_sorted) sorted[dest] = ((uint64_t)zz << 32) | gidx;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+        const uint32_t k = ln + 64 * q;
+        off_rank[k] = hall_pre[(uint64_t)tau * 256 + k];
+        off_dest[k] = gbase[(uint64_t)t * 256 + k] + hchg_pre[(uint64_t)tau * 256 + k];
+    }
+    wave_fence();
+    constexpr uint32_t U = 4;  // records per lane in flight
+    for (uint32_t j0 = 0; j0 < count; j0 += 64 * U) {
+        uint64_t r[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t j = j0 + 64 * u + ln;
+            r[u] = j < count ? a.rec[base + j] : 0ULL;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t j = j0 + 64 * u + ln;
+            const uint32_t rank = (uint32_t)(r[u] & 0x1FFFF), rc = (uint32_t)((r[u] >> 17) & 0x1FFFF);
+            const uint32_t k = (uint32_t)((r[u] >> 34) & 0xFF), zz = (uint32_t)(r[u] >> 42);
+            const uint32_t dest = off_dest[k] + rc;
+            if (j < count && dest < n_sorted) sorted[dest] = ((uint64_t)zz << 32) | (off_rank[k] + rank);
+        }
     }
 }
 
