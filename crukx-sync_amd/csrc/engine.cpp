@@ -587,7 +587,8 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     launch_tensor_sums(d_descs, T, full, t_full, s);
     launch_scan_u32(d_bb, B, boff, ar.get<unsigned long long>(scan_parts(B)), s);
 
-    uint32_t *zz = ar.get<uint32_t>(C), *local = ar.get<uint32_t>(C);
+    uint32_t *local = ar.get<uint32_t>(C);
+    unsigned long long *dz = ar.get<unsigned long long>(C);
     unsigned long long *pv = ar.get<unsigned long long>(C);
     unsigned long long *blk_sum = ar.get<unsigned long long>(B), *blk_prefix = ar.get<unsigned long long>(B + 1);
     unsigned long long *tdelta = ar.get<unsigned long long>(T), *bdelta = ar.get<unsigned long long>(B);
@@ -597,10 +598,10 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     uint32_t *lb = ar.get<uint32_t>((uint64_t)(tiles + 1) * 256);  // row tiles: read, never used
     zero(bad, 1, s);
     DecodeArgs da{pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, bmap, sizes, d_lim, d_off, d_syms, (uint32_t)syms.size(),
-                  zz, local, blk_sum, bad};
+                  dz, blk_sum, bad};
     launch_decode(da, s);
     launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), s);
-    BlockArgs ba{d_groups, (uint32_t)G, slab, bmap, d_descs, sizes, blk_prefix, local, zz, pv, bdelta, bad, B};
+    BlockArgs ba{d_groups, (uint32_t)G, slab, bmap, d_descs, sizes, blk_prefix, local, dz, pv, bdelta, bad, B};
     launch_local_fix(ba, B, s);
     uint2 *more = ar.get<uint2>(3 * (uint64_t)tiles);  // at most 3 windows after the first per slab
     unsigned int *n_more = ar.get<unsigned int>(1);

@@ -117,8 +117,7 @@ struct DecodeArgs {
     const uint32_t *off;            // [tables][17]: symbol index of code 0 of length l (mod 2^32)
     const uint32_t *syms;
     uint32_t n_syms;
-    uint32_t *zz;                   // [changes]
-    uint32_t *local;                // [changes] block-relative, then group-local index
+    unsigned long long *dz;         // [changes] zz | (block-relative local index << 32)
     unsigned long long *blk_sum;    // [blocks] sum of (gap + 1) per block
     unsigned int *bad;
 };
@@ -146,8 +145,8 @@ struct BlockArgs {                  // per-block kernels over the change list (o
     const TensorDesc *descs;
     const uint32_t *sizes;
     const unsigned long long *blk_prefix;
-    uint32_t *local;
-    const uint32_t *zz;
+    uint32_t *local;                // [changes] group-local index (written by k_local_fix)
+    const unsigned long long *dz;   // [changes] decoder output: zz | (block-relative local << 32)
     unsigned long long *pv;         // [changes] element index | bits << 32
     unsigned long long *bdelta;     // [blocks] checksum delta of each block's changes
     unsigned int *bad;

@@ -946,6 +946,7 @@ __global__ __launch_bounds__(256) void k_checksum(const uint32_t *frame, uint32_
 // of its symbol; code lengths come from comparisons of the 17-bit peek with the canonical limits
 // held in registers.  Each lane writes its block's outputs in order, so the lines fill in L2.
 constexpr uint32_t kDecPayWords = 3584;  // 28 KiB of payload per wavefront; more is read from HBM
+constexpr uint32_t kDecBuf = 8;          // changes decoded per lane between stores
 
 struct DecodeLds {
     uint64_t pay[kDecPayWords];
@@ -992,7 +993,8 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
         off[l] = a.off[(uint64_t)gr.table * 17 + l];
     }
     uint64_t rel = 0;  // sum of (gap + 1) so far in this block
-    for (uint32_t s = 0; s < cnt && !bad; ++s) {
+    // decodes change s of the block into out: zz | (block-relative local << 32); false once bad
+    auto step = [&](uint32_t s, unsigned long long &out) {
         uint64_t x = bits64<LDS_PAY>(a, S.pay, w0, cur);
         uint64_t q;
         if (~x) {  // the unary run ends inside this window
@@ -1039,9 +1041,27 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
         } else {
             rel += gap + 1;
             const uint32_t si = min(idx, a.n_syms - 1);
-            a.zz[eb + s] = LDS_SYMS ? S.syms[si] : a.syms[si];
-            a.local[eb + s] = (uint32_t)min64(rel - 1, 0xFFFFFFFFULL);
+            const uint32_t zz = LDS_SYMS ? S.syms[si] : a.syms[si];
+            out = (unsigned long long)zz | ((unsigned long long)min64(rel - 1, 0xFFFFFFFFULL) << 32);
             cur = c + rice + L;
+        }
+    };
+    // kDecBuf changes at a time, kept in registers and stored together: the block's output lines
+    // are written in few bursts instead of one 8-byte piece per change
+    unsigned long long *const dst = a.dz + eb;
+    for (uint32_t s0 = 0; s0 < cnt && !bad; s0 += kDecBuf) {
+        unsigned long long buf[kDecBuf];
+#pragma unroll
+        for (uint32_t j = 0; j < kDecBuf; ++j)
+            if (s0 + j < cnt && !bad) step(s0 + j, buf[j]);
+        if (bad) break;
+        if (s0 + kDecBuf <= cnt) {
+#pragma unroll
+            for (uint32_t j = 0; j < kDecBuf; ++j) dst[s0 + j] = buf[j];
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < kDecBuf; ++j)
+                if (s0 + j < cnt) dst[s0 + j] = buf[j];
         }
     }
     if (!bad && cur != end) bad = true;
@@ -1110,7 +1130,7 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
     }
 #pragma unroll
     for (uint32_t u = 0; u < kBlocksPerWG; ++u)
-        if (s < r[u].cnt) raw[u] = a.local[r[u].eb + s];
+        if (s < r[u].cnt) raw[u] = (uint32_t)(a.dz[r[u].eb + s] >> 32);
 #pragma unroll
     for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
         if (s < r[u].cnt) {
@@ -1484,7 +1504,7 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
     for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
         if (s < r[u].cnt) {
             pv[u] = a.pv[r[u].eb + s];
-            zz[u] = a.zz[r[u].eb + s];
+            zz[u] = (uint32_t)a.dz[r[u].eb + s];
         }
     }
 #pragma unroll
