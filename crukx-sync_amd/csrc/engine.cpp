@@ -208,8 +208,7 @@ using namespace crx;
 
 // ------------------------------------------------------------------ handles
 struct crx_update {
-    Update u;
-    std::vector<uint8_t> owned;  // empty: payload read from the caller's buffer
+    Update u;  // refers to the caller's bytes (block table, payload)
 };
 
 struct crx_encoded {
@@ -571,7 +570,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
         HIP_OK(hipMemcpyAsync(d_bb, payload_dev - (u.payload_offset - u.block_table_offset), 4 * B,
                               hipMemcpyDeviceToDevice, s));
     else
-        h2d(d_bb, u.block_bits.data(), B, s);
+        HIP_OK(hipMemcpyAsync(d_bb, u.block_table, 4 * B, hipMemcpyHostToDevice, s));
     zero(pay, pay_words, s);
     if (u.payload_len) {
         if (payload_dev)
@@ -794,10 +793,10 @@ int32_t crx_update_headers(const crx_update *u, char *names, uint64_t names_cap,
     return CRX_OK;
 }
 
-uint64_t crx_update_n_blocks(const crx_update *u) { return u->u.block_bits.size(); }
+uint64_t crx_update_n_blocks(const crx_update *u) { return u->u.n_blocks; }
 
 int32_t crx_update_block_bits(const crx_update *u, uint32_t *out) {
-    std::copy(u->u.block_bits.begin(), u->u.block_bits.end(), out);
+    if (u->u.n_blocks) std::memcpy(out, u->u.block_table, 4 * u->u.n_blocks);
     return CRX_OK;
 }
 

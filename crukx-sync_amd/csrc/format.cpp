@@ -160,6 +160,7 @@ void parse(const uint8_t *data, uint64_t avail, uint64_t total, uint8_t last, Up
         if (!(n_groups > 0 && n_groups <= 256)) throw Corrupt("bad group count");
         bool exps[256] = {};
         uint64_t sum = 0;
+        th.groups.reserve(n_groups);
         for (uint64_t g = 0; g < n_groups; ++g) {
             Group gr;
             gr.exponent = r.u8();
@@ -182,15 +183,31 @@ void parse(const uint8_t *data, uint64_t avail, uint64_t total, uint8_t last, Up
 
     if (total_blocks > r.remaining() / 4) throw Corrupt("block table longer than the update");
     u.block_table_offset = r.pos;
-    const uint8_t *bb = r.take(4 * total_blocks);
-    u.block_bits.resize(total_blocks);
-    uint64_t total_bits = 0;
-    for (uint64_t k = 0; k < total_blocks; ++k) {
-        uint32_t v = (uint32_t)bb[4 * k] | (uint32_t)bb[4 * k + 1] << 8 | (uint32_t)bb[4 * k + 2] << 16 |
-                     (uint32_t)bb[4 * k + 3] << 24;
-        u.block_bits[k] = v;
-        total_bits += v;
-    }
+    u.block_table = r.take(4 * total_blocks);
+    u.n_blocks = total_blocks;
+    static_assert(__BYTE_ORDER__ == __ORDER_LITTLE_ENDIAN__, "the block table is little-endian u32");
+    // one pass over the table: the total, and the check that each change has at least 2 + rice_r
+    // bits (wire.py:261-268; its error is raised after the payload checks, as there)
+    uint64_t total_bits = 0, b = 0, changes = 0;
+    bool short_block = false;
+    for (const TensorHeader &t : u.tensors)
+        for (const Group &g : t.groups) {
+            changes += g.count;
+            const uint64_t nb = n_blocks(g.count), full = g.count / kBlock;
+            uint32_t least = 0xFFFFFFFFu;
+            for (uint64_t k = 0; k < full; ++k) {
+                const uint32_t v = u.block_bits(b + k);
+                total_bits += v;
+                least = std::min(least, v);
+            }
+            if (full && (uint64_t)least < (uint64_t)kBlock * (2 + g.rice)) short_block = true;
+            if (nb > full) {
+                const uint32_t v = u.block_bits(b + full);
+                total_bits += v;
+                if ((uint64_t)v < (g.count - full * kBlock) * (uint64_t)(2 + g.rice)) short_block = true;
+            }
+            b += nb;
+        }
     uint64_t payload_len = r.varint();
     u.payload_offset = r.pos;
     r.skip(payload_len);
@@ -198,17 +215,7 @@ void parse(const uint8_t *data, uint64_t avail, uint64_t total, uint8_t last, Up
     if (r.remaining()) throw Corrupt("trailing bytes after the payload");
     if ((total_bits + 7) / 8 != payload_len) throw Corrupt("payload length does not match its block table");
     if ((total_bits % 8) && (last & ((1u << (8 - total_bits % 8)) - 1))) throw Corrupt("non-zero padding bits");
-    // each change costs at least 2 + rice_r bits (wire.py:261-268)
-    uint64_t b = 0, changes = 0;
-    for (const TensorHeader &t : u.tensors)
-        for (const Group &g : t.groups) {
-            changes += g.count;
-            for (uint64_t k = 0; k < n_blocks(g.count); ++k, ++b) {
-                uint64_t m = std::min<uint64_t>(kBlock, g.count - k * kBlock);
-                if ((uint64_t)u.block_bits[b] < m * (uint64_t)(2 + g.rice))
-                    throw Corrupt("block shorter than its symbols could be");
-            }
-        }
+    if (short_block) throw Corrupt("block shorter than its symbols could be");
     u.total_bits = total_bits;
     u.total_changes = changes;
 }

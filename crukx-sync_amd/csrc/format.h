@@ -4,6 +4,7 @@
 #pragma once
 
 #include <cstdint>
+#include <cstring>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -51,8 +52,16 @@ struct TensorHeader {
 struct Update {
     std::vector<Table> tables;
     std::vector<TensorHeader> tensors;
-    std::vector<uint32_t> block_bits;
+    // the block table: n_blocks little-endian u32 inside the parsed bytes (which the caller keeps
+    // alive for the life of the Update, as for the payload)
+    const uint8_t *block_table = nullptr;
+    uint64_t n_blocks = 0;
     uint64_t block_table_offset = 0;  // byte offset of the block table in the update
+    uint32_t block_bits(uint64_t k) const {
+        uint32_t v;
+        std::memcpy(&v, block_table + 4 * k, 4);
+        return v;
+    }
     uint64_t payload_offset = 0;
     uint64_t payload_len = 0;
     const uint8_t *payload_host = nullptr;  // null when the payload lives on the device

@@ -50,7 +50,8 @@ int32_t crx_abi_version(void);
  * Replaces wire.parse (src/crukx_sync/wire.py:126-212): magic, version, every limit of
  * docs/FORMAT.md:46-57 in the reference's order.  `data` holds the whole update (host memory);
  * crx_apply uploads the payload from it unless given a device copy.  For an update held in
- * device memory, crx_parse_prefix parses a host copy of its leading bytes. */
+ * device memory, crx_parse_prefix parses a host copy of its leading bytes.  The handle refers to
+ * the block table and payload in `data` / `prefix`: keep those bytes until crx_update_free. */
 int32_t crx_parse(const uint8_t *data, uint64_t len, crx_update **out, char *err, uint64_t errlen);
 /* Parses from a prefix of an update held elsewhere: `prefix` has `prefix_len` bytes of an update
  * of `total_len` bytes whose last byte is `last_byte`.  Returns CRX_OK, CRX_CORRUPT, or
