@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdio>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -256,6 +257,33 @@ void write_header(const crx_encoded &e, const char *const *names, const uint64_t
             out.push_back((uint8_t)g.rice);
         }
     }
+}
+
+// Python's repr() of a str, for names quoted in messages as the reference's f-strings do: single
+// quotes unless the name holds a single quote and no double quote; backslashes, the quote and
+// control characters escaped.
+std::string py_repr(const std::string &s) {
+    const char q = (s.find('\'') != std::string::npos && s.find('"') == std::string::npos) ? '"' : '\'';
+    std::string out(1, q);
+    for (unsigned char c : s) {
+        if (c == '\\' || c == (unsigned char)q) {
+            out += '\\';
+            out += (char)c;
+        } else if (c == '\n') {
+            out += "\\n";
+        } else if (c == '\r') {
+            out += "\\r";
+        } else if (c == '\t') {
+            out += "\\t";
+        } else if (c < 0x20 || c == 0x7F) {
+            char buf[8];
+            std::snprintf(buf, sizeof buf, "\\x%02x", c);
+            out += buf;
+        } else {
+            out += (char)c;
+        }
+    }
+    return out + q;
 }
 
 // ------------------------------------------------------------------ encode
@@ -596,7 +624,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     unsigned int *bad = ar.get<unsigned int>(1);
     uint32_t *lb = ar.get<uint32_t>((uint64_t)(tiles + 1) * 256);  // row tiles: read, never used
     zero(bad, 1, s);
-    DecodeArgs da{pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, bmap, sizes, d_lim, d_off, d_syms, (uint32_t)syms.size(),
+    DecodeArgs da{d_descs, pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, bmap, sizes, d_lim, d_off, d_syms, (uint32_t)syms.size(),
                   dz, blk_sum, bad};
     launch_decode(da, s);
     launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), s);
@@ -621,18 +649,20 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     d2h(hfull.data(), t_full, T, s);
     sync(s);
     hc.mark("apply_wait_verify");
-    if (hbad & kBadDecode) throw Corrupt("payload does not decode to its block table");
-    if (hbad) throw Corrupt("payload positions outside their exponent groups");
+    // the reference's verdict (codec.py:598-604,696-712): the group-size check first, then any
+    // checksum mismatch (naming up to three tensors), then any other inconsistency
+    if (hbad & kBadGroup) throw Corrupt("group has more changes than elements");
     std::vector<std::string> wrong;
     for (uint32_t t = 0; t < T; ++t) {
         const uint64_t old = (has_cache && has_cache[t]) ? cache_vals[t] : hfull[t];
         if (old + hdelta[t] != u.tensors[t].checksum) wrong.push_back(u.tensors[t].name);
     }
     if (!wrong.empty()) {
-        std::string m = "update does not verify (checksum mismatch: ";
-        for (size_t i = 0; i < std::min<size_t>(3, wrong.size()); ++i) m += (i ? ", '" : "'") + wrong[i] + "'";
-        throw Corrupt(m + ")");
+        std::string m = "update does not verify (checksum mismatch: [";
+        for (size_t i = 0; i < std::min<size_t>(3, wrong.size()); ++i) m += (i ? ", " : "") + py_repr(wrong[i]);
+        throw Corrupt(m + "])");
     }
+    if (hbad) throw Corrupt("payload positions outside their exponent groups");
     launch_scatter(ba, B, s);
     sync(s);
     hc.mark("apply_wait_scatter");

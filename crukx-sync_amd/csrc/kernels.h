@@ -20,6 +20,10 @@ constexpr int32_t kFar = 0x40000000;  // "no target in this slab" for the select
 constexpr unsigned int kBadDecode = 1;    // a block does not decode exactly to its length
 constexpr unsigned int kBadLocal = 2;     // a change lies beyond its exponent group
 constexpr unsigned int kBadUnplaced = 4;  // a change was not found in the receiver's weights
+// a group has more changes than its tensor has elements of that exponent, in a tensor of more than
+// 2^24 elements (the reference raises this before decoding, codec.py:598-604)
+constexpr unsigned int kBadGroup = 8;
+constexpr uint64_t kGroupCheckNumel = 1ULL << 24;
 
 // One tensor of a call.  Elements are read as 32-bit words from `frame`, the 4-byte aligned address
 // at or below the first element: tensor element i is 16-bit frame element i + lead.
@@ -104,6 +108,7 @@ struct CodeArgs {
 };
 
 struct DecodeArgs {
+    const TensorDesc *descs;
     const uint64_t *payload;        // big-endian byte stream, 8-byte aligned, zero padded
     uint64_t n_words;
     const uint32_t *block_bits;

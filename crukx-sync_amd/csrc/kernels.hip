@@ -986,7 +986,11 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
     const uint64_t qmax = size >> rice;
     uint64_t cur = a.block_off[b];
     const uint64_t end = cur + a.block_bits[b];
-    bool bad = kb == 0 && gr.count > size;  // a group with more changes than elements
+    bool bad = false;
+    if (kb == 0 && gr.count > size) {  // a group with more changes than elements
+        bad = true;
+        atomicOr(a.bad, a.descs[gr.tensor].numel > kGroupCheckNumel ? kBadGroup : kBadLocal);
+    }
 #pragma unroll
     for (int l = 0; l < 17; ++l) {
         lim[l] = a.lim[(uint64_t)gr.table * 17 + l];
@@ -1492,8 +1496,12 @@ __global__ __launch_bounds__(64) void k_select_more(SelectArgs a) {
 // new = (old + unzigzag(zz)) mod 2^16; checksum delta per tensor (codec.py:698-700).
 __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
     __shared__ unsigned long long sh[kBlocksPerWG][256];
-    if (*a.bad) return;
     const uint32_t s = threadIdx.x;
+    if (*a.bad) {  // positions were not computed: deltas of zero, so the verdict is deterministic
+        const uint64_t b = (uint64_t)blockIdx.x * kBlocksPerWG + s;
+        if (s < kBlocksPerWG && b < a.n_blocks) a.bdelta[b] = 0;
+        return;
+    }
     GroupDev gr[kBlocksPerWG];
     BlockRef r[kBlocksPerWG];
     unsigned long long pv[kBlocksPerWG];

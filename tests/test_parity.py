@@ -235,3 +235,35 @@ def test_receiver_exponent_counts_carried_across_updates():
             assert codec._hist_lookup(recv[n]) is None
     finally:
         codec._SLAB = old_slab
+
+
+def test_verdict_messages_follow_the_reference():
+    """apply's error messages and their priority are the reference's (codec.py:598-604,706-712):
+    the group-size check of tensors over 2^24 elements first, then checksum mismatches naming up to
+    three tensors as a Python list, then other inconsistencies."""
+    names = ["x", "it's", 'q"t', "z"]
+    g = torch.Generator().manual_seed(21)
+    old = {n: (torch.randn(5000, generator=g) * 0.02).bfloat16() for n in names}
+    new = {k: (v.float() + 3e-5 * torch.randn(v.shape, generator=g)).bfloat16() for k, v in old.items()}
+    upd = crukx_sync.encode_update(_cuda(old), _cuda(new))
+    recv = _cuda(old)
+    wrong = {n: (12345, recv[n]._version) for n in names}
+    with pytest.raises(crukx_sync.CorruptUpdate) as e:
+        crukx_sync.apply_update(recv, upd, wrong)
+    assert str(e.value) == f"update does not verify (checksum mismatch: {names[:3]})"
+    for n in names:
+        assert torch.equal(recv[n].cpu().view(torch.int16), old[n].view(torch.int16))
+
+    # a group with more changes than the receiver has elements of its exponent
+    n = (1 << 24) + 1000
+    base = torch.full((n,), 0x3F80, dtype=torch.int16)
+    sender = base.clone()
+    sender[100:105] = 0x3C00  # five elements of exponent 120
+    target = sender.clone()
+    target[100:105] += 1
+    upd = crukx_sync.encode_update({"w": sender.cuda()}, {"w": target.cuda()})
+    short = base.clone()
+    short[100:103] = 0x3C00  # the receiver has three
+    with pytest.raises(crukx_sync.CorruptUpdate) as e:
+        crukx_sync.apply_update({"w": short.cuda()}, upd)
+    assert str(e.value) == "group has more changes than elements"
