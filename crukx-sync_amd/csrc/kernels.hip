@@ -16,7 +16,7 @@ constexpr uint64_t kMix1 = 0xBF58476D1CE4E5B9ULL;
 constexpr uint64_t kMix2 = 0x94D049BB133111EBULL;
 constexpr int kRankRows = 8;    // rows per batch of the encode rank pass (two streams)
 constexpr uint32_t kRankCopies = 4;  // copies of each exponent count in the encode rank pass (2 or 4)
-static_assert(kRankCopies == 2 || kRankCopies == 4, "kRankCopies");
+static_assert(kRankCopies == 2 || kRankCopies == 4 || kRankCopies == 8, "kRankCopies");
 constexpr int kScanRows = 16;   // rows per batch of the apply histogram pass
 constexpr int kSelectRows = 12; // ... of the select pass (fewer registers: occupancy)
 
@@ -214,8 +214,13 @@ __device__ __forceinline__ uint32_t rank_count(const uint32_t *hall, uint32_t k)
         const uint2 h = *reinterpret_cast<const uint2 *>(&hall[2 * k]);
         return h.x + h.y;
     }
-    const uint4 h = *reinterpret_cast<const uint4 *>(&hall[4 * k]);
-    return h.x + h.y + h.z + h.w;
+    uint32_t s = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < kRankCopies; q += 4) {
+        const uint4 h = *reinterpret_cast<const uint4 *>(&hall[kRankCopies * k + q]);
+        s += h.x + h.y + h.z + h.w;
+    }
+    return s;
 }
 
 template <bool COLD>
