@@ -348,8 +348,8 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
         zero(ovf, 1, s);
         launch_enc_rank(a, tiles, s);
     }
-    launch_scan_tables(hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_all, s);
-    launch_scan_tables(hchg, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_chg, s);
+    launch_scan_tables(d_descs, hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_all, s);
+    launch_scan_tables(d_descs, hchg, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_chg, s);
     launch_enc_groups(tot_chg, T, d_groups, gbase, gcnt, s);
     unsigned long long gc[2];
     d2h(gc, gcnt, 2, s);
@@ -607,10 +607,24 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
             HIP_OK(hipMemcpyAsync(pay, u.payload_host, u.payload_len, hipMemcpyHostToDevice, s));
     }
 
-    // pass A: receiver exponent histograms (+ full old checksums on a cache miss)
-    HistArgs ha{d_descs, sd.tile_tensor, T, slab, hall, full};
-    launch_hist(ha, tiles, s);
-    launch_scan_tables(hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, sizes, s);
+    // pass A: slabs of tensors without cached counts are streamed (their counts, and old checksums
+    // when cold); cached counts are read by the scan in place (copied only to a separate hist_out)
+    std::vector<uint32_t> hist_list;
+    for (const TensorDesc &d : L.descs) {
+        const bool cached = d.hist_in && !d.cold;
+        if (!cached || (d.hist_out && d.hist_out != d.hist_in))
+            for (uint32_t i = 0; i < d.n_tiles; ++i) hist_list.push_back(d.tile_begin + i);
+    }
+    HistArgs ha{d_descs, sd.tile_tensor, T, slab, hall, full, nullptr};
+    if (hist_list.size() == tiles) {
+        launch_hist(ha, tiles, s);
+    } else if (!hist_list.empty()) {
+        uint32_t *d_list = ar.get<uint32_t>(hist_list.size());
+        h2d(d_list, hist_list.data(), hist_list.size(), s);
+        ha.list = d_list;
+        launch_hist(ha, (uint32_t)hist_list.size(), s);
+    }
+    launch_scan_tables(d_descs, hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, sizes, s);
     launch_tensor_sums(d_descs, T, full, t_full, s);
     launch_scan_u32(d_bb, B, boff, ar.get<unsigned long long>(scan_parts(B)), s);
 

@@ -72,6 +72,7 @@ struct HistArgs {
     uint32_t n_tensors, slab;
     uint32_t *hall;                 // [tiles][256]
     uint64_t *full;                 // [tiles]
+    const uint32_t *list;           // the slabs to process (one workgroup each), or null for all
 };
 
 struct ScanChunk {                  // SCAN_TILES consecutive slabs of one tensor
@@ -159,9 +160,13 @@ struct BlockArgs {                  // per-block kernels over the change list (o
 };
 
 void launch_enc_rank(const EncRankArgs &a, uint32_t tiles, hipStream_t s);
-void launch_hist(const HistArgs &a, uint32_t tiles, hipStream_t s);
-void launch_scan_tables(uint32_t *h, const ScanChunk *chunks, uint32_t n_chunks, const uint32_t *tensor_chunk_begin,
-                        uint32_t n_tensors, uint32_t *csum, uint32_t *totals, hipStream_t s);
+// Histograms of the listed slabs (all when a.list is null): n workgroups.
+void launch_hist(const HistArgs &a, uint32_t n, hipStream_t s);
+// Per-tensor exclusive scans over slabs of per-slab exponent tables, in place; slabs of tensors with
+// cached counts (descs: hist_in and not cold) are read from those counts.
+void launch_scan_tables(const TensorDesc *descs, uint32_t *h, const ScanChunk *chunks, uint32_t n_chunks,
+                        const uint32_t *tensor_chunk_begin, uint32_t n_tensors, uint32_t *csum, uint32_t *totals,
+                        hipStream_t s);
 void launch_enc_groups(const uint32_t *totals_chg, uint32_t n_tensors, GroupDev *groups, uint32_t *gbase,
                        unsigned long long *counters, hipStream_t s);
 void launch_place(const EncRankArgs &a, uint32_t tiles, const uint32_t *tile_tensor,

@@ -373,16 +373,11 @@ __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau,
 
 __global__ __launch_bounds__(64) void k_hist(HistArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t hall[257 * kHistCopies];
-    const uint32_t tau = blockIdx.x;
+    const uint32_t tau = a.list ? a.list[blockIdx.x] : blockIdx.x;
     const TensorDesc td = a.descs[a.tile_tensor[tau]];
-    if (td.hist_in && !td.cold) {  // counts recorded by the previous update of these weights
+    if (td.hist_in && !td.cold) {  // counts recorded by the previous update: copied to a separate hist_out
         const uint64_t at = (uint64_t)(tau - td.tile_begin) * 256;
-        for (uint32_t k = lane(); k < 256; k += 64) {
-            const uint32_t v = td.hist_in[at + k];
-            a.hall[(uint64_t)tau * 256 + k] = v;
-            if (td.hist_out && td.hist_out != td.hist_in) td.hist_out[at + k] = v;
-        }
-        if (lane() == 0) a.full[tau] = 0;
+        for (uint32_t k = lane(); k < 256; k += 64) td.hist_out[at + k] = td.hist_in[at + k];
         return;
     }
     const Slab sl = slab_of(td, tau - td.tile_begin, a.slab);
@@ -398,25 +393,35 @@ __global__ __launch_bounds__(64) void k_hist(HistArgs a) {
 // the compiler knows), so a batch costs one memory latency instead of one per value.
 constexpr uint32_t kScanBatch = 16;
 
-__global__ __launch_bounds__(256) void k_scan_sum(const uint32_t *h, const ScanChunk *ch, uint32_t *csum) {
+// Per-slab counts of slab t of a chunk's tensor: the receiver's cached counts when the apply uses
+// them (the histogram pass skipped those slabs), else the table being scanned.
+__device__ __forceinline__ const uint32_t *scan_src(const TensorDesc &td, const uint32_t *h, uint32_t t) {
+    return (td.hist_in && !td.cold) ? td.hist_in + (uint64_t)(t - td.tile_begin) * 256 : h + (uint64_t)t * 256;
+}
+
+__global__ __launch_bounds__(256) void k_scan_sum(const TensorDesc *descs, const uint32_t *h, const ScanChunk *ch,
+                                                  uint32_t *csum) {
     const ScanChunk c = ch[blockIdx.x];
+    const TensorDesc td = descs[c.tensor];
     const uint32_t k = threadIdx.x;
     uint32_t s = 0;
-    for (uint32_t t = c.tile_begin; t < c.tile_end; ++t) s += h[(uint64_t)t * 256 + k];
+    for (uint32_t t = c.tile_begin; t < c.tile_end; ++t) s += scan_src(td, h, t)[k];
     csum[(uint64_t)blockIdx.x * 256 + k] = s;
 }
 
-// exclusive running sums of v[(i0 + i) * 256 + k], i < n, in place; returns the total
-__device__ __forceinline__ uint32_t scan_column(uint32_t *v, uint64_t i0, uint32_t n, uint32_t k, uint32_t run) {
+// exclusive running sums of src column k over rows i0 .. i0 + n into dst (which may be src);
+// src(i) and dst(i) give row i.  Returns the total.
+template <typename Src, typename Dst>
+__device__ __forceinline__ uint32_t scan_column(Src src, Dst dst, uint32_t i0, uint32_t n, uint32_t k, uint32_t run) {
     for (uint32_t b = 0; b < n; b += kScanBatch) {
         uint32_t x[kScanBatch];
 #pragma unroll
         for (uint32_t j = 0; j < kScanBatch; ++j)
-            if (b + j < n) x[j] = v[(i0 + b + j) * 256 + k];
+            if (b + j < n) x[j] = src(i0 + b + j)[k];
 #pragma unroll
         for (uint32_t j = 0; j < kScanBatch; ++j) {
             if (b + j < n) {
-                v[(i0 + b + j) * 256 + k] = run;
+                dst(i0 + b + j)[k] = run;
                 run += x[j];
             }
         }
@@ -426,13 +431,18 @@ __device__ __forceinline__ uint32_t scan_column(uint32_t *v, uint64_t i0, uint32
 
 __global__ __launch_bounds__(256) void k_scan_mid(uint32_t *csum, const uint32_t *tcb, uint32_t *totals) {
     const uint32_t t = blockIdx.x, k = threadIdx.x;
-    totals[(uint64_t)t * 256 + k] = scan_column(csum, tcb[t], tcb[t + 1] - tcb[t], k, 0);
+    auto row = [&](uint32_t i) { return csum + (uint64_t)i * 256; };
+    totals[(uint64_t)t * 256 + k] = scan_column(row, row, tcb[t], tcb[t + 1] - tcb[t], k, 0);
 }
 
-__global__ __launch_bounds__(256) void k_scan_fin(uint32_t *h, const ScanChunk *ch, const uint32_t *csum) {
+__global__ __launch_bounds__(256) void k_scan_fin(const TensorDesc *descs, uint32_t *h, const ScanChunk *ch,
+                                                  const uint32_t *csum) {
     const ScanChunk c = ch[blockIdx.x];
+    const TensorDesc td = descs[c.tensor];
     const uint32_t k = threadIdx.x;
-    scan_column(h, c.tile_begin, c.tile_end - c.tile_begin, k, csum[(uint64_t)blockIdx.x * 256 + k]);
+    auto src = [&](uint32_t t) { return scan_src(td, h, t); };
+    auto dst = [&](uint32_t t) { return h + (uint64_t)t * 256; };
+    scan_column(src, dst, c.tile_begin, c.tile_end - c.tile_begin, k, csum[(uint64_t)blockIdx.x * 256 + k]);
 }
 
 // ================================================================== encode: groups and placement
@@ -1584,13 +1594,14 @@ inline uint32_t grid1(uint64_t n, uint32_t per) { return (uint32_t)((n + per - 1
 void launch_enc_rank(const EncRankArgs &a, uint32_t tiles, hipStream_t s) {
     CRX_LAUNCH("enc_rank", k_enc_rank, tiles, 64, s, a);
 }
-void launch_hist(const HistArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("apply_hist", k_hist, tiles, 64, s, a); }
+void launch_hist(const HistArgs &a, uint32_t n, hipStream_t s) { CRX_LAUNCH("apply_hist", k_hist, n, 64, s, a); }
 
-void launch_scan_tables(uint32_t *h, const ScanChunk *chunks, uint32_t n_chunks, const uint32_t *tensor_chunk_begin,
-                        uint32_t n_tensors, uint32_t *csum, uint32_t *totals, hipStream_t s) {
-    CRX_LAUNCH("scan_sum", k_scan_sum, n_chunks, 256, s, h, chunks, csum);
+void launch_scan_tables(const TensorDesc *descs, uint32_t *h, const ScanChunk *chunks, uint32_t n_chunks,
+                        const uint32_t *tensor_chunk_begin, uint32_t n_tensors, uint32_t *csum, uint32_t *totals,
+                        hipStream_t s) {
+    CRX_LAUNCH("scan_sum", k_scan_sum, n_chunks, 256, s, descs, h, chunks, csum);
     CRX_LAUNCH("scan_mid", k_scan_mid, n_tensors, 256, s, csum, tensor_chunk_begin, totals);
-    CRX_LAUNCH("scan_fin", k_scan_fin, n_chunks, 256, s, h, chunks, csum);
+    CRX_LAUNCH("scan_fin", k_scan_fin, n_chunks, 256, s, descs, h, chunks, csum);
 }
 
 void launch_enc_groups(const uint32_t *totals_chg, uint32_t n_tensors, GroupDev *groups, uint32_t *gbase,
