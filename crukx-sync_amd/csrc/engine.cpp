@@ -38,7 +38,18 @@ std::mutex g_tmu;
 bool g_timing = false;
 hipEvent_t g_open = nullptr;
 std::vector<Pending> g_pending;
+std::vector<hipEvent_t> g_free;  // events reused across launches (creating one per launch costs host time)
 std::map<std::string, Stat> g_stats;
+
+hipEvent_t take_event() {  // under g_tmu
+    if (!g_free.empty()) {
+        hipEvent_t e = g_free.back();
+        g_free.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+}
 
 void timing_collect() {
     std::lock_guard<std::mutex> lk(g_tmu);
@@ -48,8 +59,8 @@ void timing_collect() {
             g_stats[p.name].calls++;
             g_stats[p.name].ms += ms;
         }
-        (void)hipEventDestroy(p.a);
-        (void)hipEventDestroy(p.b);
+        g_free.push_back(p.a);
+        g_free.push_back(p.b);
     }
     g_pending.clear();
 }
@@ -58,8 +69,8 @@ void timing_collect() {
 void timing_begin(hipStream_t s) {
     if (!g_timing) return;
     std::lock_guard<std::mutex> lk(g_tmu);
-    hipEvent_t e;
-    if (hipEventCreate(&e) != hipSuccess) return;
+    hipEvent_t e = take_event();
+    if (!e) return;
     (void)hipEventRecord(e, s);
     g_open = e;
 }
@@ -68,8 +79,8 @@ void timing_end(const char *name, hipStream_t s) {
     if (!g_timing) return;
     std::lock_guard<std::mutex> lk(g_tmu);
     if (!g_open) return;
-    hipEvent_t e;
-    if (hipEventCreate(&e) != hipSuccess) return;
+    hipEvent_t e = take_event();
+    if (!e) return;
     (void)hipEventRecord(e, s);
     g_pending.push_back(Pending{name, g_open, e});
     g_open = nullptr;
@@ -87,6 +98,45 @@ struct HostClock {
         st.calls++;
         st.ms += std::chrono::duration<double, std::milli>(n - t).count();
         t = n;
+    }
+};
+
+// ------------------------------------------------------------------ auxiliary stream
+// One extra stream per device (default priority, created on first use, kept for the process) for
+// work of a call that can overlap the caller's stream.  A Fork makes it wait for everything enqueued
+// on the caller's stream so far; join() makes the caller's stream wait for what was enqueued on it.
+hipStream_t aux_stream() {
+    static std::mutex mu;
+    static std::map<int, hipStream_t> streams;
+    int dev = 0;
+    HIP_OK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(mu);
+    hipStream_t &st = streams[dev];
+    if (!st) HIP_OK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    return st;
+}
+
+struct Fork {
+    hipStream_t main, aux;
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    bool joined = false;
+    explicit Fork(hipStream_t s) : main(s), aux(aux_stream()) {
+        HIP_OK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
+        HIP_OK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
+        HIP_OK(hipEventRecord(ev[0], main));
+        HIP_OK(hipStreamWaitEvent(aux, ev[0], 0));
+    }
+    void join() {
+        HIP_OK(hipEventRecord(ev[1], aux));
+        HIP_OK(hipStreamWaitEvent(main, ev[1], 0));
+        joined = true;
+    }
+    ~Fork() {
+        // an exception before join(): the caller's stream still waits for the auxiliary work, which
+        // uses buffers the caller frees after the call
+        if (!joined && hipEventRecord(ev[1], aux) == hipSuccess) (void)hipStreamWaitEvent(main, ev[1], 0);
+        (void)hipEventDestroy(ev[0]);
+        (void)hipEventDestroy(ev[1]);
     }
 };
 
@@ -573,39 +623,61 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     for (int64_t t = (int64_t)T - 1; t >= 0; --t) tensor_blk[t] = std::min(tensor_blk[t], tensor_blk[t + 1]);
 
     hc.mark("apply_tables");
+    // what the decoder needs goes first: it starts while the rest is enqueued
     TensorDesc *d_descs = ar.get<TensorDesc>(T);
     h2d(d_descs, L.descs.data(), T, s);
-    uint32_t *hall = ar.get<uint32_t>((uint64_t)tiles * 256);
-    uint64_t *full = ar.get<uint64_t>(tiles), *t_full = ar.get<uint64_t>(T);
-    ScanDev sd = upload_scan(ar, L, d_descs, s);
-    uint32_t *sizes = ar.get<uint32_t>((uint64_t)T * 256);
     GroupDev *d_groups = ar.get<GroupDev>(G);
-    int32_t *d_gof = ar.get<int32_t>((uint64_t)T * 256);
-    uint32_t *d_lim = ar.get<uint32_t>(lim.size()), *d_off = ar.get<uint32_t>(off.size());
-    uint32_t *d_syms = ar.get<uint32_t>(syms.size());
-    uint32_t *d_bb = ar.get<uint32_t>(B);
-    unsigned long long *boff = ar.get<unsigned long long>(B + 1);
-    const uint64_t pay_words = (u.payload_len + 7) / 8 + 2;
-    uint64_t *pay = ar.get<uint64_t>(pay_words);
     h2d(d_groups, groups.data(), G, s);
-    h2d(d_gof, group_of.data(), group_of.size(), s);
     uint32_t *bmap = ar.get<uint32_t>(B);
     launch_block_map(d_groups, (uint32_t)G, bmap, s);
+    uint32_t *d_lim = ar.get<uint32_t>(lim.size()), *d_off = ar.get<uint32_t>(off.size());
+    uint32_t *d_syms = ar.get<uint32_t>(syms.size());
     h2d(d_lim, lim.data(), lim.size(), s);
     h2d(d_off, off.data(), off.size(), s);
     h2d(d_syms, syms.data(), syms.size(), s);
+    uint32_t *d_bb = ar.get<uint32_t>(B);
     if (payload_dev)  // the update is in device memory: its block table precedes the payload there
         HIP_OK(hipMemcpyAsync(d_bb, payload_dev - (u.payload_offset - u.block_table_offset), 4 * B,
                               hipMemcpyDeviceToDevice, s));
     else
         HIP_OK(hipMemcpyAsync(d_bb, u.block_table, 4 * B, hipMemcpyHostToDevice, s));
-    zero(pay, pay_words, s);
+    const uint64_t pay_words = (u.payload_len + 7) / 8 + 2;
+    uint64_t *pay = ar.get<uint64_t>(pay_words);
+    // the copy fills whole words up to payload_len / 8; the rest (partial last word, two pad words) is zeroed
+    zero(pay + u.payload_len / 8, pay_words - u.payload_len / 8, s);
     if (u.payload_len) {
         if (payload_dev)
             HIP_OK(hipMemcpyAsync(pay, payload_dev, u.payload_len, hipMemcpyDeviceToDevice, s));
         else
             HIP_OK(hipMemcpyAsync(pay, u.payload_host, u.payload_len, hipMemcpyHostToDevice, s));
     }
+    unsigned int *bad = ar.get<unsigned int>(1);
+    zero(bad, 1, s);
+    unsigned long long *boff = ar.get<unsigned long long>(B + 1);
+    launch_scan_u32(d_bb, B, boff, ar.get<unsigned long long>(scan_parts(B)), s);
+
+    // The decoder needs nothing from the receiver's weights: it runs on the auxiliary stream while
+    // the main stream takes the exponent counts (pass A) and their scans.
+    unsigned long long *dz = ar.get<unsigned long long>(C);
+    unsigned long long *blk_sum = ar.get<unsigned long long>(B), *blk_prefix = ar.get<unsigned long long>(B + 1);
+    Fork fork(s);
+    DecodeArgs da{d_descs, pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, bmap, d_lim, d_off, d_syms,
+                  (uint32_t)syms.size(), dz, blk_sum, bad};
+    launch_decode(da, fork.aux);
+    launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), fork.aux);
+
+    uint32_t *hall = ar.get<uint32_t>((uint64_t)tiles * 256);
+    uint64_t *full = ar.get<uint64_t>(tiles), *t_full = ar.get<uint64_t>(T);
+    ScanDev sd = upload_scan(ar, L, d_descs, s);
+    uint32_t *sizes = ar.get<uint32_t>((uint64_t)T * 256);
+    int32_t *d_gof = ar.get<int32_t>((uint64_t)T * 256);
+    h2d(d_gof, group_of.data(), group_of.size(), s);
+    uint32_t *local = ar.get<uint32_t>(C);
+    unsigned long long *pv = ar.get<unsigned long long>(C);
+    unsigned long long *tdelta = ar.get<unsigned long long>(T), *bdelta = ar.get<unsigned long long>(B);
+    uint32_t *tblk = ar.get<uint32_t>(T + 1);
+    h2d(tblk, tensor_blk.data(), T + 1, s);
+    uint32_t *lb = ar.get<uint32_t>((uint64_t)(tiles + 1) * 256);  // row tiles: read, never used
 
     // pass A: slabs of tensors without cached counts are streamed (their counts, and old checksums
     // when cold); cached counts are read by the scan in place (copied only to a separate hist_out)
@@ -626,22 +698,8 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     }
     launch_scan_tables(d_descs, hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, sizes, s);
     launch_tensor_sums(d_descs, T, full, t_full, s);
-    launch_scan_u32(d_bb, B, boff, ar.get<unsigned long long>(scan_parts(B)), s);
+    fork.join();
 
-    uint32_t *local = ar.get<uint32_t>(C);
-    unsigned long long *dz = ar.get<unsigned long long>(C);
-    unsigned long long *pv = ar.get<unsigned long long>(C);
-    unsigned long long *blk_sum = ar.get<unsigned long long>(B), *blk_prefix = ar.get<unsigned long long>(B + 1);
-    unsigned long long *tdelta = ar.get<unsigned long long>(T), *bdelta = ar.get<unsigned long long>(B);
-    uint32_t *tblk = ar.get<uint32_t>(T + 1);
-    h2d(tblk, tensor_blk.data(), T + 1, s);
-    unsigned int *bad = ar.get<unsigned int>(1);
-    uint32_t *lb = ar.get<uint32_t>((uint64_t)(tiles + 1) * 256);  // row tiles: read, never used
-    zero(bad, 1, s);
-    DecodeArgs da{d_descs, pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, bmap, sizes, d_lim, d_off, d_syms, (uint32_t)syms.size(),
-                  dz, blk_sum, bad};
-    launch_decode(da, s);
-    launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), s);
     BlockArgs ba{d_groups, (uint32_t)G, slab, bmap, d_descs, sizes, blk_prefix, local, dz, pv, bdelta, bad, B};
     launch_local_fix(ba, B, s);
     uint2 *more = ar.get<uint2>(3 * (uint64_t)tiles);  // at most 3 windows after the first per slab

@@ -118,7 +118,6 @@ struct DecodeArgs {
     const GroupDev *groups;
     uint32_t n_groups;
     const uint32_t *bmap;           // [blocks] group of every block
-    const uint32_t *sizes;          // [tensor][256] group sizes of the receiver
     const uint32_t *lim;            // [tables][17]: end of length l's codes, left-justified to 17 bits
     const uint32_t *off;            // [tables][17]: symbol index of code 0 of length l (mod 2^32)
     const uint32_t *syms;

@@ -996,16 +996,14 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
     const uint64_t kb = b - gr.blk_base;
     const uint32_t cnt = (uint32_t)min64(256, gr.count - kb * 256);
     const uint64_t eb = (uint64_t)gr.elem_base + kb * 256;
-    const uint64_t size = a.sizes[(uint64_t)gr.tensor * 256 + gr.exponent];
+    // the decoder does not need the receiver's exponent counts (k_local_fix checks positions against
+    // them): unary runs are bounded by the tensor's size, which bounds any valid gap
+    const uint64_t size = a.descs[gr.tensor].numel;
     const uint32_t rice = gr.rice;
     const uint64_t qmax = size >> rice;
     uint64_t cur = a.block_off[b];
     const uint64_t end = cur + a.block_bits[b];
     bool bad = false;
-    if (kb == 0 && gr.count > size) {  // a group with more changes than elements
-        bad = true;
-        atomicOr(a.bad, a.descs[gr.tensor].numel > kGroupCheckNumel ? kBadGroup : kBadLocal);
-    }
 #pragma unroll
     for (int l = 0; l < 17; ++l) {
         lim[l] = a.lim[(uint64_t)gr.table * 17 + l];
@@ -1056,7 +1054,7 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
         const uint32_t idx = o[0] + (L <= 17 ? peek >> (17 - L) : 0u);
         const uint64_t gap = (q << rice) | rem;
         if (q > qmax || cur + q >= end || L > 17 || gap >= size) {
-            bad = true;
+            bad = true;  // positions past the group's exponent count are caught by k_local_fix
         } else {
             rel += gap + 1;
             const uint32_t si = min(idx, a.n_syms - 1);
@@ -1129,9 +1127,9 @@ __device__ __forceinline__ BlockRef block_ref(const BlockArgs &a, uint64_t b, Gr
 }
 
 // local = (sum of (gap + 1) over earlier blocks of the group) + block-relative local; must stay
-// below the group size (codec.py:640-642,696-697).
+// below the group size (codec.py:640-642,696-697).  Also the group-size check (codec.py:598-604).
 __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
-    if (*a.bad) return;
+    const bool failed = *a.bad;  // read before this kernel's own flags
     const uint32_t s = threadIdx.x;
     GroupDev gr[kBlocksPerWG];
     BlockRef r[kBlocksPerWG];
@@ -1145,8 +1143,13 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
         if (r[u].cnt) {
             size[u] = a.sizes[(uint64_t)gr[u].tensor * 256 + gr[u].exponent];
             base[u] = a.blk_prefix[b] - a.blk_prefix[gr[u].blk_base];
+            // a group with more changes than the receiver has elements of its exponent (checked even
+            // after a failed decode: the reference checks it first)
+            if (b == gr[u].blk_base && gr[u].count > size[u] && threadIdx.x == 0)
+                atomicOr(a.bad, a.descs[gr[u].tensor].numel > kGroupCheckNumel ? kBadGroup : kBadLocal);
         }
     }
+    if (failed) return;
 #pragma unroll
     for (uint32_t u = 0; u < kBlocksPerWG; ++u)
         if (s < r[u].cnt) raw[u] = (uint32_t)(a.dz[r[u].eb + s] >> 32);
