@@ -40,7 +40,8 @@ def main():
     ap.add_argument("--p-one", type=float, default=0.87)
     ap.add_argument("--cpu-baseline-layers", type=int, default=2,
                     help="decoder layers in the CPU baseline sample (0 disables it)")
-    ap.add_argument("--host-bytes", action="store_true", help="also time the bytes API (PCIe-inclusive)")
+    ap.add_argument("--host-bytes", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time the bytes API (PCIe-inclusive; reported in detail, never in value)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run three 2 GiB device-to-device copies (reference for HBM traffic counters)")
     args = ap.parse_args()
@@ -139,6 +140,10 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic(args.workload, args.rho, dom),
                 "avg_launch_ms": round(avg_ms, 4), "alg_bytes_per_launch": alg_bytes[dom]}
+    copy_gbs, read_gbs = stream_ceilings(torch, dev)
+    roofline["copy_gbs"] = round(copy_gbs, 1)  # measured ceilings: device-to-device copy (read + write bytes)
+    roofline["read_gbs"] = round(read_gbs, 1)  # and a read-only reduction
+    roofline["frac_of_copy"] = round(achieved / copy_gbs, 4)
     whole = (6 * N + upd_bytes + 2 * changes) / (ms_step * 1e-3) / 1e9  # encode 4N+P, apply 2N+P+2C
 
     detail = {"encode_ms": round(enc_ms, 3), "apply_ms": round(app_ms, 3),
@@ -175,6 +180,37 @@ def main():
                       "tensors": len(shapes), "weights": N, "rho": args.rho},
            "roofline": roofline, "cpu_baseline": cpu, "detail": detail}
     print(json.dumps(out), flush=True)
+
+
+def stream_ceilings(torch, dev, nbytes=4 << 30, reps=5):
+    """Best rates (GB/s) of a device-to-device copy of nbytes (read + write bytes) and of a sum over
+    them (read only): achievable HBM ceilings to set beside the 8 TB/s peak."""
+    a = torch.ones(nbytes // 8, dtype=torch.int64, device=dev)
+    b = torch.empty_like(a)
+    best_c = best_r = float("inf")
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        b.copy_(a)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        a.sum()
+        torch.cuda.synchronize()
+        best_c = min(best_c, t1 - t)
+        best_r = min(best_r, time.perf_counter() - t1)
+    del a, b
+    return 2 * nbytes / best_c / 1e9, nbytes / best_r / 1e9
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
 
 
 def measured_traffic(workload, rho, kernel):
@@ -219,8 +255,8 @@ def cpu_baseline(args, shapes, states, N, log):
         f"-> {ms / 1e3:.1f}s per full update")
     return {"value": round(ms, 1), "unit": "ms", "cores": 1, "kind": "port",
             "sample": f"decoder layers 0..{layers - 1} of the same synthetic step ({n_sample} of {N} weights, "
-                      f"warm checksum caches), encode + apply by the C oracle on one host core, time scaled by "
-                      f"{scale:.2f} to the full update",
+                      f"warm checksum caches), encode + apply by the C oracle on one host core ({cpu_model()}), "
+                      f"time scaled by {scale:.2f} to the full update",
             "sample_encode_s": round(t1 - t0, 3), "sample_apply_s": round(t2 - t1, 3)}
 
 
