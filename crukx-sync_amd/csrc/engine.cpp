@@ -140,6 +140,53 @@ struct Fork {
     }
 };
 
+// ------------------------------------------------------------------ device-to-host copies
+// Copies into pageable host memory through two pinned staging buffers: the DMA of one chunk runs
+// while the previous chunk is copied out on the host (a direct copy to pageable memory is staged by
+// the runtime at a fraction of the link's rate).  The buffers are allocated once per process.
+constexpr uint64_t kStageBytes = 8ULL << 20;
+std::mutex g_stage_mu;
+uint8_t *g_stage[2] = {nullptr, nullptr};
+
+void copy_to_host(uint8_t *dst, const uint8_t *src, uint64_t n, hipStream_t s) {
+    if (!n) return;
+    std::lock_guard<std::mutex> lk(g_stage_mu);
+    for (int i = 0; i < 2; ++i)
+        if (!g_stage[i]) HIP_OK(hipHostMalloc(reinterpret_cast<void **>(&g_stage[i]), kStageBytes, hipHostMallocDefault));
+    hipEvent_t ev[2];
+    HIP_OK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
+    if (hipEventCreateWithFlags(&ev[1], hipEventDisableTiming) != hipSuccess) {
+        (void)hipEventDestroy(ev[0]);
+        throw DeviceError("hipEventCreateWithFlags failed");
+    }
+    auto done = [&] {
+        (void)hipEventDestroy(ev[0]);
+        (void)hipEventDestroy(ev[1]);
+    };
+    try {
+        uint64_t prev_off = 0, prev_n = 0;
+        int k = 0;
+        for (uint64_t off = 0; off < n; off += kStageBytes, k ^= 1) {
+            const uint64_t m = std::min(kStageBytes, n - off);
+            HIP_OK(hipMemcpyAsync(g_stage[k], src + off, m, hipMemcpyDeviceToHost, s));
+            HIP_OK(hipEventRecord(ev[k], s));
+            if (prev_n) {  // the previous chunk, in the other buffer
+                HIP_OK(hipEventSynchronize(ev[k ^ 1]));
+                std::memcpy(dst + prev_off, g_stage[k ^ 1], prev_n);
+            }
+            prev_off = off;
+            prev_n = m;
+        }
+        HIP_OK(hipEventSynchronize(ev[k ^ 1]));
+        std::memcpy(dst + prev_off, g_stage[k ^ 1], prev_n);
+    } catch (...) {
+        (void)hipStreamSynchronize(s);  // no DMA may still target the staging buffers
+        done();
+        throw;
+    }
+    done();
+}
+
 // ------------------------------------------------------------------ workspace
 // Device buffers of one call.  Small buffers are carved from chunks of kArenaChunk bytes so that a
 // call makes few trips through the caller's allocator; large ones are allocated on their own.
@@ -990,9 +1037,14 @@ int32_t crx_encoded_write(const crx_encoded *e, const char *const *names, const 
             std::memcpy(dst, hdr.data(), hdr.size());
             std::memcpy(dst + off_pl, pl.data(), pl.size());
         }
-        if (e->n_blocks) HIP_OK(hipMemcpyAsync(dst + off_bt, e->d_block_bits, 4 * e->n_blocks, from_dev, s));
-        if (e->payload_len) HIP_OK(hipMemcpyAsync(dst + off_pay, e->d_payload, e->payload_len, from_dev, s));
-        if (!dst_on_device) HIP_OK(hipStreamSynchronize(s));
+        if (dst_on_device) {
+            if (e->n_blocks) HIP_OK(hipMemcpyAsync(dst + off_bt, e->d_block_bits, 4 * e->n_blocks, from_dev, s));
+            if (e->payload_len) HIP_OK(hipMemcpyAsync(dst + off_pay, e->d_payload, e->payload_len, from_dev, s));
+        } else {
+            HIP_OK(hipStreamSynchronize(s));  // the encode's work, before the staged copies below
+            copy_to_host(dst + off_bt, reinterpret_cast<const uint8_t *>(e->d_block_bits), 4 * e->n_blocks, s);
+            copy_to_host(dst + off_pay, e->d_payload, e->payload_len, s);
+        }
     });
 }
 
