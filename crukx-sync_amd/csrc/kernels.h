@@ -8,7 +8,6 @@
 namespace crx {
 
 constexpr int kRow = 128;             // elements per wavefront row: 64 lanes x one 32-bit word
-constexpr int kChgCap = 256;          // changes a wavefront buffers in LDS; a flush leaves room for a row
 constexpr int kDense = 32;            // residual symbols below this are counted in a dense table
 constexpr int kLocalGroups = 64;      // groups a statistics workgroup accumulates in LDS
 constexpr uint32_t kScanTiles = 32;   // slabs per chunk of the per-tensor histogram scan

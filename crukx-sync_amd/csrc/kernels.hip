@@ -15,6 +15,7 @@ constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ULL;
 constexpr uint64_t kMix1 = 0xBF58476D1CE4E5B9ULL;
 constexpr uint64_t kMix2 = 0x94D049BB133111EBULL;
 constexpr int kRankRows = 8;    // rows per batch of the encode rank pass (two streams)
+constexpr int kChgCap = 256;    // changes the rank pass buffers in LDS; a flush leaves room for a row
 constexpr uint32_t kRankCopies = 4;  // copies of each exponent count in the encode rank pass (2 or 4)
 static_assert(kRankCopies == 2 || kRankCopies == 4 || kRankCopies == 8, "kRankCopies");
 constexpr int kScanRows = 16;   // rows per batch of the apply histogram pass
