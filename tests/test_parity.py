@@ -112,6 +112,22 @@ def test_slab_size_never_changes_bytes(golden, monkeypatch, slab, name):
         assert torch.equal(w[k].cpu().view(torch.int16), new[k].view(torch.int16))
 
 
+def test_many_exponent_windows_per_slab(monkeypatch):
+    """Slabs whose targets span all 256 exponents take four select windows each; with 128-element
+    slabs there are more extra windows than the select pass's front blocks, so the overflow kernel
+    runs too.  Every element changes to arbitrary bits; the result must equal the oracle's."""
+    monkeypatch.setattr(codec, "_SLAB", 128)
+    g = torch.Generator().manual_seed(31)
+    a = torch.randint(-32768, 32768, (200_000,), generator=g, dtype=torch.int16)
+    b = a ^ torch.randint(1, 32768, (200_000,), generator=g, dtype=torch.int16)
+    old, new = {"w": a}, {"w": b}
+    upd = crukx_sync.encode_update(_cuda(old), _cuda(new))
+    assert upd == oracle.encode_update(old, new)
+    w = _cuda({"w": a.clone()})
+    assert crukx_sync.apply_update(w, upd).changed == 200_000
+    assert torch.equal(w["w"].cpu(), b)
+
+
 def test_device_resident_bytes_and_apply(golden):
     old, new = _scen()["three_tensors"]
     dev_upd = crukx_sync.encode_update_device(_cuda(old), _cuda(new))
