@@ -1244,9 +1244,9 @@ __global__ __launch_bounds__(64) void k_locate(SelectArgs a) {
 // spare counter no other lane uses.  Lane e owns window exponent e: it sums that exponent's copies
 // and compares the total with the exponent's next target, so one ballot names the exponents with
 // targets in the row.  For each of them, ballots and mbcnt give every element of that exponent its
-// stable in-row rank, and the lane holding the element whose rank matches the target records it.  A row with more
-// targets of one exponent publishes that exponent's elements in LDS by rank and takes the rest of
-// its targets one per lane.
+// stable in-row rank, and the lane holding the element whose rank matches the target records it.
+// A row with more targets of one exponent publishes that exponent's elements in LDS by rank and
+// takes the rest one per lane.
 //
 // The pass is bound by instruction issue and LDS latency: per-row instructions and the LDS footprint
 // (occupancy) set its speed.  The per-row path is six packed-16-bit and address operations, two LDS
@@ -1283,7 +1283,7 @@ struct SelectLds {
 };
 
 template <bool LDS_LIST>
-__device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase, SelectLds &S,
+__device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase, SelectLds &S,
                             uint32_t nxt, uint32_t nix, const uint32_t end, const uint32_t jofs, const uint32_t pre_k) {
     // lane e, for window exponent e: nxt = slab rank of its next target (kFar: none left), nix = that
     // target's list index, end = end of its list, jofs = change index - list index, pre_k = its count
@@ -1339,7 +1339,8 @@ __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Sla
                 ++i;
                 tc = i < ke ? target(i, jo, pr) : (uint32_t)kFar;
             }
-            if (tc < after) {  // more targets of exponent k in this row
+            if (tc < after) {  // more targets of exponent k in this row (taking them one at a time
+                               // measured slower than this lane-parallel path, from the second on)
                 // publish by in-row rank; other lanes write a slot of their own past the ranks
                 S.slot[m0 ? rr0 : kRow + ln] = w0;
                 S.slot[m1 ? rr1 : kRow + ln] = w1;
@@ -1372,7 +1373,7 @@ __device__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Sla
 // One window of one slab: exponents [kfirst, kfirst + kWin), or from the slab's lowest exponent with
 // targets when kfirst is 256.  The slab's targets are the group changes [lb(slab), lb(next slab)) of
 // each exponent (to the group's end for a tensor's last slab).
-__device__ void select_window(const SelectArgs &a, uint32_t tau, uint32_t kfirst, SelectLds &S) {
+__device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau, uint32_t kfirst, SelectLds &S) {
     const uint32_t ln = lane();
     const uint32_t t = a.tile_tensor[tau];
     const TensorDesc td = a.descs[t];
