@@ -16,7 +16,7 @@ constexpr uint64_t kMix1 = 0xBF58476D1CE4E5B9ULL;
 constexpr uint64_t kMix2 = 0x94D049BB133111EBULL;
 constexpr int kRankRows = 8;    // rows per batch of the encode rank pass (two streams)
 constexpr int kChgCap = 256;    // changes the rank pass buffers in LDS; a flush leaves room for a row
-constexpr uint32_t kRankCopies = 4;  // copies of each exponent count in the encode rank pass (2 or 4)
+constexpr uint32_t kRankCopies = 4;  // copies of each exponent count in the rank pass (2, 4 or 8; 4 measured best)
 static_assert(kRankCopies == 2 || kRankCopies == 4 || kRankCopies == 8, "kRankCopies");
 constexpr int kScanRows = 16;   // rows per batch of the apply histogram pass
 constexpr int kSelectRows = 12; // ... of the select pass (fewer registers: occupancy)
@@ -960,7 +960,10 @@ __global__ __launch_bounds__(256) void k_checksum(const uint32_t *frame, uint32_
 // host-order 64-bit words, and so are the decoding symbols when they fit.  A change normally costs
 // one 64-bit window of the stream (unary run, remainder and Huffman peek together) and one LDS read
 // of its symbol; code lengths come from comparisons of the 17-bit peek with the canonical limits
-// held in registers.  Each lane writes its block's outputs in order, so the lines fill in L2.
+// held in registers.  The decoder does not read the receiver's weights or counts (positions are
+// checked against those by k_local_fix), so it can run beside the exponent-count pass.  Each lane
+// keeps kDecBuf decoded changes in registers and stores them together: storing one change at a time
+// left each lane's output lines half-written in L2, and they reached HBM several times over.
 constexpr uint32_t kDecPayWords = 3584;  // 28 KiB of payload per wavefront; more is read from HBM
 constexpr uint32_t kDecBuf = 8;          // changes decoded per lane between stores
 
