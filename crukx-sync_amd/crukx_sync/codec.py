@@ -278,9 +278,9 @@ def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
 # ---------------------------------------------------------------- apply
 
 # Receiver-side exponent counts per slab, kept on the device across updates of the same tensors:
-# id(tensor) -> (weakref, _version after our last write, device buffer).  They are used only with a
-# checksum-cache hit for the tensor (the same trust rule), and let apply skip its full read of
-# those weights (crx_apply_cached).
+# id(tensor) -> (weakref, _version after our last write, device buffer, slab size).  They are used
+# only with the same slab size and a checksum-cache hit for the tensor (the same trust rule), and
+# let apply skip its full read of those weights (crx_apply_cached).
 _hist = {}
 
 
@@ -291,11 +291,11 @@ def _hist_lookup(t):
     return e
 
 
-def _hist_store(t, buf):
+def _hist_store(t, buf, slab):
     key = id(t)
     e = _hist.get(key)
     ref = e[0] if e is not None and e[0]() is t else weakref.ref(t, lambda _r, key=key: _hist.pop(key, None))
-    _hist[key] = (ref, t._version, buf)
+    _hist[key] = (ref, t._version, buf, slab)
 
 
 def _cache_get(checksums, name, t):
@@ -342,16 +342,17 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     changed = ctypes.c_uint64()
     # exponent counts carried across updates: only for tensors updated in place with a trusted cache
     keep = checksums is not None and staged is targets
+    slab = int(_SLAB)
     hist_in, hist_out, bufs = [], [], []
     if keep:
         fresh = []  # tensors without usable counts: one allocation, sliced per tensor
         for i, (a, c) in enumerate(zip(targets, cache)):
             e = _hist_lookup(a)
-            if c is not None and e is not None and e[1] == a._version and e[2].device == dev:
+            if c is not None and e is not None and e[1] == a._version and e[2].device == dev and e[3] == slab:
                 bufs.append(e[2])
             else:
                 bufs.append(None)
-                fresh.append((i, L.crx_apply_hist_words(a.numel(), int(_SLAB))))
+                fresh.append((i, L.crx_apply_hist_words(a.numel(), slab)))
         if fresh:
             block = torch.empty(sum(w for _, w in fresh), dtype=torch.int32, device=dev)
             at = 0
@@ -368,7 +369,7 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
                                 _native.u64_array(vals),
                                 _native.ptr_array(hist_in) if keep else None,
                                 _native.ptr_array(hist_out) if keep else None,
-                                int(_SLAB), _native.stream_of(dev), ws.fn, None, ctypes.byref(changed), err, 512)
+                                slab, _native.stream_of(dev), ws.fn, None, ctypes.byref(changed), err, 512)
     ws.check()
     ws.release()
     if rc != _native.OK:
@@ -381,7 +382,7 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
         for a, s in zip(targets, staged):
             a.copy_(s)  # an in-place op: bumps the tensor's version
     for a, buf in zip(targets, bufs):
-        _hist_store(a, buf)
+        _hist_store(a, buf, slab)
     if checksums is not None:  # record the version after our own write
         checksums.update({name: (c, t._version) for name, c, t in zip(names, header_chk, targets)})
     return changed.value

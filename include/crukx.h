@@ -101,7 +101,9 @@ int32_t crx_apply(const crx_update *u, const uint8_t *payload_dev, uint16_t *con
  * only when an element crosses a power of two, so the histogram pass (a full read of the weights)
  * is skipped for tensors whose counts are known.  hist_in[i] (device, crx_apply_hist_words(numel,
  * slab) u32, or NULL) holds tensor i's counts, valid only while its weights are unchanged since they
- * were recorded and only with a trusted cached checksum (has_cache[i]); hist_out[i] (or NULL)
+ * were recorded, only for the same slab size and only with a trusted cached checksum (has_cache[i]);
+ * the library cannot check its size, so counts recorded with another slab size read out of bounds;
+ * hist_out[i] (or NULL)
  * receives the counts after this update (it may equal hist_in[i]).  On any status but CRX_OK the
  * weights are untouched but hist_out may hold partial results: discard them.  No counterpart in
  * the reference (its analogue is the checksum cache, codec.py:457-460,713-716). */

@@ -253,6 +253,29 @@ def test_receiver_exponent_counts_carried_across_updates():
         codec._SLAB = old_slab
 
 
+def test_exponent_counts_are_not_reused_across_slab_sizes(monkeypatch):
+    """Counts recorded with one slab size are recomputed, not reused, when the slab size changes
+    between updates of the same receiver tensors (their layout differs)."""
+    g = torch.Generator().manual_seed(9)
+    cur = {"a": (torch.randn(200_003, generator=g) * 0.02).to(torch.bfloat16),
+           "b": (torch.randn(96, 1024, generator=g) * 0.02).to(torch.bfloat16)}
+    recv = _cuda(cur)
+    send_chk, recv_chk = {}, {}
+    for step, slab in enumerate((1 << 16, 4096, 1 << 14, 1 << 16, 4096)):
+        monkeypatch.setattr(codec, "_SLAB", slab)
+        nxt = {}
+        for n, t in cur.items():
+            bits = t.view(torch.int16).clone()
+            m = torch.rand(bits.shape, generator=g) < 0.03
+            bits[m] = bits[m] + torch.randint(1, 200, bits.shape, generator=g, dtype=torch.int16)[m]
+            nxt[n] = bits.view(torch.bfloat16)
+        crukx_sync.apply_update(recv, crukx_sync.encode_update(_cuda(cur), _cuda(nxt), send_chk), recv_chk)
+        for n in nxt:
+            assert torch.equal(recv[n].cpu().view(torch.int16), nxt[n].view(torch.int16)), (step, n)
+            assert codec._hist_lookup(recv[n])[3] == slab
+        cur = nxt
+
+
 def test_verdict_messages_follow_the_reference():
     """apply's error messages and their priority are the reference's (codec.py:598-604,706-712):
     the group-size check of tensors over 2^24 elements first, then checksum mismatches naming up to
