@@ -755,7 +755,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, pv, bad, more, n_more,
                   std::min(1024u, 3 * tiles)};
     launch_locate(sa, tiles, s);
-    launch_select(sa, tiles, s);
+    launch_select(sa, tiles, C > kSelectDenseTargets * tiles, s);
     launch_verify(ba, B, s);
     launch_range_sums(bdelta, tblk, T, tdelta, s);
     hc.mark("apply_launch");

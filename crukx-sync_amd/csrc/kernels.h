@@ -195,7 +195,9 @@ void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
 void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s);
 // tile_tensor[tile] = tensor of every slab of the layout
 void launch_tile_map(const TensorDesc *descs, uint32_t n_tensors, uint32_t *tile_tensor, hipStream_t s);
-void launch_select(const SelectArgs &a, uint32_t tiles, hipStream_t s);
+// dense: the larger LDS target list (for updates averaging over kSelectDenseTargets changes per slab)
+constexpr uint64_t kSelectDenseTargets = 800;
+void launch_select(const SelectArgs &a, uint32_t tiles, bool dense, hipStream_t s);
 void launch_verify(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
 void launch_scatter(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
 void launch_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial, uint32_t n_parts,

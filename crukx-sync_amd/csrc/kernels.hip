@@ -1247,19 +1247,22 @@ __global__ __launch_bounds__(64) void k_locate(SelectArgs a) {
 // spare counter no other lane uses.  Lane e owns window exponent e: it sums that exponent's copies
 // and compares the total with the exponent's next target, so one ballot names the exponents with
 // targets in the row.  For each of them, ballots and mbcnt give every element of that exponent its
-// stable in-row rank, and the lane holding the element whose rank matches the target records it.
-// A row with more targets of one exponent publishes that exponent's elements in LDS by rank and
-// takes the rest one per lane.
+// stable in-row rank, and the lane holding the element whose rank matches the target records it;
+// then the lanes of all those exponents read their next targets together.  A row with more targets
+// of one exponent publishes that exponent's elements in LDS by rank and takes the rest one per lane.
 //
-// The pass is bound by instruction issue and LDS latency: per-row instructions and the LDS footprint
-// (occupancy) set its speed.  The per-row path is six packed-16-bit and address operations, two LDS
-// atomics, one LDS read and one compare.
-constexpr uint32_t kTgtCap = 1024;            // targets per window held in LDS; more are read from HBM
+// The pass is bound by instruction issue: about 15 vector instructions per target and 10 per row
+// (six packed-16-bit and address operations, two LDS atomics, one LDS read and one compare), with
+// the LDS footprint setting occupancy.
+// targets per window held in LDS (a multiple of 1024; more are read from HBM): the smaller list keeps
+// the footprint small (occupancy) for sparse updates, the larger one serves denser updates
+constexpr uint32_t kTgtCapSparse = 1024, kTgtCapDense = 2048;
 constexpr uint32_t kWin = kSelWin;           // exponents per window: one per lane
 constexpr uint32_t kSelCopies = 4;            // copies of each running count (4 or 8)
 constexpr uint32_t kSpare = 64 / kSelCopies;  // spare counters: lane l uses copy l % kSelCopies of spare l / kSelCopies
 constexpr uint32_t kCntShift = kSelCopies == 4 ? 3 : 2;  // (window index << 7) >> kCntShift = counter byte offset
 static_assert(kSelCopies == 4 || kSelCopies == 8, "kSelCopies");
+static_assert(kTgtCapSparse % 1024 == 0 && kTgtCapDense % 1024 == 0, "target list capacity");
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u16x2 as16(uint32_t v) { return __builtin_bit_cast(u16x2, v); }
@@ -1275,9 +1278,10 @@ __device__ __forceinline__ uint32_t sel_count(const uint32_t *cnt, uint32_t c) {
     return s;
 }
 
+template <uint32_t CAP>
 struct SelectLds {
     uint32_t cnt[(kWin + kSpare) * kSelCopies];  // running counts, kSelCopies copies (by lane)
-    alignas(16) uint16_t list[kTgtCap];            // slab ranks of the window's targets, per exponent in order
+    alignas(16) uint16_t list[CAP];                // slab ranks of the window's targets, per exponent in order
     union {
         uint32_t slot[2 * kRow];  // streaming: in-row rank -> (in-row offset << 16) | bits; [kRow, 2 kRow): per lane
         uint4 info[kWin];         // set-up, per window exponent: {list begin, list end, change index - list
@@ -1285,20 +1289,24 @@ struct SelectLds {
     };
 };
 
-template <bool LDS_LIST>
-__device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase, SelectLds &S,
-                            uint32_t nxt, uint32_t nix, const uint32_t end, const uint32_t jofs, const uint32_t pre_k) {
-    // lane e, for window exponent e: nxt = slab rank of its next target (kFar: none left), nix = that
-    // target's list index, end = end of its list, jofs = change index - list index, pre_k = its count
-    // before the slab (HBM list only)
+template <uint32_t CAP, bool LDS_LIST>
+__device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase, SelectLds<CAP> &S,
+                            uint32_t nxt, uint32_t ci, const uint32_t cend, const uint32_t jofs, const uint32_t pre_k) {
+    // lane e, for window exponent e: nxt = slab rank of its next target (kFar: none left), ci = that
+    // target's change index, cend = the end of its changes, jofs = change index - list index (LDS
+    // list), pre_k = its count before the slab (HBM list)
     const uint32_t ln = lane(), rep4 = (ln & (kSelCopies - 1)) * 4u;
     const uint32_t kb = (kbase << 7) * 0x10001u, sp = ((kWin + ln / kSelCopies) << 7) * 0x10001u;
     char *const cnt = reinterpret_cast<char *>(S.cnt);
-    // slab rank of list entry i of the exponent whose offsets are (jo, pr); i below the list's end
-    auto target = [&](uint32_t i, uint32_t jo, uint32_t pr) -> uint32_t {
-        if (LDS_LIST) return S.list[min(i, kTgtCap - 1)];
-        return a.local[jo + i] - pr;
+    // slab rank of the target with change index c (below its exponent's end)
+    auto target = [&](uint32_t c, uint32_t jo, uint32_t pr) -> uint32_t {
+        if (LDS_LIST) return S.list[min(c - jo, CAP - 1)];
+        return a.local[c] - pr;
     };
+    auto put = [&](uint32_t c, uint32_t r, uint32_t w) {  // w = (in-row offset << 16) | bits
+        a.pv[c] = (unsigned long long)(sl.base + r * kRow + (w >> 16)) | ((unsigned long long)(w & 0xFFFFu) << 32);
+    };
+    uint32_t prev = 0;  // exponent ln's count before the row
     const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
     stream_rows<kSelectRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
         // window index << 7 of both elements (16-bit halves); outside the window or the slab: the spare
@@ -1312,63 +1320,69 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
         atomicAdd(reinterpret_cast<uint32_t *>(cnt + ((uint32_t)ad.x | rep4)), 1u);
         atomicAdd(reinterpret_cast<uint32_t *>(cnt + ((uint32_t)ad.y | rep4)), 1u);
         const uint32_t s = sel_count(S.cnt, ln);  // exponent ln's count up to the row's end
+        const uint32_t seen = prev;
+        prev = s;
         uint64_t H = ballot(s > nxt);
         if (!H) return;
         wave_fence();
         const uint32_t c0 = c.x, c1 = c.y;
-        do {  // once per exponent with targets in this row
+        // this lane's elements as published: (in-row offset << 16) | bits
+        const uint32_t w0 = ((2 * ln) << 16) | (o & 0xFFFFu), w1 = ((2 * ln + 1) << 16) | (o >> 16);
+        const uint32_t q = nxt - seen;  // in-row rank of the next target, for the exponents in H
+        const bool hit = s > nxt;       // this lane's exponent is in H
+        do {  // the next target of each exponent with targets in this row
             const uint32_t k = (uint32_t)__builtin_ctzll(H);
-            const uint32_t after = rdlane(s, k), ke = rdlane(end, k), jo = rdlane(jofs, k);
-            const uint32_t pr = LDS_LIST ? 0u : rdlane(pre_k, k);
-            uint32_t tc = rdlane(nxt, k), i = rdlane(nix, k);
+            const uint32_t qk = rdlane(q, k), ck = rdlane(ci, k);
             const bool m0 = c0 == (k << 7), m1 = c1 == (k << 7);
             const uint64_t M0 = ballot(m0), M1 = ballot(m1);
-            const uint32_t seen = after - (uint32_t)(__popcll(M0) + __popcll(M1));  // ... before this row
             // in-row rank of this lane's first element among exponent k's (the second's is one more
             // when the first is one of them)
             const uint32_t rr0 = __builtin_amdgcn_mbcnt_hi((uint32_t)(M1 >> 32),
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)M1, mbcnt(M0)));
             const uint32_t rr1 = rr0 + (m0 ? 1u : 0u);
-            // this lane's elements as published: (in-row offset << 16) | bits
-            const uint32_t w0 = ((2 * ln) << 16) | (o & 0xFFFFu), w1 = ((2 * ln + 1) << 16) | (o >> 16);
-            {  // the first target: the element of in-row rank tc - seen writes itself
-                const uint32_t q = tc - seen;
-                const bool t0 = m0 && rr0 == q, t1 = m1 && rr1 == q;  // one element of the row
-                if (t0 || t1) {
-                    const uint32_t w = t1 ? w1 : w0;
-                    a.pv[jo + i] = (unsigned long long)(sl.base + r * kRow + (w >> 16)) |
-                                   ((unsigned long long)(w & 0xFFFFu) << 32);
-                }
-                ++i;
-                tc = i < ke ? target(i, jo, pr) : (uint32_t)kFar;
-            }
-            if (tc < after) {  // more targets of exponent k in this row (taking them one at a time
-                               // measured slower than this lane-parallel path, from the second on)
-                // publish by in-row rank; other lanes write a slot of their own past the ranks
-                S.slot[m0 ? rr0 : kRow + ln] = w0;
-                S.slot[m1 ? rr1 : kRow + ln] = w1;
-                wave_fence();
-                uint32_t n, tl;
-                do {  // one target per lane (64 more if all lanes take one)
-                    const uint32_t j = i + ln;
-                    tl = j < ke ? target(j, jo, pr) : (uint32_t)kFar;
-                    const bool take = tl < after;
-                    n = (uint32_t)__popcll(ballot(take));
-                    if (take) {
-                        const uint32_t w = S.slot[tl - seen];
-                        a.pv[jo + j] = (unsigned long long)(sl.base + r * kRow + (w >> 16)) |
-                                       ((unsigned long long)(w & 0xFFFFu) << 32);
-                    }
-                    i += n;
-                } while (n == 64);
-                tc = rdlane(tl, n);  // the first target not taken, or kFar
-                wave_fence();
-            }
+            const bool t0 = m0 && rr0 == qk, t1 = m1 && rr1 == qk;  // one element of the row
+            if (t0 || t1) put(ck, r, t1 ? w1 : w0);
+            H &= H - 1;
+        } while (H);
+        if (hit) {  // every exponent that had one: its next target, lane-parallel
+            ++ci;
+            nxt = ci < cend ? target(ci, jofs, pre_k) : (uint32_t)kFar;
+        }
+        H = ballot(s > nxt);
+        if (!H) return;
+        // more targets of an exponent in this row (rare at low densities): publish its elements by
+        // in-row rank (other lanes write a slot of their own past the ranks) and take the rest one per
+        // lane
+        wave_fence();
+        do {
+            const uint32_t k = (uint32_t)__builtin_ctzll(H);
+            const uint32_t after = rdlane(s, k), seen_k = rdlane(seen, k), ke = rdlane(cend, k);
+            const uint32_t jo = LDS_LIST ? rdlane(jofs, k) : 0u, pr = LDS_LIST ? 0u : rdlane(pre_k, k);
+            uint32_t ck = rdlane(ci, k);
+            const bool m0 = c0 == (k << 7), m1 = c1 == (k << 7);
+            const uint64_t M0 = ballot(m0), M1 = ballot(m1);
+            const uint32_t rr0 = __builtin_amdgcn_mbcnt_hi((uint32_t)(M1 >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)M1, mbcnt(M0)));
+            const uint32_t rr1 = rr0 + (m0 ? 1u : 0u);
+            S.slot[m0 ? rr0 : kRow + ln] = w0;
+            S.slot[m1 ? rr1 : kRow + ln] = w1;
+            wave_fence();
+            uint32_t n, tl;
+            do {  // one target per lane (64 more if all lanes take one)
+                const uint32_t j = ck + ln;
+                tl = j < ke ? target(j, jo, pr) : (uint32_t)kFar;
+                const bool take = tl < after;
+                n = (uint32_t)__popcll(ballot(take));
+                if (take) put(j, r, S.slot[tl - seen_k]);
+                ck += n;
+            } while (n == 64);
+            const uint32_t tc = rdlane(tl, n);  // the first target not taken, or kFar
+            wave_fence();
             if (ln == k) {
                 nxt = tc;
-                nix = i;
+                ci = ck;
             }
-            H &= ~(1ULL << k);
+            H &= H - 1;
         } while (H);
     });
 }
@@ -1376,7 +1390,8 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
 // One window of one slab: exponents [kfirst, kfirst + kWin), or from the slab's lowest exponent with
 // targets when kfirst is 256.  The slab's targets are the group changes [lb(slab), lb(next slab)) of
 // each exponent (to the group's end for a tensor's last slab).
-__device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau, uint32_t kfirst, SelectLds &S) {
+template <uint32_t CAP>
+__device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau, uint32_t kfirst, SelectLds<CAP> &S) {
     const uint32_t ln = lane();
     const uint32_t t = a.tile_tensor[tau];
     const TensorDesc td = a.descs[t];
@@ -1423,7 +1438,7 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
             if (ln >= (uint32_t)o) incl += v;
         }
         const uint32_t total = __shfl(incl, 63, 64);
-        const bool in_lds = total <= kTgtCap;
+        const bool in_lds = total <= CAP;
         S.info[ln] = make_uint4(0u, 0u, 0u, 0u);  // window exponents past 255
         wave_fence();
         uint32_t start[4], off = incl - mine;
@@ -1437,44 +1452,51 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
         wave_fence();
         if (in_lds) {
             // list entry x belongs to the last exponent whose list starts at or before x: mark the starts
-            // of the non-empty lists, then a running maximum over the entries (16 per lane, in order)
-            uint16_t *mark = S.list;  // read into registers before the list overwrites it
-            for (uint32_t x = ln; x < kTgtCap; x += 64) mark[x] = 0;
+            // of the non-empty lists, then a running maximum over the entries, 1024 at a time (16 per
+            // lane, in order)
+            uint16_t *mark = S.list;  // each round reads its marks before its list entries overwrite them
+            for (uint32_t x = ln; x < CAP; x += 64) mark[x] = 0;
             wave_fence();
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 if (nw[q]) mark[start[q]] = (uint16_t)(4 * ln + q - kbase + 1);
             wave_fence();
-            uint32_t v[16], run = 0;
+            uint32_t carry = 0;  // the maximum over earlier rounds
+            for (uint32_t x0 = 0; x0 < total; x0 += 1024) {
+                uint32_t v[16], run = 0;
 #pragma unroll
-            for (int i = 0; i < 16; i += 8) {
-                const uint4 m = *reinterpret_cast<const uint4 *>(&mark[16 * ln + i]);
-                const uint32_t w4[4] = {m.x, m.y, m.z, m.w};
+                for (int i = 0; i < 16; i += 8) {
+                    const uint4 m = *reinterpret_cast<const uint4 *>(&mark[x0 + 16 * ln + i]);
+                    const uint32_t w4[4] = {m.x, m.y, m.z, m.w};
 #pragma unroll
-                for (int h = 0; h < 4; ++h) {
-                    v[i + 2 * h] = run = max(run, w4[h] & 0xFFFF);
-                    v[i + 2 * h + 1] = run = max(run, w4[h] >> 16);
+                    for (int h = 0; h < 4; ++h) {
+                        v[i + 2 * h] = run = max(run, w4[h] & 0xFFFF);
+                        v[i + 2 * h + 1] = run = max(run, w4[h] >> 16);
+                    }
                 }
-            }
-            uint32_t before = run;  // inclusive max-scan of the lane maxima, then shifted by one lane
-            for (int o = 1; o < 64; o <<= 1) {
-                const uint32_t w = __shfl_up(before, o, 64);
-                if (ln >= (uint32_t)o) before = max(before, w);
-            }
-            before = __shfl_up(before, 1, 64);
-            if (ln == 0) before = 0;
-            uint32_t idx[16], sub[16];
+                uint32_t incl = run;  // inclusive max-scan of the lane maxima
+                for (int o = 1; o < 64; o <<= 1) {
+                    const uint32_t w = __shfl_up(incl, o, 64);
+                    if (ln >= (uint32_t)o) incl = max(incl, w);
+                }
+                uint32_t before = __shfl_up(incl, 1, 64);
+                before = max(ln == 0 ? 0u : before, carry);
+                carry = max(carry, (uint32_t)__shfl(incl, 63, 64));
+                uint32_t idx[16], sub[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const uint32_t c = max(before, v[i]);
-                const uint4 inf = S.info[c ? c - 1 : 0];
-                idx[i] = inf.z + 16 * ln + i;
-                sub[i] = inf.w;
-            }
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t c = max(before, v[i]);
+                    const uint4 inf = S.info[c ? c - 1 : 0];
+                    idx[i] = inf.z + x0 + 16 * ln + i;
+                    sub[i] = inf.w;
+                }
+                wave_fence();
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const uint32_t x = 16 * ln + i;
-                if (x < total) S.list[x] = (uint16_t)(a.local[idx[i]] - sub[i]);
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t x = x0 + 16 * ln + i;
+                    if (x < total) S.list[x] = (uint16_t)(a.local[idx[i]] - sub[i]);
+                }
+                wave_fence();
             }
         }
         wave_fence();
@@ -1484,15 +1506,17 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
         wave_fence();
         for (uint32_t i = ln; i < (kWin + kSpare) * kSelCopies; i += 64) S.cnt[i] = 0;
         wave_fence();
-        if (in_lds) select_slab<true>(a, td, sl, kbase, S, first, inf.x, inf.y, inf.z, inf.w);
-        else select_slab<false>(a, td, sl, kbase, S, first, inf.x, inf.y, inf.z, inf.w);
+        const uint32_t c_first = inf.x + inf.z, c_end = inf.y + inf.z;  // change indices
+        if (in_lds) select_slab<CAP, true>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w);
+        else select_slab<CAP, false>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w);
     }
 }
 
 // Blocks [0, n_front): the first n_front windows k_locate listed (started first, so they overlap
 // the rest); then one block per slab for its first window.
+template <uint32_t CAP>
 __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
-    __shared__ __attribute__((aligned(16))) SelectLds S;
+    __shared__ __attribute__((aligned(16))) SelectLds<CAP> S;
     if (*a.bad) return;
     const uint32_t b = blockIdx.x;
     if (b < a.n_front) {
@@ -1505,8 +1529,9 @@ __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
 }
 
 // Listed windows past the first n_front (normally none); a fixed grid walks them.
+template <uint32_t CAP>
 __global__ __launch_bounds__(64) void k_select_more(SelectArgs a) {
-    __shared__ __attribute__((aligned(16))) SelectLds S;
+    __shared__ __attribute__((aligned(16))) SelectLds<CAP> S;
     if (*a.bad) return;
     const uint32_t n = *a.n_more;
     for (uint32_t i = a.n_front + blockIdx.x; i < n; i += gridDim.x) {
@@ -1696,9 +1721,14 @@ void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
 
 void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("locate", k_locate, tiles, 64, s, a); }
 
-void launch_select(const SelectArgs &a, uint32_t tiles, hipStream_t s) {
-    CRX_LAUNCH("select", k_select, a.n_front + tiles, 64, s, a);
-    CRX_LAUNCH("select_more", k_select_more, 256, 64, s, a);
+void launch_select(const SelectArgs &a, uint32_t tiles, bool dense, hipStream_t s) {
+    if (dense) {
+        CRX_LAUNCH("select", k_select<kTgtCapDense>, a.n_front + tiles, 64, s, a);
+        CRX_LAUNCH("select_more", k_select_more<kTgtCapDense>, 256, 64, s, a);
+    } else {
+        CRX_LAUNCH("select", k_select<kTgtCapSparse>, a.n_front + tiles, 64, s, a);
+        CRX_LAUNCH("select_more", k_select_more<kTgtCapSparse>, 256, 64, s, a);
+    }
 }
 
 void launch_verify(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {

@@ -253,6 +253,29 @@ def test_receiver_exponent_counts_carried_across_updates():
         codec._SLAB = old_slab
 
 
+@pytest.mark.parametrize("rho", [0.005, 0.02, 0.025, 0.1, 0.6, "mixed"])
+def test_change_densities_across_target_list_sizes(rho):
+    """Slabs with a few hundred to tens of thousands of changes (the select pass keeps up to a fixed
+    number of a window's targets in LDS, more for denser updates, and reads larger lists from HBM):
+    exact round trips and the oracle's bytes.  "mixed": one dense slab in a sparse update."""
+    g = torch.Generator().manual_seed(7 if rho == "mixed" else int(rho * 1000))
+    n = 400_003 if rho == "mixed" else 200_003
+    a = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    bits = a.view(torch.int16).clone()
+    if rho == "mixed":
+        m = torch.rand(bits.shape, generator=g) < 0.002
+        m[70_000:70_000 + 65_536] |= torch.rand(65_536, generator=g) < 0.06
+    else:
+        m = torch.rand(bits.shape, generator=g) < rho
+    bits[m] = bits[m] + torch.randint(-3, 4, bits.shape, generator=g, dtype=torch.int16)[m]
+    b = bits.view(torch.bfloat16)
+    upd = crukx_sync.encode_update({"w": a.cuda()}, {"w": b.cuda()})
+    assert upd == oracle.encode_update({"w": a}, {"w": b})
+    got = {"w": a.cuda()}
+    crukx_sync.apply_update(got, upd)
+    assert torch.equal(got["w"].cpu().view(torch.int16), b.view(torch.int16))
+
+
 def test_exponent_counts_are_not_reused_across_slab_sizes(monkeypatch):
     """Counts recorded with one slab size are recomputed, not reused, when the slab size changes
     between updates of the same receiver tensors (their layout differs)."""
