@@ -135,7 +135,7 @@ struct SelectArgs {
     const int32_t *group_of;        // [tensor][256] group index or -1
     const GroupDev *groups;
     const uint32_t *local;          // group-local index of every change
-    unsigned long long *pv;         // [changes] element index | bits << 32 (old, then new bits)
+    unsigned long long *pv;         // [changes] (in-row offset << 16 | old bits) | row's element index << 32; kNone: unplaced
     const unsigned int *bad;
     uint2 *more;                    // [3 tiles] (slab, first exponent) of windows after a slab's first
     unsigned int *n_more;           // their number (zero before k_locate)
@@ -151,7 +151,7 @@ struct BlockArgs {                  // per-block kernels over the change list (o
     const unsigned long long *blk_prefix;
     uint32_t *local;                // [changes] group-local index (written by k_local_fix)
     const unsigned long long *dz;   // [changes] decoder output: zz | (block-relative local << 32)
-    unsigned long long *pv;         // [changes] element index | bits << 32
+    unsigned long long *pv;         // [changes] the select pass's output, then element index | new bits << 32 (k_verify)
     unsigned long long *bdelta;     // [blocks] checksum delta of each block's changes
     unsigned int *bad;
     uint64_t n_blocks;

@@ -1267,6 +1267,14 @@ static_assert(kTgtCapSparse % 1024 == 0 && kTgtCapDense % 1024 == 0, "target lis
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u16x2 as16(uint32_t v) { return __builtin_bit_cast(u16x2, v); }
 
+// v + this lane's bit of m, in one instruction (the mask as carry-in)
+__device__ __forceinline__ uint32_t add_bit(uint32_t v, uint64_t m) {
+    uint32_t r;
+    uint64_t carry;
+    asm("v_addc_co_u32_e64 %0, %1, 0, %2, %3" : "=v"(r), "=s"(carry) : "v"(v), "s"(m));
+    return r;
+}
+
 // sum of the copies of count c
 __device__ __forceinline__ uint32_t sel_count(const uint32_t *cnt, uint32_t c) {
     uint32_t s = 0;
@@ -1304,7 +1312,7 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
         return a.local[c] - pr;
     };
     auto put = [&](uint32_t c, uint32_t r, uint32_t w) {  // w = (in-row offset << 16) | bits
-        a.pv[c] = (unsigned long long)(sl.base + r * kRow + (w >> 16)) | ((unsigned long long)(w & 0xFFFFu) << 32);
+        a.pv[c] = (unsigned long long)w | ((unsigned long long)(sl.base + r * kRow) << 32);
     };
     uint32_t prev = 0;  // exponent ln's count before the row
     const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
@@ -1339,7 +1347,7 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
             // when the first is one of them)
             const uint32_t rr0 = __builtin_amdgcn_mbcnt_hi((uint32_t)(M1 >> 32),
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)M1, mbcnt(M0)));
-            const uint32_t rr1 = rr0 + (m0 ? 1u : 0u);
+            const uint32_t rr1 = add_bit(rr0, M0);
             const bool t0 = m0 && rr0 == qk, t1 = m1 && rr1 == qk;  // one element of the row
             if (t0 || t1) put(ck, r, t1 ? w1 : w0);
             H &= H - 1;
@@ -1363,7 +1371,7 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
             const uint64_t M0 = ballot(m0), M1 = ballot(m1);
             const uint32_t rr0 = __builtin_amdgcn_mbcnt_hi((uint32_t)(M1 >> 32),
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)M1, mbcnt(M0)));
-            const uint32_t rr1 = rr0 + (m0 ? 1u : 0u);
+            const uint32_t rr1 = add_bit(rr0, M0);
             S.slot[m0 ? rr0 : kRow + ln] = w0;
             S.slot[m1 ? rr1 : kRow + ln] = w1;
             wave_fence();
@@ -1566,13 +1574,14 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
 #pragma unroll
     for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
         unsigned long long d = 0;
-        const uint32_t p = (uint32_t)pv[u];
+        const uint32_t lo = (uint32_t)pv[u];  // (in-row offset << 16) | old bits; row start << 32
+        const uint32_t p = (uint32_t)(pv[u] >> 32) + (lo >> 16);
         if (s < r[u].cnt) {
-            if (p == kNone) {
+            if (lo == kNone) {
                 atomicOr(a.bad, kBadUnplaced);
             } else {
                 const int32_t delta = (int32_t)(zz[u] >> 1) ^ -(int32_t)(zz[u] & 1);
-                const uint32_t old = (uint32_t)(pv[u] >> 32);
+                const uint32_t old = lo & 0xFFFFu;
                 const uint32_t nu = (uint32_t)((int32_t)old + delta) & 0xFFFF;
                 d = (uint64_t)((int64_t)nu - (int64_t)old) * weight(p);
                 a.pv[r[u].eb + s] = p | ((unsigned long long)nu << 32);
