@@ -123,23 +123,28 @@ class Workspace:
 
     def __init__(self, device: torch.device):
         self.device = device
-        self.tensors: list[torch.Tensor] = []
-        self.error: BaseException | None = None
+        # the callback holds these, not the workspace: no reference cycle, so the buffers are freed as
+        # soon as the workspace is dropped rather than at the next garbage collection
+        tensors: list[torch.Tensor] = []
+        errors: list[BaseException] = []
+        self.tensors = tensors
+        self._errors = errors
 
         def _alloc(_ctx, nbytes):
             try:
-                t = torch.empty(int(nbytes), dtype=torch.uint8, device=self.device)
+                t = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
             except BaseException as e:  # noqa: BLE001  (re-raised after the native call returns)
-                self.error = e
+                errors.append(e)
                 return None
-            self.tensors.append(t)
+            tensors.append(t)
             return t.data_ptr()
 
         self.fn = ALLOC_FN(_alloc)
 
     def check(self):
-        if self.error is not None:
-            e, self.error = self.error, None
+        if self._errors:
+            e = self._errors[0]
+            self._errors.clear()
             raise e
 
     def release(self):

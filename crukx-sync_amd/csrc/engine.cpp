@@ -189,7 +189,8 @@ void copy_to_host(uint8_t *dst, const uint8_t *src, uint64_t n, hipStream_t s) {
 
 // ------------------------------------------------------------------ workspace
 // Device buffers of one call.  Small buffers are carved from chunks of kArenaChunk bytes so that a
-// call makes few trips through the caller's allocator; large ones are allocated on their own.
+// call makes few trips through the caller's allocator; large ones are allocated on their own unless
+// a reserved block (reserve) still has room for them.
 constexpr uint64_t kArenaChunk = 8ULL << 20;
 
 struct Arena {
@@ -197,18 +198,28 @@ struct Arena {
     void *ctx;
     uint8_t *chunk = nullptr;
     uint64_t used = 0, size = 0;
+    uint64_t total = 0;  // bytes handed out by get()
 
     void *raw(uint64_t bytes) {
         void *p = fn(ctx, bytes);
         if (!p) throw std::bad_alloc();
         return p;
     }
+    // one block of `bytes` for the buffers that follow
+    void reserve(uint64_t bytes) {
+        bytes = (bytes + 255) & ~uint64_t(255);
+        if (bytes <= size - used) return;
+        chunk = static_cast<uint8_t *>(raw(bytes));
+        used = 0;
+        size = bytes;
+    }
     template <typename T>
     T *get(uint64_t count) {
         uint64_t bytes = std::max<uint64_t>(count * sizeof(T), 16);
         bytes = (bytes + 255) & ~uint64_t(255);
-        if (bytes > kArenaChunk / 4) return static_cast<T *>(raw(bytes));
+        total += bytes;
         if (used + bytes > size) {
+            if (bytes > kArenaChunk / 4) return static_cast<T *>(raw(bytes));
             chunk = static_cast<uint8_t *>(raw(kArenaChunk));
             used = 0;
             size = kArenaChunk;
@@ -218,6 +229,27 @@ struct Arena {
         return p;
     }
 };
+
+// Workspace bytes of the last call of one kind and its size key (e.g. its slab count): a following
+// call with a key within 1/16 of it reserves that much (plus 1/32) in one allocation, instead of one
+// trip through the caller's allocator per large buffer.  Only a hint: a call that needs more
+// allocates the rest buffer by buffer.
+struct ArenaHint {
+    std::mutex m;
+    uint64_t key = 0, bytes = 0;
+
+    uint64_t get(uint64_t k) {
+        std::lock_guard<std::mutex> g(m);
+        if (!key || k + k / 16 < key || key + key / 16 < k) return 0;
+        return bytes + bytes / 32;
+    }
+    void put(uint64_t k, uint64_t b) {
+        std::lock_guard<std::mutex> g(m);
+        key = k;
+        bytes = b;
+    }
+};
+ArenaHint g_apply_hint, g_encode_hint;
 
 template <typename T>
 void h2d(T *dst, const T *src, uint64_t n, hipStream_t s) {
@@ -409,6 +441,9 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     if (L.descs.empty()) return;
     finish_layout(L, slab);
     const uint32_t T = (uint32_t)L.descs.size(), tiles = L.tiles;
+    const uint64_t hint_key = tiles;
+    ar.reserve(g_encode_hint.get(hint_key));
+    hc.mark("enc_layout");
 
     TensorDesc *d_descs = ar.get<TensorDesc>(T);
     h2d(d_descs, L.descs.data(), T, s);
@@ -590,6 +625,7 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     sync(s);
     hc.mark("enc_wait_pack");
     if (hovf) throw Invalid("a block exceeds 2^32 bits; the update cannot be represented");
+    g_encode_hint.put(hint_key, ar.total);
     E.d_block_bits = bb;
     E.payload_len = (total_bits + 7) / 8;
     E.d_payload = reinterpret_cast<const uint8_t *>(words);
@@ -621,6 +657,9 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     }
     finish_layout(L, slab);
     const uint32_t tiles = L.tiles;
+    const uint64_t hint_key = (uint64_t)tiles + C / 256;
+    ar.reserve(g_apply_hint.get(hint_key));
+    hc.mark("apply_layout");
 
     // groups, decoding tables and the group lookup (codec.py:594-625)
     int table_of[256];
@@ -707,6 +746,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     // the main stream takes the exponent counts (pass A) and their scans.
     unsigned long long *dz = ar.get<unsigned long long>(C);
     unsigned long long *blk_sum = ar.get<unsigned long long>(B), *blk_prefix = ar.get<unsigned long long>(B + 1);
+    hc.mark("apply_upload");
     Fork fork(s);
     DecodeArgs da{d_descs, pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, bmap, d_lim, d_off, d_syms,
                   (uint32_t)syms.size(), dz, blk_sum, bad};
@@ -746,6 +786,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     launch_scan_tables(d_descs, hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, sizes, s);
     launch_tensor_sums(d_descs, T, full, t_full, s);
     fork.join();
+    hc.mark("apply_pass_a");
 
     BlockArgs ba{d_groups, (uint32_t)G, slab, bmap, d_descs, sizes, blk_prefix, local, dz, pv, bdelta, bad, B};
     launch_local_fix(ba, B, s);
@@ -782,6 +823,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
         throw Corrupt(m + "])");
     }
     if (hbad) throw Corrupt("payload positions outside their exponent groups");
+    g_apply_hint.put(hint_key, ar.total);
     launch_scatter(ba, B, s);
     sync(s);
     hc.mark("apply_wait_scatter");

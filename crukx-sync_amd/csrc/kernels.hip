@@ -1267,6 +1267,13 @@ static_assert(kTgtCapSparse % 1024 == 0 && kTgtCapDense % 1024 == 0, "target lis
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u16x2 as16(uint32_t v) { return __builtin_bit_cast(u16x2, v); }
 
+// (a & m) | b in one instruction (the mask from a scalar register)
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t b) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(b));
+    return r;
+}
+
 // v + this lane's bit of m, in one instruction (the mask as carry-in)
 __device__ __forceinline__ uint32_t add_bit(uint32_t v, uint64_t m) {
     uint32_t r;
@@ -1324,9 +1331,9 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
             if (f < sl.f_lo || f >= sl.f_hi) c.x = as16(sp).x;
             if (f + 1 < sl.f_lo || f + 1 >= sl.f_hi) c.y = as16(sp).y;
         }
-        const u16x2 ad = c >> (unsigned short)kCntShift;
-        atomicAdd(reinterpret_cast<uint32_t *>(cnt + ((uint32_t)ad.x | rep4)), 1u);
-        atomicAdd(reinterpret_cast<uint32_t *>(cnt + ((uint32_t)ad.y | rep4)), 1u);
+        const uint32_t ad = __builtin_bit_cast(uint32_t, c >> (unsigned short)kCntShift);
+        atomicAdd(reinterpret_cast<uint32_t *>(cnt + and_or(ad, 0xFFFFu, rep4)), 1u);
+        atomicAdd(reinterpret_cast<uint32_t *>(cnt + ((ad >> 16) | rep4)), 1u);
         const uint32_t s = sel_count(S.cnt, ln);  // exponent ln's count up to the row's end
         const uint32_t seen = prev;
         prev = s;
