@@ -234,20 +234,25 @@ def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
     if not names:
         return Update([], []), {}
     A, B = [], []
+    T16 = torch.Tensor
     for name in names:
-        a, b = _check16(name, old[name]), _check16(name, new[name])
+        a, b = old[name], new[name]
+        if (type(a) is not T16 or type(b) is not T16 or a.dtype not in _DTYPES16 or b.dtype not in _DTYPES16
+                or not a.is_contiguous() or not b.is_contiguous()):
+            a, b = _check16(name, a), _check16(name, b)  # raise, or pass tensor subclasses
         if a.shape != b.shape:
             raise ValueError(f"{name}: old and new differ in shape")
         A.append(a)
         B.append(b)
-    src = A[0].device
-    if any(t.device != src for t in A) or any(t.device != src for t in B):
-        raise ValueError("all tensors must be on one device")
+    src = _device_of(A + B, "all tensors must be on one device")
     dev = _hip_device(src)
     if src != dev:
         A, B = [a.to(dev) for a in A], [b.to(dev) for b in B]
-    A = [a if a.data_ptr() & 3 == 0 else a.clone() for a in A]  # the kernels read 32-bit words
-    B = [b if b.data_ptr() & 3 == 0 else b.clone() for b in B]
+    pa, pb = [a.data_ptr() for a in A], [b.data_ptr() for b in B]
+    if any((x | y) & 3 for x, y in zip(pa, pb)):  # the kernels read 32-bit words
+        A = [a if a.data_ptr() & 3 == 0 else a.clone() for a in A]
+        B = [b if b.data_ptr() & 3 == 0 else b.clone() for b in B]
+        pa, pb = [a.data_ptr() for a in A], [b.data_ptr() for b in B]
     numels = [a.numel() for a in A]
     if checksums is None:
         has, vals = [0] * len(names), [0] * len(names)
@@ -261,8 +266,7 @@ def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
     err = _native.errbuf()
     h = ctypes.c_void_p()
     with torch.cuda.device(dev):
-        rc = L.crx_encode(n, _native.ptr_array([a.data_ptr() for a in A]),
-                          _native.ptr_array([b.data_ptr() for b in B]), _native.u64_array(numels),
+        rc = L.crx_encode(n, _native.ptr_array(pa), _native.ptr_array(pb), _native.u64_array(numels),
                           _native.i32_array(has), _native.u64_array(vals), int(_SLAB),
                           _native.stream_of(dev), ws.fn, None, ctypes.byref(h), err, 512)
     ws.check()
@@ -278,9 +282,9 @@ def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
 # ---------------------------------------------------------------- apply
 
 # Receiver-side exponent counts per slab, kept on the device across updates of the same tensors:
-# id(tensor) -> (weakref, _version after our last write, device buffer, slab size).  They are used
-# only with the same slab size and a checksum-cache hit for the tensor (the same trust rule), and
-# let apply skip its full read of those weights (crx_apply_cached).
+# id(tensor) -> (weakref, _version after our last write, device buffer, slab size, device, buffer
+# address).  They are used only with the same slab size and a checksum-cache hit for the tensor (the
+# same trust rule), and let apply skip its full read of those weights (crx_apply_cached).
 _hist = {}
 
 
@@ -291,11 +295,11 @@ def _hist_lookup(t):
     return e
 
 
-def _hist_store(t, buf, slab):
+def _hist_store(t, buf, slab, dev):
     key = id(t)
     e = _hist.get(key)
     ref = e[0] if e is not None and e[0]() is t else weakref.ref(t, lambda _r, key=key: _hist.pop(key, None))
-    _hist[key] = (ref, t._version, buf, slab)
+    _hist[key] = (ref, t._version, buf, slab, dev, buf.data_ptr())
 
 
 def _cache_get(checksums, name, t):
@@ -303,6 +307,17 @@ def _cache_get(checksums, name, t):
     (codec.py:457-460)."""
     hit = checksums.get(name) if checksums is not None else None
     return hit[0] if isinstance(hit, tuple) and hit[1] == t._version else None
+
+
+def _device_of(ts: list, what: str) -> torch.device:
+    """The one device of all tensors in `ts` (ValueError naming `what` otherwise)."""
+    idx = {t.get_device() for t in ts}
+    if len(idx) == 1 and next(iter(idx)) >= 0:  # all on one GPU
+        return ts[0].device
+    src = ts[0].device
+    if any(t.device != src for t in ts):
+        raise ValueError(what)
+    return src
 
 
 def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None = None) -> int:
@@ -314,20 +329,30 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     if not names:
         return 0
     targets = []
+    get = weights.get if isinstance(weights, dict) else None
+    T16 = torch.Tensor
     for name, numel in zip(names, numels):
-        t = weights.get(name) if isinstance(weights, dict) else (weights[name] if name in weights else None)
+        t = get(name) if get is not None else (weights[name] if name in weights else None)
         if t is None:
             raise ValueError(f"update has tensor {name!r} that the receiver does not have")
-        a = _check16(name, t)
-        if a.numel() != numel:
-            raise ValueError(f"{name}: update is for {numel} elements, receiver has {a.numel()}")
-        targets.append(a)
-    src = targets[0].device
-    if any(a.device != src for a in targets):
-        raise ValueError("all updated tensors must be on one device")
+        if type(t) is not T16 or t.dtype not in _DTYPES16 or not t.is_contiguous():
+            t = _check16(name, t)  # raises, or passes a tensor subclass
+        if t.numel() != numel:
+            raise ValueError(f"{name}: update is for {numel} elements, receiver has {t.numel()}")
+        targets.append(t)
+    src = _device_of(targets, "all updated tensors must be on one device")
     dev = _hip_device(src)
     staged = [a.to(dev) for a in targets] if src != dev else targets
-    cache = [_cache_get(checksums, name, t) for name, t in zip(names, targets)] if checksums is not None else [None] * len(names)
+    n = len(names)
+    vers = [t._version for t in targets]
+    if checksums is not None:
+        cg = checksums.get
+        cache = []
+        for name, v in zip(names, vers):
+            hit = cg(name)
+            cache.append(hit[0] if isinstance(hit, tuple) and hit[1] == v else None)
+    else:
+        cache = [None] * n
     has = [0 if c is None else 1 for c in cache]
     vals = [0 if c is None else c & _MASK64 for c in cache]
     L = _native.lib()
@@ -346,26 +371,28 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     hist_in, hist_out, bufs = [], [], []
     if keep:
         fresh = []  # tensors without usable counts: one allocation, sliced per tensor
-        for i, (a, c) in enumerate(zip(targets, cache)):
-            e = _hist_lookup(a)
-            if c is not None and e is not None and e[1] == a._version and e[2].device == dev and e[3] == slab:
+        hg = _hist.get
+        for i, (a, c, v) in enumerate(zip(targets, cache, vers)):
+            e = hg(id(a)) if c is not None else None
+            if e is not None and e[0]() is a and e[1] == v and e[3] == slab and e[4] == dev:
                 bufs.append(e[2])
+                hist_in.append(e[5])
+                hist_out.append(e[5])
             else:
                 bufs.append(None)
+                hist_in.append(0)
+                hist_out.append(0)
                 fresh.append((i, L.crx_apply_hist_words(a.numel(), slab)))
         if fresh:
             block = torch.empty(sum(w for _, w in fresh), dtype=torch.int32, device=dev)
-            at = 0
+            at, base = 0, block.data_ptr()
             for i, w in fresh:
                 bufs[i] = block[at:at + w]
+                hist_out[i] = base + 4 * at
                 at += w
-        fresh_set = {i for i, _ in fresh}
-        for i, buf in enumerate(bufs):
-            hist_in.append(0 if i in fresh_set else buf.data_ptr())
-            hist_out.append(buf.data_ptr())
     with torch.cuda.device(dev):
         rc = L.crx_apply_cached(u.handle, payload_dev or None, _native.ptr_array([a.data_ptr() for a in staged]),
-                                _native.u64_array([a.numel() for a in staged]), _native.i32_array(has),
+                                _native.u64_array(numels), _native.i32_array(has),
                                 _native.u64_array(vals),
                                 _native.ptr_array(hist_in) if keep else None,
                                 _native.ptr_array(hist_out) if keep else None,
@@ -381,8 +408,9 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     else:
         for a, s in zip(targets, staged):
             a.copy_(s)  # an in-place op: bumps the tensor's version
-    for a, buf in zip(targets, bufs):
-        _hist_store(a, buf, slab)
+    if keep:
+        for a, buf in zip(targets, bufs):
+            _hist_store(a, buf, slab, dev)
     if checksums is not None:  # record the version after our own write
         checksums.update({name: (c, t._version) for name, c, t in zip(names, header_chk, targets)})
     return changed.value
