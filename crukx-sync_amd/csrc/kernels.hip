@@ -558,10 +558,20 @@ __global__ __launch_bounds__(256) void k_r0(GroupDev *groups, uint32_t n_groups,
 // spreads one wavefront's reads of its threads' k-th records over the banks).
 constexpr uint32_t kRecPad = kElemsPerThread + 1;
 
+// All of a thread's loads are issued before any is stored (one memory latency per workgroup, not
+// one per record).
 __device__ __forceinline__ void stage_records(const uint64_t *sorted, uint64_t n, uint64_t wbase, uint64_t *rec) {
-    for (uint32_t j = threadIdx.x; j < (uint32_t)kElemsPerWG; j += 256) {
-        const uint64_t i = wbase + j;
-        rec[(j / kElemsPerThread) * kRecPad + (j % kElemsPerThread)] = i < n ? sorted[i] : 0ULL;
+    constexpr uint32_t kPer = kElemsPerWG / 256;
+    uint64_t v[kPer];
+#pragma unroll
+    for (uint32_t u = 0; u < kPer; ++u) {
+        const uint64_t i = wbase + threadIdx.x + 256 * u;
+        v[u] = i < n ? sorted[i] : 0ULL;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kPer; ++u) {
+        const uint32_t j = threadIdx.x + 256 * u;
+        rec[(j / kElemsPerThread) * kRecPad + (j % kElemsPerThread)] = v[u];
     }
     __syncthreads();
 }
