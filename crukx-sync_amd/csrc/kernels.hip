@@ -15,6 +15,7 @@ constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ULL;
 constexpr uint64_t kMix1 = 0xBF58476D1CE4E5B9ULL;
 constexpr uint64_t kMix2 = 0x94D049BB133111EBULL;
 constexpr int kRankRows = 8;    // rows per batch of the encode rank pass (two streams)
+constexpr uint32_t kPlaceRecs = 12;  // records per lane per batch of the placement pass
 constexpr int kChgCap = 256;    // changes the rank pass buffers in LDS; a flush leaves room for a row
 constexpr uint32_t kRankCopies = 4;  // copies of each exponent count in the rank pass (2, 4 or 8; 4 measured best)
 static_assert(kRankCopies == 2 || kRankCopies == 4 || kRankCopies == 8, "kRankCopies");
@@ -523,7 +524,9 @@ __global__ __launch_bounds__(64) void k_place(EncRankArgs a, const uint32_t *til
         off_dest[k] = gbase[(uint64_t)t * 256 + k] + hchg_pre[(uint64_t)tau * 256 + k];
     }
     wave_fence();
-    constexpr uint32_t U = 4;  // records per lane in flight
+    // kPlaceRecs records per lane: all loads, then all LDS lookups, then all stores (a load issued
+    // after a store would wait for the store too)
+    constexpr uint32_t U = kPlaceRecs;
     for (uint32_t j0 = 0; j0 < count; j0 += 64 * U) {
         uint64_t r[U];
 #pragma unroll
@@ -531,13 +534,18 @@ __global__ __launch_bounds__(64) void k_place(EncRankArgs a, const uint32_t *til
             const uint32_t j = j0 + 64 * u + ln;
             r[u] = j < count ? a.rec[base + j] : 0ULL;
         }
+        uint32_t dest[U], lo[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t rank = (uint32_t)(r[u] & 0x1FFFF), rc = (uint32_t)((r[u] >> 17) & 0x1FFFF);
+            const uint32_t k = (uint32_t)((r[u] >> 34) & 0xFF);
+            dest[u] = off_dest[k] + rc;
+            lo[u] = off_rank[k] + rank;
+        }
 #pragma unroll
         for (uint32_t u = 0; u < U; ++u) {
             const uint32_t j = j0 + 64 * u + ln;
-            const uint32_t rank = (uint32_t)(r[u] & 0x1FFFF), rc = (uint32_t)((r[u] >> 17) & 0x1FFFF);
-            const uint32_t k = (uint32_t)((r[u] >> 34) & 0xFF), zz = (uint32_t)(r[u] >> 42);
-            const uint32_t dest = off_dest[k] + rc;
-            if (j < count && dest < n_sorted) sorted[dest] = ((uint64_t)zz << 32) | (off_rank[k] + rank);
+            if (j < count && dest[u] < n_sorted) sorted[dest[u]] = ((r[u] >> 42) << 32) | lo[u];
         }
     }
 }
