@@ -715,7 +715,8 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     GroupDev *d_groups = ar.get<GroupDev>(G);
     h2d(d_groups, groups.data(), G, s);
     uint32_t *bmap = ar.get<uint32_t>(B);
-    launch_block_map(d_groups, (uint32_t)G, bmap, s);
+    BlockInfo *binfo = ar.get<BlockInfo>(B);
+    launch_block_map(d_groups, (uint32_t)G, bmap, binfo, s);
     uint32_t *d_lim = ar.get<uint32_t>(lim.size()), *d_off = ar.get<uint32_t>(off.size());
     uint32_t *d_syms = ar.get<uint32_t>(syms.size());
     h2d(d_lim, lim.data(), lim.size(), s);
@@ -788,7 +789,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     fork.join();
     hc.mark("apply_pass_a");
 
-    BlockArgs ba{d_groups, (uint32_t)G, slab, bmap, d_descs, sizes, blk_prefix, local, dz, pv, bdelta, bad, B};
+    BlockArgs ba{d_groups, (uint32_t)G, slab, binfo, d_descs, sizes, blk_prefix, local, dz, pv, bdelta, bad, B};
     launch_local_fix(ba, B, s);
     uint2 *more = ar.get<uint2>(3 * (uint64_t)tiles);  // at most 3 windows after the first per slab
     unsigned int *n_more = ar.get<unsigned int>(1);

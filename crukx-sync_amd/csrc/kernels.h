@@ -52,6 +52,18 @@ struct GroupDev {
     uint32_t table;      // apply: decoding table index
 };
 
+// Per change block of an update (apply): what the per-block kernels need, in one load.
+struct BlockInfo {
+    uint32_t g;         // group
+    uint32_t eb;        // first change of the block in update order
+    uint32_t cnt;       // changes in the block (1..256)
+    uint32_t key;       // tensor << 8 | exponent of the group
+    uint32_t blk_base;  // first block of the group
+    uint32_t count;     // changes in the group
+    uint32_t tensor;
+    uint32_t pad;
+};
+
 struct EncRankArgs {
     const TensorDesc *descs;
     const uint32_t *tile_tensor;    // [tiles] tensor of each slab
@@ -145,7 +157,7 @@ struct SelectArgs {
 struct BlockArgs {                  // per-block kernels over the change list (one workgroup per block)
     const GroupDev *groups;
     uint32_t n_groups, slab;
-    const uint32_t *bmap;           // [blocks] group of every block
+    const BlockInfo *binfo;         // [blocks]
     const TensorDesc *descs;
     const uint32_t *sizes;
     const unsigned long long *blk_prefix;
@@ -175,7 +187,7 @@ void launch_stats(const StatsArgs &a, hipStream_t s);
 void launch_code_lengths(const CodeArgs &a, hipStream_t s);
 // cmap[c] = group of change kElemsPerThread * c; bmap[b] = group of block b
 void launch_chunk_map(const GroupDev *groups, uint32_t n_groups, uint32_t *cmap, hipStream_t s);
-void launch_block_map(const GroupDev *groups, uint32_t n_groups, uint32_t *bmap, hipStream_t s);
+void launch_block_map(const GroupDev *groups, uint32_t n_groups, uint32_t *bmap, BlockInfo *binfo, hipStream_t s);
 void launch_pack(const CodeArgs &a, hipStream_t s);
 void launch_block_bits(const unsigned long long *bstart, uint64_t n_blocks, uint32_t *out, unsigned int *overflow,
                        hipStream_t s);

@@ -66,10 +66,14 @@ __global__ __launch_bounds__(256) void k_chunk_map(const GroupDev *groups, uint3
     for (uint64_t c = c0 + threadIdx.x; c < c1; c += 256) cmap[c] = blockIdx.x;
 }
 
-__global__ __launch_bounds__(256) void k_block_map(const GroupDev *groups, uint32_t *bmap) {
+__global__ __launch_bounds__(256) void k_block_map(const GroupDev *groups, uint32_t *bmap, BlockInfo *binfo) {
     const GroupDev g = groups[blockIdx.x];
     const uint32_t nb = (g.count + 255) / 256;
-    for (uint32_t i = threadIdx.x; i < nb; i += 256) bmap[g.blk_base + i] = blockIdx.x;
+    for (uint32_t i = threadIdx.x; i < nb; i += 256) {
+        bmap[g.blk_base + i] = blockIdx.x;
+        binfo[g.blk_base + i] = BlockInfo{blockIdx.x, g.elem_base + 256 * i, min(256u, g.count - 256 * i),
+                                          (g.tensor << 8) | g.exponent, g.blk_base, g.count, g.tensor, 0};
+    }
 }
 
 // last group whose first change is <= i
@@ -1131,21 +1135,10 @@ __global__ __launch_bounds__(64) void k_decode(DecodeArgs a) {
 // loads are issued together).
 constexpr uint32_t kBlocksPerWG = 4;
 
-// Where the per-block kernels find block b's changes: [eb, eb + cnt) of its group g.
-struct BlockRef {
-    uint32_t g, cnt;
-    uint64_t eb;
-};
-__device__ __forceinline__ BlockRef block_ref(const BlockArgs &a, uint64_t b, GroupDev &gr) {
-    BlockRef r{0, 0, 0};
-    if (b < a.n_blocks) {
-        r.g = a.bmap[b];
-        gr = a.groups[r.g];
-        const uint64_t kb = b - gr.blk_base;
-        r.cnt = (uint32_t)min64(256, gr.count - kb * 256);
-        r.eb = (uint64_t)gr.elem_base + kb * 256;
-    }
-    return r;
+// Block b's changes [eb, eb + cnt) and its group (cnt 0 past the last block).
+__device__ __forceinline__ BlockInfo block_info(const BlockArgs &a, uint64_t b) {
+    if (b < a.n_blocks) return a.binfo[b];
+    return BlockInfo{0, 0, 0, 0, 0, 0, 0, 0};
 }
 
 // local = (sum of (gap + 1) over earlier blocks of the group) + block-relative local; must stay
@@ -1153,35 +1146,40 @@ __device__ __forceinline__ BlockRef block_ref(const BlockArgs &a, uint64_t b, Gr
 __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
     const bool failed = *a.bad;  // read before this kernel's own flags
     const uint32_t s = threadIdx.x;
-    GroupDev gr[kBlocksPerWG];
-    BlockRef r[kBlocksPerWG];
+    BlockInfo r[kBlocksPerWG];
     unsigned long long base[kBlocksPerWG];
     uint64_t size[kBlocksPerWG];
     uint32_t raw[kBlocksPerWG];
 #pragma unroll
+    for (uint32_t u = 0; u < kBlocksPerWG; ++u) r[u] = block_info(a, (uint64_t)blockIdx.x * kBlocksPerWG + u);
+#pragma unroll
     for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
         const uint64_t b = (uint64_t)blockIdx.x * kBlocksPerWG + u;
-        r[u] = block_ref(a, b, gr[u]);
+        size[u] = 0;
+        base[u] = 0;
+        raw[u] = 0;
         if (r[u].cnt) {
-            size[u] = a.sizes[(uint64_t)gr[u].tensor * 256 + gr[u].exponent];
-            base[u] = a.blk_prefix[b] - a.blk_prefix[gr[u].blk_base];
-            // a group with more changes than the receiver has elements of its exponent (checked even
-            // after a failed decode: the reference checks it first)
-            if (b == gr[u].blk_base && gr[u].count > size[u] && threadIdx.x == 0)
-                atomicOr(a.bad, a.descs[gr[u].tensor].numel > kGroupCheckNumel ? kBadGroup : kBadLocal);
+            size[u] = a.sizes[r[u].key];
+            base[u] = a.blk_prefix[b] - a.blk_prefix[r[u].blk_base];
+            if (s < r[u].cnt) raw[u] = (uint32_t)(a.dz[(uint64_t)r[u].eb + s] >> 32);
         }
     }
-    if (failed) return;
 #pragma unroll
-    for (uint32_t u = 0; u < kBlocksPerWG; ++u)
-        if (s < r[u].cnt) raw[u] = (uint32_t)(a.dz[r[u].eb + s] >> 32);
+    for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
+        const uint64_t b = (uint64_t)blockIdx.x * kBlocksPerWG + u;
+        // a group with more changes than the receiver has elements of its exponent (checked even
+        // after a failed decode: the reference checks it first)
+        if (r[u].cnt && b == r[u].blk_base && r[u].count > size[u] && threadIdx.x == 0)
+            atomicOr(a.bad, a.descs[r[u].tensor].numel > kGroupCheckNumel ? kBadGroup : kBadLocal);
+    }
+    if (failed) return;
 #pragma unroll
     for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
         if (s < r[u].cnt) {
             const unsigned long long local = base[u] + raw[u];
             if (local >= size[u]) atomicOr(a.bad, kBadLocal);
-            a.local[r[u].eb + s] = (uint32_t)min64(local, 0xFFFFFFFFULL);
-            a.pv[r[u].eb + s] = kNone;
+            a.local[(uint64_t)r[u].eb + s] = (uint32_t)min64(local, 0xFFFFFFFFULL);
+            a.pv[(uint64_t)r[u].eb + s] = kNone;
         }
     }
 }
@@ -1583,17 +1581,16 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
         if (s < kBlocksPerWG && b < a.n_blocks) a.bdelta[b] = 0;
         return;
     }
-    GroupDev gr[kBlocksPerWG];
-    BlockRef r[kBlocksPerWG];
+    BlockInfo r[kBlocksPerWG];
     unsigned long long pv[kBlocksPerWG];
     uint32_t zz[kBlocksPerWG];
 #pragma unroll
-    for (uint32_t u = 0; u < kBlocksPerWG; ++u) r[u] = block_ref(a, (uint64_t)blockIdx.x * kBlocksPerWG + u, gr[u]);
+    for (uint32_t u = 0; u < kBlocksPerWG; ++u) r[u] = block_info(a, (uint64_t)blockIdx.x * kBlocksPerWG + u);
 #pragma unroll
     for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
         if (s < r[u].cnt) {
-            pv[u] = a.pv[r[u].eb + s];
-            zz[u] = (uint32_t)a.dz[r[u].eb + s];
+            pv[u] = a.pv[(uint64_t)r[u].eb + s];
+            zz[u] = (uint32_t)a.dz[(uint64_t)r[u].eb + s];
         }
     }
 #pragma unroll
@@ -1609,10 +1606,10 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
                 const uint32_t old = lo & 0xFFFFu;
                 const uint32_t nu = (uint32_t)((int32_t)old + delta) & 0xFFFF;
                 d = (uint64_t)((int64_t)nu - (int64_t)old) * weight(p);
-                a.pv[r[u].eb + s] = p | ((unsigned long long)nu << 32);
+                a.pv[(uint64_t)r[u].eb + s] = p | ((unsigned long long)nu << 32);
                 const uint32_t eo = (old >> 7) & 0xFF, en = (nu >> 7) & 0xFF;
                 if (eo != en) {  // the element moves between exponent counts of its slab
-                    uint32_t *h = a.descs[gr[u].tensor].hist_out;
+                    uint32_t *h = a.descs[r[u].tensor].hist_out;
                     if (h) {
                         h += (uint64_t)(p / a.slab) * 256;
                         atomicSub(&h[eo], 1u);
@@ -1635,12 +1632,11 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
 // One workgroup per block: the stores are bound by HBM partial writes, and more blocks per workgroup
 // measured slower.
 __global__ __launch_bounds__(256) void k_scatter(BlockArgs a) {
-    GroupDev gr;
-    const BlockRef r = block_ref(a, blockIdx.x, gr);
+    const BlockInfo r = block_info(a, blockIdx.x);
     const uint32_t s = threadIdx.x;
     if (s < r.cnt) {
-        const unsigned long long pv = a.pv[r.eb + s];
-        a.descs[gr.tensor].base[(uint32_t)pv] = (uint16_t)(pv >> 32);
+        const unsigned long long pv = a.pv[(uint64_t)r.eb + s];
+        a.descs[r.tensor].base[(uint32_t)pv] = (uint16_t)(pv >> 32);
     }
 }
 
@@ -1695,8 +1691,8 @@ void launch_chunk_map(const GroupDev *groups, uint32_t n_groups, uint32_t *cmap,
     CRX_LAUNCH("chunk_map", k_chunk_map, n_groups, 256, s, groups, cmap);
 }
 
-void launch_block_map(const GroupDev *groups, uint32_t n_groups, uint32_t *bmap, hipStream_t s) {
-    CRX_LAUNCH("block_map", k_block_map, n_groups, 256, s, groups, bmap);
+void launch_block_map(const GroupDev *groups, uint32_t n_groups, uint32_t *bmap, BlockInfo *binfo, hipStream_t s) {
+    CRX_LAUNCH("block_map", k_block_map, n_groups, 256, s, groups, bmap, binfo);
 }
 
 void launch_code_lengths(const CodeArgs &a, hipStream_t s) {
