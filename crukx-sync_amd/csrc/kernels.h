@@ -147,8 +147,8 @@ struct SelectArgs {
     const int32_t *group_of;        // [tensor][256] group index or -1
     const GroupDev *groups;
     const uint32_t *local;          // group-local index of every change
-    unsigned long long *pv;         // [changes] (in-row offset << 16 | old bits) | row's element index << 32; kNone: unplaced
-    const unsigned int *bad;
+    unsigned long long *pv;         // [changes] (in-row offset << 16 | old bits) | row's element index << 32
+    unsigned int *bad;              // kBadUnplaced: a slab's targets were not all found
     uint2 *more;                    // [3 tiles] (slab, first exponent) of windows after a slab's first
     unsigned int *n_more;           // their number (zero before k_locate)
     uint32_t n_front;               // listed windows taken by the front blocks of the select pass

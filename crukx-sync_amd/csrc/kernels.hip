@@ -1179,7 +1179,6 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
             const unsigned long long local = base[u] + raw[u];
             if (local >= size[u]) atomicOr(a.bad, kBadLocal);
             a.local[(uint64_t)r[u].eb + s] = (uint32_t)min64(local, 0xFFFFFFFFULL);
-            a.pv[(uint64_t)r[u].eb + s] = kNone;
         }
     }
 }
@@ -1416,6 +1415,9 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
             H &= H - 1;
         } while (H);
     });
+    // every target of this window's exponents is found once its rank is passed: one still pending
+    // lies past the slab's elements of its exponent (never so when the local indices were in range)
+    if (ci < cend) atomicOr(a.bad, kBadUnplaced);
 }
 
 // One window of one slab: exponents [kfirst, kfirst + kWin), or from the slab's lowest exponent with
@@ -1598,10 +1600,8 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
         unsigned long long d = 0;
         const uint32_t lo = (uint32_t)pv[u];  // (in-row offset << 16) | old bits; row start << 32
         const uint32_t p = (uint32_t)(pv[u] >> 32) + (lo >> 16);
-        if (s < r[u].cnt) {
-            if (lo == kNone) {
-                atomicOr(a.bad, kBadUnplaced);
-            } else {
+        if (s < r[u].cnt) {  // every change was placed: the select pass flags a slab that missed one
+            {
                 const int32_t delta = (int32_t)(zz[u] >> 1) ^ -(int32_t)(zz[u] & 1);
                 const uint32_t old = lo & 0xFFFFu;
                 const uint32_t nu = (uint32_t)((int32_t)old + delta) & 0xFFFF;
