@@ -453,61 +453,6 @@ __global__ __launch_bounds__(256) void k_scan_fin(const TensorDesc *descs, uint3
 
 // ================================================================== encode: groups and placement
 // Groups are the non-empty (tensor, exponent) pairs in (tensor, exponent) order (codec.py:317-333).
-__global__ __launch_bounds__(1024) void k_enc_groups(const uint32_t *tot, uint32_t n_tensors, GroupDev *groups,
-                                                     uint32_t *gbase, unsigned long long *counters) {
-    // each thread owns a run of consecutive (tensor, exponent) totals: sums, a block scan of the
-    // sums, then the run again with its offsets
-    __shared__ unsigned long long wsum_v[16], wsum_z[16];
-    const uint32_t tid = threadIdx.x, ln = lane(), w = tid >> 6;
-    const uint64_t n = (uint64_t)n_tensors * 256, per = (n + 1023) / 1024;
-    const uint64_t lo = min64(tid * per, n), hi = min64(lo + per, n);
-    unsigned long long sv = 0, sz = 0;
-    for (uint64_t i = lo; i < hi; ++i) {
-        const uint32_t v = tot[i];
-        sv += v;
-        sz += v ? 1u : 0u;
-    }
-    unsigned long long iv = sv, iz = sz;  // inclusive scans within the wavefront
-    for (int o = 1; o < 64; o <<= 1) {
-        const unsigned long long tv = __shfl_up(iv, o, 64), tz = __shfl_up(iz, o, 64);
-        if (ln >= (uint32_t)o) {
-            iv += tv;
-            iz += tz;
-        }
-    }
-    if (ln == 63) {
-        wsum_v[w] = iv;
-        wsum_z[w] = iz;
-    }
-    __syncthreads();
-    unsigned long long ev = iv - sv, ez = iz - sz, tv = 0, tz = 0;
-    for (uint32_t q = 0; q < 16; ++q) {
-        if (q < w) {
-            ev += wsum_v[q];
-            ez += wsum_z[q];
-        }
-        tv += wsum_v[q];
-        tz += wsum_z[q];
-    }
-    for (uint64_t i = lo; i < hi; ++i) {
-        const uint32_t v = tot[i];
-        gbase[i] = (uint32_t)ev;  // meaningful while the total stays below 2^32 (checked by the host)
-        if (v) {
-            GroupDev g{};
-            g.tensor = (uint32_t)(i >> 8);
-            g.exponent = (uint32_t)(i & 255);
-            g.count = v;
-            g.elem_base = (uint32_t)ev;
-            groups[ez] = g;
-            ++ez;
-        }
-        ev += v;
-    }
-    if (tid == 0) {
-        counters[0] = tz;  // groups
-        counters[1] = tv;  // changes
-    }
-}
 
 // Records -> update order: position = group start + changes of the group in earlier slabs + rank
 // among the slab's changes of that exponent; value = zz and the group-local index.
@@ -772,6 +717,65 @@ __device__ unsigned long long block_exclusive_sum(unsigned long long v, unsigned
     __syncthreads();  // sh may be reused by the caller
     *total = tot;
     return before + incl - v;
+}
+
+// Groups from the (tensor, exponent) change totals, in that order: kGroupChunk totals per workgroup
+// (16 consecutive per thread).  A workgroup first sums the totals before its chunk (coalesced, a few
+// hundred KB at most), then scans its own.  gbase[i] = changes before entry i; counters[0] = groups,
+// counters[1] = changes (written by the last workgroup).
+constexpr uint32_t kGroupChunk = 4096;
+__global__ __launch_bounds__(256) void k_enc_groups(const uint32_t *tot, uint32_t n_tensors, GroupDev *groups,
+                                                    uint32_t *gbase, unsigned long long *counters) {
+    __shared__ unsigned long long sh[8];
+    const uint32_t tid = threadIdx.x;
+    const uint64_t n = (uint64_t)n_tensors * 256, c0 = (uint64_t)blockIdx.x * kGroupChunk;
+    unsigned long long pv = 0, pz = 0;  // totals before the chunk
+    for (uint64_t i0 = tid; i0 < c0; i0 += 256 * 8) {
+        uint32_t v[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) v[u] = i0 + 256 * u < c0 ? tot[i0 + 256 * u] : 0u;
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+            pv += v[u];
+            pz += v[u] ? 1u : 0u;
+        }
+    }
+    unsigned long long bv, bz;
+    block_exclusive_sum(pv, sh, &bv);
+    block_exclusive_sum(pz, sh, &bz);
+    const uint64_t lo = min64(c0 + 16ull * tid, n), hi = min64(lo + 16, n);
+    uint32_t v[16];
+    unsigned long long sv = 0, sz = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < 16; ++u) {
+        v[u] = lo + u < hi ? tot[lo + u] : 0u;
+        sv += v[u];
+        sz += v[u] ? 1u : 0u;
+    }
+    unsigned long long tv, tz;
+    unsigned long long ev = bv + block_exclusive_sum(sv, sh, &tv);
+    unsigned long long ez = bz + block_exclusive_sum(sz, sh, &tz);
+#pragma unroll
+    for (uint32_t u = 0; u < 16; ++u) {
+        const uint64_t i = lo + u;
+        if (i < hi) {
+            gbase[i] = (uint32_t)ev;  // meaningful while the total stays below 2^32 (checked by the host)
+            if (v[u]) {
+                GroupDev g{};
+                g.tensor = (uint32_t)(i >> 8);
+                g.exponent = (uint32_t)(i & 255);
+                g.count = v[u];
+                g.elem_base = (uint32_t)ev;
+                groups[ez] = g;
+                ++ez;
+            }
+            ev += v[u];
+        }
+    }
+    if (blockIdx.x + 1 == gridDim.x && tid == 0) {
+        counters[0] = bz + tz;  // groups
+        counters[1] = bv + tv;  // changes
+    }
 }
 
 __global__ __launch_bounds__(256) void k_code_lengths(CodeArgs a) {
@@ -1669,7 +1673,8 @@ void launch_scan_tables(const TensorDesc *descs, uint32_t *h, const ScanChunk *c
 
 void launch_enc_groups(const uint32_t *totals_chg, uint32_t n_tensors, GroupDev *groups, uint32_t *gbase,
                        unsigned long long *counters, hipStream_t s) {
-    CRX_LAUNCH("enc_groups", k_enc_groups, 1, 1024, s, totals_chg, n_tensors, groups, gbase, counters);
+    CRX_LAUNCH("enc_groups", k_enc_groups, grid1((uint64_t)n_tensors * 256, kGroupChunk), 256, s, totals_chg, n_tensors,
+               groups, gbase, counters);
 }
 
 void launch_place(const EncRankArgs &a, uint32_t tiles, const uint32_t *tile_tensor, const uint32_t *hall_pre,
