@@ -397,7 +397,7 @@ __global__ __launch_bounds__(64) void k_hist(HistArgs a) {
 // h[tile][256] -> exclusive prefix over the tensor's slabs, in place; totals[tensor][256].
 // The loops below read a batch of values before writing any (the reads and writes alias as far as
 // the compiler knows), so a batch costs one memory latency instead of one per value.
-constexpr uint32_t kScanBatch = 16;
+constexpr uint32_t kScanBatch = 32;  // = kScanTiles: a chunk in one batch
 
 // Per-slab counts of slab t of a chunk's tensor: the receiver's cached counts when the apply uses
 // them (the histogram pass skipped those slabs), else the table being scanned.
@@ -411,7 +411,13 @@ __global__ __launch_bounds__(256) void k_scan_sum(const TensorDesc *descs, const
     const TensorDesc td = descs[c.tensor];
     const uint32_t k = threadIdx.x;
     uint32_t s = 0;
-    for (uint32_t t = c.tile_begin; t < c.tile_end; ++t) s += scan_src(td, h, t)[k];
+    for (uint32_t t0 = c.tile_begin; t0 < c.tile_end; t0 += kScanBatch) {  // a batch of loads in flight
+        uint32_t x[kScanBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kScanBatch; ++j) x[j] = t0 + j < c.tile_end ? scan_src(td, h, t0 + j)[k] : 0u;
+#pragma unroll
+        for (uint32_t j = 0; j < kScanBatch; ++j) s += x[j];
+    }
     csum[(uint64_t)blockIdx.x * 256 + k] = s;
 }
 
