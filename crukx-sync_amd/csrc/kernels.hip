@@ -664,7 +664,7 @@ __device__ __forceinline__ uint32_t huff_entry(const CodeArgs &a, uint32_t e, ui
     return lo < a.n_rare ? a.rare_vals[lo] : 0u;
 }
 
-__device__ void thread_codes(const CodeArgs &a, const uint64_t *rec, uint64_t wbase, ThreadCodes &tc) {
+__device__ __forceinline__ void thread_codes(const CodeArgs &a, const uint64_t *rec, uint64_t wbase, ThreadCodes &tc) {
     const uint32_t t = threadIdx.x;
     const uint64_t ib = wbase + (uint64_t)t * kElemsPerThread;
     tc.n = ib < a.n ? (uint32_t)min64(kElemsPerThread, a.n - ib) : 0u;
@@ -802,6 +802,12 @@ __global__ __launch_bounds__(256) void k_code_lengths(CodeArgs a) {
 // range are written with plain stores; the first word (when the range starts inside it) and the
 // last partial word are shared with the neighbouring threads and are ORed in.  The stream is
 // big-endian bytes in 32-bit words and starts zeroed.
+// A thread's codes fill the contiguous bit range [off, off + its total).  In LDS (the workgroup's
+// words staged in `words`, indexed from word `w0`) every word is ORed in; in HBM, words wholly inside
+// the range are written with plain stores and only the first (when the range starts inside it) and
+// the last partial word, shared with the neighbouring threads, are ORed in.  Big-endian bytes in
+// 32-bit words; the words start zeroed.
+template <bool LDS>
 struct BitWriter {
     uint32_t *words;
     uint64_t w;       // next word to write
@@ -809,10 +815,11 @@ struct BitWriter {
     uint32_t n;       // number of pending bits (< 32 between calls)
     bool shared;      // the next word is shared with the previous thread
 
-    __device__ BitWriter(uint32_t *words_, uint64_t off) : words(words_), w(off >> 5), acc(0), n((uint32_t)(off & 31)), shared((off & 31) != 0) {}
+    __device__ BitWriter(uint32_t *words_, uint64_t w0, uint64_t off)
+        : words(words_ - (LDS ? w0 : 0)), w(off >> 5), acc(0), n((uint32_t)(off & 31)), shared((off & 31) != 0) {}
 
     __device__ __forceinline__ void emit(uint32_t v) {
-        if (shared) atomicOr(&words[w], __builtin_bswap32(v));
+        if (LDS || shared) atomicOr(&words[w], __builtin_bswap32(v));
         else words[w] = __builtin_bswap32(v);
         shared = false;
         ++w;
@@ -827,7 +834,7 @@ struct BitWriter {
             acc &= (1ULL << n) - 1;
         }
     }
-    __device__ void ones(uint64_t q) {
+    __device__ __forceinline__ void ones(uint64_t q) {
         for (; q >= 32; q -= 32) put(0xFFFFFFFFULL, 32);
         if (q) put((1ULL << q) - 1, (uint32_t)q);
     }
@@ -837,7 +844,8 @@ struct BitWriter {
 };
 
 // 1^q 0 r-bit remainder, then the Huffman code (codec.py:214-257)
-__device__ __forceinline__ void put_code(BitWriter &bw, uint64_t gap, uint32_t rice, uint32_t hv) {
+template <bool LDS>
+__device__ __forceinline__ void put_code(BitWriter<LDS> &bw, uint64_t gap, uint32_t rice, uint32_t hv) {
     const uint64_t q = gap >> rice;
     const uint32_t hl = hv & 31;
     const uint64_t tail = ((gap & ((1ULL << rice) - 1)) << hl) | (hv >> 5);  // 0, r bits, Huffman code
@@ -855,15 +863,10 @@ __device__ __forceinline__ void put_code(BitWriter &bw, uint64_t gap, uint32_t r
     }
 }
 
-__global__ __launch_bounds__(256) void k_pack(CodeArgs a) {
-    __shared__ uint64_t rec[256 * kRecPad];
-    const uint64_t wbase = (uint64_t)blockIdx.x * kElemsPerWG;
-    stage_records(a.sorted, a.n, wbase, rec);
-    ThreadCodes tc;
-    thread_codes(a, rec, wbase, tc);
-    if (!tc.n) return;
-    unsigned long long off = a.toff[(uint64_t)blockIdx.x * 256 + threadIdx.x];
-    BitWriter bw(a.words, off);
+template <bool LDS>
+__device__ __forceinline__ void pack_thread(const CodeArgs &a, const ThreadCodes &tc, uint32_t *words, uint64_t w0,
+                                            unsigned long long off) {
+    BitWriter<LDS> bw(words, w0, off);
 #pragma unroll
     for (int k = 0; k < kElemsPerThread; ++k) {
         if ((uint32_t)k < tc.n) {
@@ -874,6 +877,41 @@ __global__ __launch_bounds__(256) void k_pack(CodeArgs a) {
         }
     }
     bw.finish();
+}
+
+// The workgroup's bits are assembled in LDS (the record staging area, free once the codes are in
+// registers) and written out with coalesced stores; only its first and last words, which it may
+// share with the neighbouring workgroups, are ORed into HBM.  A workgroup whose bits do not fit
+// writes them directly.
+constexpr uint32_t kPackLdsWords = 256 * kRecPad * 2;
+__global__ __launch_bounds__(256) void k_pack(CodeArgs a) {
+    __shared__ uint64_t rec[256 * kRecPad];
+    const uint64_t wbase = (uint64_t)blockIdx.x * kElemsPerWG;
+    stage_records(a.sorted, a.n, wbase, rec);
+    ThreadCodes tc;
+    thread_codes(a, rec, wbase, tc);
+    const uint64_t t0 = (uint64_t)blockIdx.x * 256, n_thr = (a.n + kElemsPerThread - 1) / kElemsPerThread;
+    const unsigned long long b_lo = a.toff[t0], b_hi = a.toff[min64(t0 + 256, n_thr)];
+    const uint64_t w0 = b_lo >> 5, nw = ((b_hi + 31) >> 5) - w0;
+    const unsigned long long off = tc.n ? a.toff[t0 + threadIdx.x] : 0ULL;
+    if (nw > kPackLdsWords) {  // uniform across the workgroup
+        if (tc.n) pack_thread<false>(a, tc, a.words, 0, off);
+        return;
+    }
+    uint32_t *buf = reinterpret_cast<uint32_t *>(rec);
+    __syncthreads();  // every thread has read its records
+    for (uint32_t i = threadIdx.x; i < nw; i += 256) buf[i] = 0;
+    __syncthreads();
+    if (tc.n) pack_thread<true>(a, tc, buf, w0, off);
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < nw; i += 256) {
+        const uint32_t v = buf[i];
+        if (i == 0 || i + 1 == nw) {
+            if (v) atomicOr(&a.words[w0 + i], v);
+        } else {
+            a.words[w0 + i] = v;
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void k_block_bits(const unsigned long long *bstart, uint64_t n_blocks, uint32_t *out,
