@@ -251,19 +251,94 @@ struct ArenaHint {
 };
 ArenaHint g_apply_hint, g_encode_hint;
 
+// The small transfers of a call go through pinned host memory, so each is a plain asynchronous DMA (a
+// copy from or to pageable memory is staged by the runtime and holds the host thread until it is
+// done).  Uploads are copied in when issued; downloads land in the arena and are copied out by
+// sync(), which every call runs before it reads them.  One arena per host thread; its memory is
+// reused only after the stream it served was synchronized (or its last copy waited for).
+struct PinnedStage {
+    std::vector<std::pair<uint8_t *, uint64_t>> blocks;  // the last one is in use
+    uint64_t used = 0;
+    struct Out {
+        void *dst;
+        const uint8_t *src;
+        uint64_t n;
+    };
+    std::vector<Out> out;  // downloads to copy out at the next sync
+    hipEvent_t ev = nullptr;
+    bool pending = false;  // the pinned blocks and the event are kept until the process ends: no HIP
+                           // call from a destructor that may run after the runtime's own teardown
+
+    uint8_t *get(uint64_t n) {
+        n = (n + 63) & ~uint64_t(63);
+        if (blocks.empty() || used + n > blocks.back().second) {
+            const uint64_t size = std::max<uint64_t>({n, uint64_t(4) << 20, blocks.empty() ? 0 : 2 * blocks.back().second});
+            uint8_t *p = nullptr;
+            HIP_OK(hipHostMalloc(reinterpret_cast<void **>(&p), size, hipHostMallocDefault));
+            blocks.emplace_back(p, size);
+            used = 0;
+        }
+        uint8_t *p = blocks.back().first + used;
+        used += n;
+        return p;
+    }
+    void copied(hipStream_t s) {
+        if (!ev) HIP_OK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+        HIP_OK(hipEventRecord(ev, s));
+        pending = true;
+    }
+    void wait() {
+        if (pending) HIP_OK(hipEventSynchronize(ev));
+        pending = false;
+    }
+    // after the stream is synchronized: deliver the downloads, keep only the largest block
+    void finish() {
+        wait();
+        for (const Out &o : out) std::memcpy(o.dst, o.src, o.n);
+        out.clear();
+        restart();
+    }
+    // at the start of a call: whatever an interrupted call left is dropped, once no DMA can still use it
+    void abandon() {
+        if (pending) (void)hipEventSynchronize(ev);
+        pending = false;
+        out.clear();
+        restart();
+    }
+    void restart() {
+        while (blocks.size() > 1) {
+            (void)hipHostFree(blocks.front().first);
+            blocks.erase(blocks.begin());
+        }
+        used = 0;
+    }
+};
+thread_local PinnedStage t_stage;
+
 template <typename T>
 void h2d(T *dst, const T *src, uint64_t n, hipStream_t s) {
-    if (n) HIP_OK(hipMemcpyAsync(dst, src, n * sizeof(T), hipMemcpyHostToDevice, s));
+    if (!n) return;
+    uint8_t *p = t_stage.get(n * sizeof(T));
+    std::memcpy(p, src, n * sizeof(T));
+    HIP_OK(hipMemcpyAsync(dst, p, n * sizeof(T), hipMemcpyHostToDevice, s));
+    t_stage.copied(s);
 }
 template <typename T>
 void d2h(T *dst, const T *src, uint64_t n, hipStream_t s) {
-    if (n) HIP_OK(hipMemcpyAsync(dst, src, n * sizeof(T), hipMemcpyDeviceToHost, s));
+    if (!n) return;
+    uint8_t *p = t_stage.get(n * sizeof(T));
+    HIP_OK(hipMemcpyAsync(p, src, n * sizeof(T), hipMemcpyDeviceToHost, s));
+    t_stage.copied(s);
+    t_stage.out.push_back({dst, p, n * sizeof(T)});
 }
 template <typename T>
 void zero(T *dst, uint64_t n, hipStream_t s) {
     if (n) HIP_OK(hipMemsetAsync(dst, 0, n * sizeof(T), s));
 }
-void sync(hipStream_t s) { HIP_OK(hipStreamSynchronize(s)); }
+void sync(hipStream_t s) {
+    HIP_OK(hipStreamSynchronize(s));
+    t_stage.finish();
+}
 
 // Elements per slab: a multiple of kRow, at most 65536 (slab ranks and offsets are kept in 16 bits).
 uint32_t slab_size(int32_t slab) {
@@ -851,6 +926,7 @@ int32_t guarded(char *err, uint64_t errlen, F &&f) {
         if (err && errlen) std::snprintf(err, (size_t)errlen, "%s", m);
     };
     try {
+        t_stage.abandon();
         f();
         if (g_timing) timing_collect();
         return CRX_OK;
