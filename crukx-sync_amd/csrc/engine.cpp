@@ -540,11 +540,20 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
                   per_slab, rec_count, ovf, delta, full};
     launch_enc_rank(a, tiles, s);
     hc.mark("enc_setup");
+    // the scans and groups need only the counts, which are exact even when a slab's records overflowed
+    // their region; the overflow flag is read with the group totals, and on overflow the rank pass runs
+    // again into exact regions (rewriting the counts, so they are scanned again)
     unsigned int hovf1 = 0;
-    d2h(&hovf1, ovf, 1, s);
-    sync(s);
-    hc.mark("enc_wait_rank");
-    if (hovf1) {
+    unsigned long long gc[2];
+    for (int pass = 0;; ++pass) {
+        launch_scan_tables(d_descs, hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_all, s);
+        launch_scan_tables(d_descs, hchg, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_chg, s);
+        launch_enc_groups(tot_chg, T, d_groups, gbase, gcnt, s);
+        d2h(&hovf1, ovf, 1, s);
+        d2h(gc, gcnt, 2, s);
+        sync(s);
+        if (!hovf1) break;
+        if (pass) throw DeviceError("change records overflowed exact regions");
         unsigned long long *rec_base = ar.get<unsigned long long>(tiles + 1);
         launch_scan_u32(rec_count, tiles, rec_base, ar.get<unsigned long long>(scan_parts(tiles)), s);
         unsigned long long total = 0;
@@ -555,12 +564,6 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
         zero(ovf, 1, s);
         launch_enc_rank(a, tiles, s);
     }
-    launch_scan_tables(d_descs, hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_all, s);
-    launch_scan_tables(d_descs, hchg, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_chg, s);
-    launch_enc_groups(tot_chg, T, d_groups, gbase, gcnt, s);
-    unsigned long long gc[2];
-    d2h(gc, gcnt, 2, s);
-    sync(s);
     hc.mark("enc_wait_groups");
     const uint64_t G = gc[0], C = gc[1];
     E.total_changes = C;
