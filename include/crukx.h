@@ -15,8 +15,11 @@
  *     aligned, contiguous, with an element count.
  *   - Device memory: the library calls `alloc(alloc_ctx, nbytes)` for every device buffer it
  *     needs (the Python layer hands out torch caching-allocator tensors); the caller frees them
- *     after the call (encode: when the crx_encoded handle is freed).  Work runs on `stream`
- *     (a hipStream_t); the calls are synchronous with respect to the host on return.
+ *     after the call (encode: when the crx_encoded handle is freed).  A call usually asks for one
+ *     block sized from the previous call of its kind and carves its buffers from it.  Small
+ *     host<->device transfers use pinned host memory the library allocates per host thread and
+ *     keeps until the process ends.  Work runs on `stream` (a hipStream_t); the calls are
+ *     synchronous with respect to the host on return.
  *   - `slab` is the number of elements ranked by one wavefront (a multiple of 128, at most
  *     65536; 0 = default 65536).  It plays the role of codec._SLAB (codec.py:30): it changes
  *     how the work is cut, never the bytes.
