@@ -1330,6 +1330,9 @@ static_assert(kTgtCapSparse % 1024 == 0 && kTgtCapDense % 1024 == 0, "target lis
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u16x2 as16(uint32_t v) { return __builtin_bit_cast(u16x2, v); }
 
+// m with bit k (uniform) cleared, in one scalar instruction
+__device__ __forceinline__ void clear_bit(uint64_t &m, uint32_t k) { asm("s_bitset0_b64 %0, %1" : "+s"(m) : "s"(k)); }
+
 // (a & m) | b in one instruction (the mask from a scalar register)
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t b) {
     uint32_t r;
@@ -1420,7 +1423,7 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
             const uint32_t rr1 = add_bit(rr0, M0);
             const bool t0 = m0 && rr0 == qk, t1 = m1 && rr1 == qk;  // one element of the row
             if (t0 || t1) put(ck, r, t1 ? w1 : w0);
-            H &= H - 1;
+            clear_bit(H, k);
         } while (H);
         if (hit) {  // every exponent that had one: its next target, lane-parallel
             ++ci;
@@ -1460,7 +1463,7 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
                 nxt = tc;
                 ci = ck;
             }
-            H &= H - 1;
+            clear_bit(H, k);
         } while (H);
     });
     // every target of this window's exponents is found once its rank is passed: one still pending
