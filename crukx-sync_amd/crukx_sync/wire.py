@@ -287,8 +287,9 @@ def _parse_tensor(t, L, err):
     while True:
         # the leading bytes and the last byte, through pinned host memory
         host = torch.empty(have + 1, dtype=torch.uint8, pin_memory=True)
-        host[:have].copy_(t[:have])
-        host[have:].copy_(t[total - 1:])
+        host[:have].copy_(t[:have], non_blocking=True)
+        host[have:].copy_(t[total - 1:], non_blocking=True)
+        torch.cuda.current_stream(t.device).synchronize()  # one wait for both copies
         h = ctypes.c_void_p()
         need = ctypes.c_uint64()
         rc = L.crx_parse_prefix(ctypes.c_void_p(host.data_ptr()), have, total, int(host[have]), ctypes.byref(h),

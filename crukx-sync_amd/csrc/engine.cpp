@@ -1150,11 +1150,9 @@ int32_t crx_encoded_write(const crx_encoded *e, const char *const *names, const 
         const hipMemcpyKind from_dev = dst_on_device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
         const uint64_t off_bt = hdr.size(), off_pl = off_bt + 4 * e->n_blocks, off_pay = off_pl + pl.size();
         if (dst_on_device) {
-            // host bytes first, waited for (their buffers end with this call); the device-to-device
-            // copies are left ordered on the stream
-            HIP_OK(hipMemcpyAsync(dst, hdr.data(), hdr.size(), hipMemcpyHostToDevice, s));
-            HIP_OK(hipMemcpyAsync(dst + off_pl, pl.data(), pl.size(), hipMemcpyHostToDevice, s));
-            HIP_OK(hipStreamSynchronize(s));
+            // the host bytes go through the pinned arena: every copy is left ordered on the stream
+            h2d(dst, hdr.data(), hdr.size(), s);
+            h2d(dst + off_pl, pl.data(), pl.size(), s);
         } else {
             std::memcpy(dst, hdr.data(), hdr.size());
             std::memcpy(dst + off_pl, pl.data(), pl.size());

@@ -5,6 +5,7 @@
 #include <cmath>
 #include <cstring>
 #include <numeric>
+#include <string_view>
 #include <unordered_set>
 
 namespace crx {
@@ -32,6 +33,18 @@ struct Reader {
     }
     int u8() { return take(1)[0]; }
     uint64_t varint() {
+        const uint64_t lim = std::min(avail, total);
+        if (pos + 1 < lim) {  // one- and two-byte values, the common case
+            const uint64_t b0 = d[pos], b1 = d[pos + 1];
+            if (!(b0 & 0x80)) {
+                pos += 1;
+                return b0;
+            }
+            if (!(b1 & 0x80)) {
+                pos += 2;
+                return (b0 & 0x7F) | (b1 << 7);
+            }
+        }
         uint64_t v = 0;
         int shift = 0;
         for (;;) {
@@ -74,6 +87,27 @@ bool valid_utf8(const uint8_t *s, uint64_t n) {
         i += (uint64_t)len;
     }
     return true;
+}
+
+// The sum of n little-endian u32 (block table entries), and whether any is below `lo`: plain
+// loops the compiler vectorises.
+uint64_t sum_u32(const uint8_t *p, uint64_t n) {
+    uint64_t s = 0;
+    for (uint64_t k = 0; k < n; ++k) {
+        uint32_t v;
+        std::memcpy(&v, p + 4 * k, 4);
+        s += v;
+    }
+    return s;
+}
+bool any_below(const uint8_t *p, uint64_t n, uint32_t lo) {
+    uint32_t f = 0;
+    for (uint64_t k = 0; k < n; ++k) {
+        uint32_t v;
+        std::memcpy(&v, p + 4 * k, 4);
+        f |= v < lo;
+    }
+    return f != 0;
 }
 
 inline uint64_t sat_add(uint64_t a, uint64_t b, uint64_t cap) {  // the reference's ints do not wrap
@@ -145,14 +179,16 @@ void parse(const uint8_t *data, uint64_t avail, uint64_t total, uint8_t last, Up
     u.tensors.reserve(n_tensors);
     uint64_t total_blocks = 0, per_exp[256] = {};
     const uint64_t kCap = 1ULL << 63;
-    std::unordered_set<std::string> names;
+    std::unordered_set<std::string_view> names;  // views into the parsed bytes
+    names.reserve(std::min<uint64_t>(n_tensors, 1 << 16));
     for (uint64_t i = 0; i < n_tensors; ++i) {
         TensorHeader th;
         uint64_t name_len = r.varint();
         const uint8_t *name = r.take(name_len);
         if (!valid_utf8(name, name_len)) throw Corrupt("tensor name is not valid UTF-8");
         th.name.assign((const char *)name, name_len);
-        if (!names.insert(th.name).second) throw Corrupt("tensor '" + th.name + "' appears twice");
+        if (!names.insert(std::string_view((const char *)name, name_len)).second)
+            throw Corrupt("tensor '" + th.name + "' appears twice");
         th.numel = r.varint();
         const uint8_t *c = r.take(8);
         for (int k = 0; k < 8; ++k) th.checksum |= (uint64_t)c[k] << (8 * k);
@@ -194,13 +230,8 @@ void parse(const uint8_t *data, uint64_t avail, uint64_t total, uint8_t last, Up
         for (const Group &g : t.groups) {
             changes += g.count;
             const uint64_t nb = n_blocks(g.count), full = g.count / kBlock;
-            uint32_t least = 0xFFFFFFFFu;
-            for (uint64_t k = 0; k < full; ++k) {
-                const uint32_t v = u.block_bits(b + k);
-                total_bits += v;
-                least = std::min(least, v);
-            }
-            if (full && (uint64_t)least < (uint64_t)kBlock * (2 + g.rice)) short_block = true;
+            total_bits += sum_u32(u.block_table + 4 * b, full);
+            if (any_below(u.block_table + 4 * b, full, kBlock * (2 + (uint32_t)g.rice))) short_block = true;
             if (nb > full) {
                 const uint32_t v = u.block_bits(b + full);
                 total_bits += v;

@@ -1236,67 +1236,86 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
 // its first one (the select pass streams the slab once per window): windows of kSelWin exponents,
 // each starting at the lowest exponent with targets past the previous window.
 constexpr uint32_t kSelWin = 64;
-__global__ __launch_bounds__(64) void k_locate(SelectArgs a) {
+constexpr uint32_t kLocTiles = 2;  // slabs per wavefront: their searches share the lanes
+__global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
+    __shared__ uint4 arg[kLocTiles * 256];     // searches, packed: (target, next, group, slot = 256 u + exponent)
+    __shared__ uint32_t res[kLocTiles * 256];  // per slot: the first change at or past the slab (kNone: no group)
+    __shared__ uint8_t has[kLocTiles * 256];   // per slot: the slab holds at least one of its changes
     if (*a.bad) return;
-    const uint32_t tau = blockIdx.x, ln = lane();
-    const uint32_t t = a.tile_tensor[tau];
-    const bool last = tau + 1 >= a.descs[t].tile_begin + a.descs[t].n_tiles;
-    // exponents ln + 64 q: four lower-bound searches per lane, advanced together
-    int32_t g[4];
-    uint32_t lo[4], hi[4], end[4], vhi[4], target[4], next[4];
+    const uint32_t ln = lane();
+    // slab u of the wavefront, exponents ln + 64 q: those with a group are packed into consecutive
+    // entries, so that the lower-bound searches (one per lane) take as few load instructions as the
+    // slabs have groups
+    uint32_t n_act = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t k = ln + 64 * q;
-        g[q] = a.group_of[(uint64_t)t * 256 + k];
-        target[q] = a.pre[(uint64_t)tau * 256 + k];
-        next[q] = last ? kNone : a.pre[(uint64_t)(tau + 1) * 256 + k];
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        lo[q] = hi[q] = end[q] = 0;
-        vhi[q] = kNone;  // local[hi] once hi has moved
-        if (g[q] >= 0) {
-            const GroupDev gr = a.groups[g[q]];
-            lo[q] = gr.elem_base;
-            hi[q] = end[q] = gr.elem_base + gr.count;
-        }
-    }
-    for (;;) {
-        bool more = false;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) more |= lo[q] < hi[q];
-        if (!__any(more)) break;
+    for (uint32_t u = 0; u < kLocTiles; ++u) {
+        const uint32_t tau = blockIdx.x * kLocTiles + u;
+        if (tau >= tiles) break;
+        const uint32_t t = a.tile_tensor[tau];
+        const bool last = tau + 1 >= a.descs[t].tile_begin + a.descs[t].n_tiles;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            if (lo[q] < hi[q]) {
-                const uint32_t mid = lo[q] + ((hi[q] - lo[q]) >> 1), v = a.local[mid];
-                if (v < target[q]) {
-                    lo[q] = mid + 1;
+            const uint32_t k = ln + 64 * q;
+            const int32_t g = a.group_of[(uint64_t)t * 256 + k];
+            const uint32_t target = a.pre[(uint64_t)tau * 256 + k];
+            const uint32_t next = last ? kNone : a.pre[(uint64_t)(tau + 1) * 256 + k];
+            res[256 * u + k] = kNone;
+            has[256 * u + k] = 0;
+            const uint64_t m = ballot(g >= 0);
+            if (g >= 0) arg[n_act + mbcnt(m)] = make_uint4(target, next, (uint32_t)g, 256 * u + k);
+            n_act += (uint32_t)__popcll(m);
+        }
+    }
+    wave_fence();
+    for (uint32_t i0 = 0; i0 < n_act; i0 += 64) {
+        const bool on = i0 + ln < n_act;
+        uint4 x = make_uint4(0u, 0u, 0u, 0u);
+        uint32_t lo = 0, hi = 0, end = 0, vhi = kNone;  // vhi: local[hi] once hi has moved
+        if (on) {
+            x = arg[i0 + ln];
+            const GroupDev gr = a.groups[x.z];
+            lo = gr.elem_base;
+            hi = end = gr.elem_base + gr.count;
+        }
+        while (__any(lo < hi)) {
+            if (lo < hi) {
+                const uint32_t mid = lo + ((hi - lo) >> 1), v = a.local[mid];
+                if (v < x.x) {
+                    lo = mid + 1;
                 } else {
-                    hi[q] = mid;
-                    vhi[q] = v;
+                    hi = mid;
+                    vhi = v;
                 }
             }
         }
+        if (on) {  // x.y, the count before the next slab, is kNone for a tensor's last slab
+            res[x.w] = lo;
+            has[x.w] = lo < end && (x.y == kNone || vhi < x.y);
+        }
     }
-    uint64_t w[4];  // bit ln of w[q]: exponent ln + 64 q has targets in this slab
+    wave_fence();
+    for (uint32_t u = 0; u < kLocTiles; ++u) {
+        const uint32_t tau = blockIdx.x * kLocTiles + u;
+        if (tau >= tiles) break;
+        uint64_t w[4];  // bit ln of w[q]: exponent ln + 64 q has targets in this slab
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        ((uint32_t *)a.lb)[(uint64_t)tau * 256 + ln + 64 * q] = g[q] >= 0 ? lo[q] : kNone;
-        w[q] = ballot(g[q] >= 0 && lo[q] < end[q] && (last || vhi[q] < next[q]));
-    }
-    if (ln == 0) {  // windows greedy from the lowest exponent with targets
-        auto first_at = [&](uint32_t from) -> uint32_t {  // lowest set bit at or past `from` (256: none)
-            for (uint32_t q = from >> 6; q < 4; ++q) {
-                const uint64_t v = q == (from >> 6) ? w[q] & (~0ULL << (from & 63)) : w[q];
-                if (v) return 64 * q + (uint32_t)__builtin_ctzll(v);
+        for (int q = 0; q < 4; ++q) {
+            ((uint32_t *)a.lb)[(uint64_t)tau * 256 + ln + 64 * q] = res[256 * u + ln + 64 * q];
+            w[q] = ballot(has[256 * u + ln + 64 * q] != 0);
+        }
+        if (ln == 0) {  // windows greedy from the lowest exponent with targets
+            auto first_at = [&](uint32_t from) -> uint32_t {  // lowest set bit at or past `from` (256: none)
+                for (uint32_t q = from >> 6; q < 4; ++q) {
+                    const uint64_t v = q == (from >> 6) ? w[q] & (~0ULL << (from & 63)) : w[q];
+                    if (v) return 64 * q + (uint32_t)__builtin_ctzll(v);
+                }
+                return 256u;
+            };
+            uint32_t kb = first_at(0);
+            while (kb < 256 - kSelWin) {
+                kb = first_at(kb + kSelWin);
+                if (kb < 256) a.more[atomicAdd(a.n_more, 1u)] = make_uint2(tau, kb);
             }
-            return 256u;
-        };
-        uint32_t kb = first_at(0);
-        while (kb < 256 - kSelWin) {
-            kb = first_at(kb + kSelWin);
-            if (kb < 256) a.more[atomicAdd(a.n_more, 1u)] = make_uint2(tau, kb);
         }
     }
 }
@@ -1801,7 +1820,9 @@ void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
     CRX_LAUNCH("local_fix", k_local_fix, grid1(n_blocks, kBlocksPerWG), 256, s, a);
 }
 
-void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("locate", k_locate, tiles, 64, s, a); }
+void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s) {
+    CRX_LAUNCH("locate", k_locate, grid1(tiles, kLocTiles), 64, s, a, tiles);
+}
 
 void launch_select(const SelectArgs &a, uint32_t tiles, bool dense, hipStream_t s) {
     if (dense) {
