@@ -18,7 +18,9 @@
  *     after the call (encode: when the crx_encoded handle is freed).  A call usually asks for one
  *     block sized from the previous call of its kind and carves its buffers from it.  Small
  *     host<->device transfers use pinned host memory the library allocates per host thread and
- *     keeps until the process ends.  Work runs on `stream` (a hipStream_t); the calls are
+ *     keeps until the process ends.  Copies of an update's bytes between device memory and
+ *     pageable host memory go through 64 MiB of pinned buffers (allocated once per process) on up
+ *     to four threads that the call starts and joins.  Work runs on `stream` (a hipStream_t); the calls are
  *     synchronous with respect to the host on return.
  *   - `slab` is the number of elements ranked by one wavefront (a multiple of 128, at most
  *     65536; 0 = default 65536).  It plays the role of codec._SLAB (codec.py:30): it changes
