@@ -55,9 +55,18 @@ hipEvent_t take_event() {  // under g_tmu
     return hipEventCreate(&e) == hipSuccess ? e : nullptr;
 }
 
-void timing_collect() {
+// Adds the launches that have finished to the statistics; with `wait`, waits for all of them first
+// (a call may return with work still on its stream: apply's writes).
+void timing_collect(bool wait) {
     std::lock_guard<std::mutex> lk(g_tmu);
+    std::vector<Pending> running;
     for (Pending &p : g_pending) {
+        if (wait) {
+            (void)hipEventSynchronize(p.b);
+        } else if (hipEventQuery(p.b) == hipErrorNotReady) {
+            running.push_back(p);
+            continue;
+        }
         float ms = 0;
         if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
             g_stats[p.name].calls++;
@@ -66,7 +75,7 @@ void timing_collect() {
         g_free.push_back(p.a);
         g_free.push_back(p.b);
     }
-    g_pending.clear();
+    g_pending.swap(running);
 }
 }  // namespace
 
@@ -997,9 +1006,10 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     }
     if (hbad) throw Corrupt("payload positions outside their exponent groups");
     g_apply_hint.put(hint_key, ar.total);
+    // the verdict is final: the writes are left ordered on the stream, as an in-place torch op's
+    // would be (the reference's index_put_, codec.py:706, is not waited for either)
     launch_scatter(ba, B, s);
-    sync(s);
-    hc.mark("apply_wait_scatter");
+    hc.mark("apply_scatter");
     *changed = C;
 }
 
@@ -1025,11 +1035,11 @@ int32_t guarded(char *err, uint64_t errlen, F &&f) {
     try {
         t_stage.abandon();
         f();
-        if (g_timing) timing_collect();
+        if (g_timing) timing_collect(false);
         return CRX_OK;
     } catch (const Corrupt &e) {
         put(e.what());
-        if (g_timing) timing_collect();
+        if (g_timing) timing_collect(false);
         return CRX_CORRUPT;
     } catch (const Invalid &e) {
         put(e.what());
@@ -1354,13 +1364,13 @@ int32_t crx_rice_choose(uint64_t count, const int32_t cand[3], const uint64_t sh
 void crx_timing_enable(int32_t on) { g_timing = on != 0; }
 
 void crx_timing_reset(void) {
-    timing_collect();
+    timing_collect(true);
     std::lock_guard<std::mutex> lk(g_tmu);
     g_stats.clear();
 }
 
 int32_t crx_timing_read(char *buf, uint64_t len) {
-    timing_collect();
+    timing_collect(true);
     std::lock_guard<std::mutex> lk(g_tmu);
     std::string out;
     char line[256];

@@ -20,8 +20,12 @@
  *     host<->device transfers use pinned host memory the library allocates per host thread and
  *     keeps until the process ends.  Copies of an update's bytes between device memory and
  *     pageable host memory go through 64 MiB of pinned buffers (allocated once per process) on up
- *     to four threads that the call starts and joins.  Work runs on `stream` (a hipStream_t); the calls are
- *     synchronous with respect to the host on return.
+ *     to four threads that the call starts and joins.  Work runs on `stream` (a hipStream_t).
+ *     Results are final on return; crx_apply's writes (issued once the update has verified) and
+ *     crx_encoded_write's device copies are left ordered on `stream`, so the buffers `alloc`
+ *     handed out must stay usable by work already on `stream` after the call (a stream-ordered
+ *     allocator such as torch's caching allocator does this).  Everything else is complete on
+ *     return.
  *   - `slab` is the number of elements ranked by one wavefront (a multiple of 128, at most
  *     65536; 0 = default 65536).  It plays the role of codec._SLAB (codec.py:30): it changes
  *     how the work is cut, never the bytes.
@@ -95,7 +99,8 @@ uint64_t crx_update_total_changes(const crx_update *u);
  * computed from the weights).  `payload_dev` is NULL to upload the payload (and block table) from
  * the parsed host bytes, or the address of the payload inside a device-resident copy of the whole
  * update (the block table, which precedes the payload, is read from there too).  On any status but
- * CRX_OK nothing is written.
+ * CRX_OK nothing is written; on CRX_OK the writes are enqueued on `stream` (later work on it sees
+ * them).
  * `*changed` receives the number of changed elements. */
 int32_t crx_apply(const crx_update *u, const uint8_t *payload_dev, uint16_t *const *targets,
                   const uint64_t *numels, const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab,
