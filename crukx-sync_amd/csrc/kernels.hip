@@ -144,23 +144,25 @@ __device__ __forceinline__ Rsrc slab_rsrc(const uint32_t *frame, const Slab &s) 
 // with the next batch already in flight (double buffering keeps U..2U rows of loads outstanding
 // per wavefront while a batch is processed).  Every batch is whole: rows at or past nrows read as
 // zero and lie outside [f_lo, f_hi), so the body treats them as partial rows with no valid lane.
-// CPOL is the loads' cache policy: kStreamNT marks them non-temporal (the select pass measured
-// 5.08 -> 4.93 ms with it; the rank pass, which reads two streams, 6.55 -> 6.71 ms, so it keeps 0).
+// CPOL is the cache policy of the loads of the first stream, CPOL_LAST that of the last stream
+// (kStreamNT: non-temporal).  Measured: the select pass with non-temporal loads 5.08 -> 4.93 ms; the
+// rank pass 6.50 -> 6.18 ms with them on one of its two streams, 6.71 ms with them on both.
 constexpr int kStreamNT = 2;
-template <int U, int S, int CPOL = 0, typename Body>
+template <int U, int S, int CPOL = 0, int CPOL_LAST = CPOL, typename Body>
 __device__ __forceinline__ void stream_rows(const Slab &sl, const Rsrc (&src)[S], Body &&body) {
+    static_assert(S == 1 || S == 2, "one or two streams");
     const uint32_t lb = lane() * 4u;
     uint32_t cur[S][U], nxt[S][U];
+    auto load = [&](uint32_t(&dst)[S][U], uint32_t base) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int q = 0; q < S; ++q) cur[q][u] = __builtin_amdgcn_raw_buffer_load_b32(src[q], lb + u * 256u, 0, CPOL);
+        for (int u = 0; u < U; ++u) {
+            dst[0][u] = __builtin_amdgcn_raw_buffer_load_b32(src[0], base + u * 256u, 0, S == 1 ? CPOL_LAST : CPOL);
+            if (S == 2) dst[S - 1][u] = __builtin_amdgcn_raw_buffer_load_b32(src[S - 1], base + u * 256u, 0, CPOL_LAST);
+        }
+    };
+    load(cur, lb);
     for (uint32_t r0 = 0; r0 < sl.nrows; r0 += U) {
-        const uint32_t nb = (r0 + U) * 256u + lb;
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int q = 0; q < S; ++q) nxt[q][u] = __builtin_amdgcn_raw_buffer_load_b32(src[q], nb + u * 256u, 0, CPOL);
+        load(nxt, (r0 + U) * 256u + lb);
 #pragma unroll
         for (int u = 0; u < U; ++u) body(r0 + u, cur[0][u], cur[S - 1][u]);
 #pragma unroll
@@ -242,7 +244,7 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
     uint64_t written = 0;
     uint32_t cnt = 0;
     uint64_t dacc = 0, facc = 0;
-    stream_rows<kRankRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t nw) {
+    stream_rows<kRankRows, 2, 0, kStreamNT>(sl, src, [&](uint32_t r, uint32_t o, uint32_t nw) {
         // exponents; lanes outside the slab count into slot 256 and never change
         uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF, x = o ^ nw, n = nw;
         if (!row_full(sl, r)) {
@@ -1411,7 +1413,7 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
     };
     uint32_t prev = 0;  // exponent ln's count before the row
     const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
-    stream_rows<kSelectRows, 1, kStreamNT>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
+    stream_rows<kSelectRows, 1, kStreamNT, kStreamNT>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
         // window index << 7 of both elements (16-bit halves); outside the window or the slab: the spare
         u16x2 c = __builtin_elementwise_min(as16(o & 0x7F807F80u) - as16(kb), as16(sp));
         if (!row_full(sl, r)) {
