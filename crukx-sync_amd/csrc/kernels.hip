@@ -1039,21 +1039,25 @@ __global__ __launch_bounds__(256) void k_checksum(const uint32_t *frame, uint32_
 // checked against those by k_local_fix), so it can run beside the exponent-count pass.  Each lane
 // keeps kDecBuf decoded changes in registers and stores them together: storing one change at a time
 // left each lane's output lines half-written in L2, and they reached HBM several times over.
-constexpr uint32_t kDecPayWords = 3584;  // 28 KiB of payload per wavefront; more is read from HBM
 constexpr uint32_t kDecBuf = 8;          // changes decoded per lane between stores
 
+// The decoder's LDS, sized per launch (decode_lds_bytes): the wavefront's payload words, then the
+// symbols.  Sizing it to the update's widest wavefront rather than the largest allowed lets more
+// wavefronts share a CU (1% updates: 23 instead of 36 KiB, 6 instead of 4 per CU).
 struct DecodeLds {
-    uint64_t pay[kDecPayWords];
-    uint32_t syms[kDecSyms];
+    uint64_t *pay;
+    uint32_t *syms;
+    uint32_t pay_words;
 };
 
 // 64 bits of the stream from bit `pos`: LDS words [w0, ...) when staged, else HBM.
 template <bool LDS>
-__device__ __forceinline__ uint64_t bits64(const DecodeArgs &a, const uint64_t *W, uint64_t w0, uint64_t pos) {
+__device__ __forceinline__ uint64_t bits64(const DecodeArgs &a, const DecodeLds &S, uint64_t w0, uint64_t pos) {
     const uint32_t s = (uint32_t)(pos & 63);
     uint64_t hi, lo;
     if (LDS) {
-        const uint32_t w = (uint32_t)min64((pos >> 6) - w0, kDecPayWords - 2);
+        const uint64_t *W = S.pay;
+        const uint32_t w = (uint32_t)min64((pos >> 6) - w0, S.pay_words - 2);
         hi = W[w];
         lo = W[w + 1];
     } else {
@@ -1065,7 +1069,7 @@ __device__ __forceinline__ uint64_t bits64(const DecodeArgs &a, const uint64_t *
 }
 
 template <bool LDS_PAY, bool LDS_SYMS>
-__device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
+__device__ void decode_blocks(const DecodeArgs &a, const DecodeLds &S, uint64_t w0) {
     const uint32_t ln = lane();
     const uint64_t b = (uint64_t)blockIdx.x * 64 + ln;
     if (b >= a.n_blocks) return;
@@ -1091,7 +1095,7 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
     uint64_t rel = 0;  // sum of (gap + 1) so far in this block
     // decodes change s of the block into out: zz | (block-relative local << 32); false once bad
     auto step = [&](uint32_t s, unsigned long long &out) {
-        uint64_t x = bits64<LDS_PAY>(a, S.pay, w0, cur);
+        uint64_t x = bits64<LDS_PAY>(a, S, w0, cur);
         uint64_t q;
         if (~x) {  // the unary run ends inside this window
             q = (uint64_t)__builtin_clzll(~x);
@@ -1099,7 +1103,7 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
             q = 64;
             for (;;) {
                 if (q > qmax || cur + q >= end) break;
-                const uint64_t y = ~bits64<LDS_PAY>(a, S.pay, w0, cur + q);
+                const uint64_t y = ~bits64<LDS_PAY>(a, S, w0, cur + q);
                 if (y) {
                     q += (uint64_t)__builtin_clzll(y);
                     break;
@@ -1110,7 +1114,7 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
         const uint64_t c = cur + q + 1;
         // remainder and Huffman peek: from the same window when they fit in it, else a new read
         if (q + 1 + rice + 17 <= 64) x <<= (q + 1);
-        else x = bits64<LDS_PAY>(a, S.pay, w0, c);
+        else x = bits64<LDS_PAY>(a, S, w0, c);
         const uint64_t rem = rice ? x >> (64 - rice) : 0ULL;
         const uint32_t peek = (uint32_t)((x << rice) >> (64 - 17));
         // code length: 1 + #{l : lim[l] <= peek} (lim is non-decreasing), summed as a tree; then the
@@ -1167,14 +1171,15 @@ __device__ void decode_blocks(const DecodeArgs &a, DecodeLds &S, uint64_t w0) {
 
 template <bool LDS_SYMS>
 __global__ __launch_bounds__(64) void k_decode(DecodeArgs a) {
-    __shared__ __attribute__((aligned(16))) DecodeLds S;
+    extern __shared__ __attribute__((aligned(16))) uint64_t dyn_lds[];
+    const DecodeLds S{dyn_lds, reinterpret_cast<uint32_t *>(dyn_lds + a.lds_pay_words), a.lds_pay_words};
     const uint32_t ln = lane();
     const uint64_t b0 = (uint64_t)blockIdx.x * 64;
     const uint64_t nb = min64(64, a.n_blocks - b0);
     // this wavefront's bits [block_off[b0], block_off[b0 + nb]) lie in words [w0, wend)
     const uint64_t w0 = a.block_off[b0] >> 6;
     const uint64_t wend = min64(a.n_words, ((a.block_off[b0 + nb] + 63) >> 6) + 2);
-    const bool lds_pay = wend > w0 && wend - w0 <= kDecPayWords;
+    const bool lds_pay = wend > w0 && wend - w0 <= a.lds_pay_words;
     if (lds_pay)
         for (uint64_t w = w0 + ln; w < wend; w += 64) S.pay[w - w0] = __builtin_bswap64(a.payload[w]);
     if (LDS_SYMS)
@@ -1817,8 +1822,12 @@ void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint6
 }
 
 void launch_decode(const DecodeArgs &a, hipStream_t s) {
-    if (a.n_syms <= kDecSyms) CRX_LAUNCH("decode", k_decode<true>, grid1(a.n_blocks, 64), 64, s, a);
-    else CRX_LAUNCH("decode", k_decode<false>, grid1(a.n_blocks, 64), 64, s, a);
+    const uint32_t grid = grid1(a.n_blocks, 64), lds = decode_lds_bytes(a.lds_pay_words, a.n_syms);
+    if (!grid) return;
+    timing_begin(s);
+    if (a.n_syms <= kDecSyms) hipLaunchKernelGGL(k_decode<true>, dim3(grid), dim3(64), lds, s, a);
+    else hipLaunchKernelGGL(k_decode<false>, dim3(grid), dim3(64), lds, s, a);
+    timing_end("decode", s);
 }
 
 void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
