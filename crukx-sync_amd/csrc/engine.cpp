@@ -977,7 +977,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     fork.join();
     hc.mark("apply_pass_a");
 
-    BlockArgs ba{d_groups, (uint32_t)G, slab, binfo, d_descs, sizes, blk_prefix, local, dz, pv, bdelta, bad, B};
+    BlockArgs ba{d_groups, (uint32_t)G, slab, binfo, d_descs, sizes, blk_prefix, local, dz, pv, bdelta, bad, B, nullptr};
     launch_local_fix(ba, B, s);
     uint2 *more = ar.get<uint2>(3 * (uint64_t)tiles);  // at most 3 windows after the first per slab
     unsigned int *n_more = ar.get<unsigned int>(1);
@@ -988,6 +988,22 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     launch_select(sa, tiles, C > kSelectDenseTargets * tiles, s);
     launch_verify(ba, B, s);
     launch_range_sums(bdelta, tblk, T, tdelta, s);
+    // the verdict on the device too, and the scatter behind it: it writes only if the update verifies,
+    // and the host waits for the verdict's data, not for the writes
+    std::vector<uint64_t> want(T), cached(T, 0);
+    std::vector<int32_t> has(T, 0);
+    for (uint32_t t = 0; t < T; ++t) {
+        want[t] = u.tensors[t].checksum;
+        has[t] = (has_cache && has_cache[t]) ? 1 : 0;
+        if (has[t]) cached[t] = cache_vals[t];
+    }
+    uint64_t *d_want = ar.get<uint64_t>(T), *d_cached = ar.get<uint64_t>(T);
+    int32_t *d_has = ar.get<int32_t>(T);
+    unsigned int *ok = ar.get<unsigned int>(1);
+    h2d(d_want, want.data(), T, s);
+    h2d(d_cached, cached.data(), T, s);
+    h2d(d_has, has.data(), T, s);
+    launch_verdict(T, tdelta, t_full, d_has, d_cached, d_want, bad, ok, s);
     hc.mark("apply_launch");
 
     unsigned int hbad = 0;
@@ -996,7 +1012,9 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     d2h(&hbad, bad, 1, s);
     d2h(hdelta.data(), tdelta, T, s);
     d2h(hfull.data(), t_full, T, s);
-    sync(s);
+    ba.ok = ok;
+    launch_scatter(ba, B, s);
+    t_stage.finish();  // the downloads above (enqueued before the scatter) have arrived
     hc.mark("apply_wait_verify");
     // the reference's verdict (codec.py:598-604,696-712): the group-size check first, then any
     // checksum mismatch (naming up to three tensors), then any other inconsistency
@@ -1015,8 +1033,6 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     g_apply_hint.put(hint_key, ar.total);
     // the verdict is final: the writes are left ordered on the stream, as an in-place torch op's
     // would be (the reference's index_put_, codec.py:706, is not waited for either)
-    launch_scatter(ba, B, s);
-    hc.mark("apply_scatter");
     *changed = C;
 }
 

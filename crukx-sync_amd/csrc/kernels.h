@@ -168,6 +168,7 @@ struct BlockArgs {                  // per-block kernels over the change list (o
     unsigned long long *bdelta;     // [blocks] checksum delta of each block's changes
     unsigned int *bad;
     uint64_t n_blocks;
+    const unsigned int *ok;         // k_scatter writes only when *ok: the device's verdict (k_verdict)
 };
 
 void launch_enc_rank(const EncRankArgs &a, uint32_t tiles, hipStream_t s);
@@ -198,6 +199,11 @@ void launch_scan_u64(const unsigned long long *in, uint64_t n, unsigned long lon
                      hipStream_t s);
 void launch_scan_u32(const uint32_t *in, uint64_t n, unsigned long long *out, unsigned long long *part, hipStream_t s);
 // out[t] = sum of v[begin[t] .. begin[t + 1])
+// ok = 1 iff *bad is 0 and every tensor's old checksum (cached[t] where has[t], else full[t]) plus
+// its delta equals want[t]; 0 otherwise.  One workgroup.
+void launch_verdict(uint32_t n, const unsigned long long *delta, const uint64_t *full, const int32_t *has,
+                    const uint64_t *cached, const uint64_t *want, const unsigned int *bad, unsigned int *ok,
+                    hipStream_t s);
 void launch_range_sums(const unsigned long long *v, const uint32_t *begin, uint32_t n, unsigned long long *out,
                        hipStream_t s);
 void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint64_t *per_tile, uint64_t *out,

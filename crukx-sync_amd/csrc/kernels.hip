@@ -1709,9 +1709,26 @@ __global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
     if (ln == 0 && b < a.n_blocks) a.bdelta[b] = t;
 }
 
+// The host's verdict (codec.py:598-604,696-712), computed on the device as well so that the scatter
+// can follow it without a host round trip; the host still raises the errors from the same data.
+__global__ __launch_bounds__(256) void k_verdict(uint32_t n, const unsigned long long *delta, const uint64_t *full,
+                                                 const int32_t *has, const uint64_t *cached, const uint64_t *want,
+                                                 const unsigned int *bad, unsigned int *ok) {
+    __shared__ unsigned int miss;
+    if (threadIdx.x == 0) miss = 0;
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t < n; t += 256) {
+        const uint64_t old = has[t] ? cached[t] : full[t];
+        if (old + delta[t] != want[t]) atomicOr(&miss, 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) *ok = (miss == 0 && *bad == 0) ? 1u : 0u;
+}
+
 // One workgroup per block: the stores are bound by HBM partial writes, and more blocks per workgroup
-// measured slower.
+// measured slower.  Nothing is written unless the device's verdict is ok.
 __global__ __launch_bounds__(256) void k_scatter(BlockArgs a) {
+    if (!*a.ok) return;
     const BlockInfo r = block_info(a, blockIdx.x);
     const uint32_t s = threadIdx.x;
     if (s < r.cnt) {
@@ -1809,6 +1826,14 @@ void launch_scan_u64(const unsigned long long *in, uint64_t n, unsigned long lon
 
 void launch_scan_u32(const uint32_t *in, uint64_t n, unsigned long long *out, unsigned long long *part, hipStream_t s) {
     launch_scan("scan_u32", in, n, out, part, s);
+}
+
+void launch_verdict(uint32_t n, const unsigned long long *delta, const uint64_t *full, const int32_t *has,
+                    const uint64_t *cached, const uint64_t *want, const unsigned int *bad, unsigned int *ok,
+                    hipStream_t s) {
+    timing_begin(s);
+    hipLaunchKernelGGL(k_verdict, dim3(1), dim3(256), 0, s, n, delta, full, has, cached, want, bad, ok);
+    timing_end("verdict", s);
 }
 
 void launch_range_sums(const unsigned long long *v, const uint32_t *begin, uint32_t n, unsigned long long *out,
