@@ -21,7 +21,7 @@
  *     keeps until the process ends.  Copies of an update's bytes between device memory and
  *     pageable host memory go through 64 MiB of pinned buffers (allocated once per process) on up
  *     to four threads that the call starts and joins.  Work runs on `stream` (a hipStream_t).
- *     Results are final on return; crx_apply's writes (issued once the update has verified) and
+ *     Results are final on return; crx_apply's writes (gated on the device by the verdict) and
  *     crx_encoded_write's device copies are left ordered on `stream`, so the buffers `alloc`
  *     handed out must stay usable by work already on `stream` after the call (a stream-ordered
  *     allocator such as torch's caching allocator does this).  Everything else is complete on
