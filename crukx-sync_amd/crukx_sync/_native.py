@@ -65,6 +65,7 @@ SIGNATURES = {
     "crx_encoded_payload": (_i32, [_vp, _vp, _vp]),
     "crx_encoded_free": (None, [_vp]),
     "crx_checksum": (_i32, [_vp, _u64, _vp, ALLOC_FN, _vp, _u64p, _cp, _u64]),
+    "crx_checksum_noalloc": (_i32, [_vp, _u64, _vp, _u64p, _cp, _u64]),
     "crx_huffman_lengths": (_i32, [_vp, _i64, _vp]),
     "crx_canonical_codes": (_i32, [_vp, _i64, _vp]),
     "crx_rice_candidates": (None, [_u64, _u64, _vp]),

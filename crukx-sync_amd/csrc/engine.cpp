@@ -1351,6 +1351,24 @@ int32_t crx_checksum(const uint16_t *data, uint64_t n, void *stream, crx_alloc_f
     });
 }
 
+int32_t crx_checksum_noalloc(const uint16_t *data, uint64_t n, void *stream, uint64_t *out, char *err,
+                             uint64_t errlen) {
+    // no exceptions, containers or pinned staging here: nothing on this path allocates
+    *out = 0;
+    auto fail = [&](int32_t rc, const char *m) {
+        if (err && errlen) std::snprintf(err, (size_t)errlen, "%s", m);
+        return rc;
+    };
+    if (!n) return CRX_OK;
+    if (reinterpret_cast<uintptr_t>(data) & 1) return fail(CRX_INVALID, "tensor data must be 2-byte aligned");
+    if (n >= (1ULL << 32)) return fail(CRX_INVALID, "crx_checksum_noalloc takes at most 2^32 - 1 elements");
+    const uint32_t *frame = reinterpret_cast<const uint32_t *>(reinterpret_cast<uintptr_t>(data) & ~uintptr_t(3));
+    const uint32_t lead = (uint32_t)((reinterpret_cast<uintptr_t>(data) & 3) >> 1);
+    const hipError_t e = checksum_noalloc(frame, lead, n, (hipStream_t)stream, out);
+    if (e != hipSuccess) return fail(CRX_DEVICE, hipGetErrorString(e));
+    return CRX_OK;
+}
+
 int32_t crx_huffman_lengths(const uint64_t *counts, int64_t n, int32_t *lengths) {
     if (n <= 0) return CRX_INVALID;
     try {

@@ -226,6 +226,10 @@ void launch_verify(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
 void launch_scatter(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
 void launch_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial, uint32_t n_parts,
                      hipStream_t s);
+// The full checksum of n 16-bit elements (frame words, lead as in TensorDesc) into *out (host
+// memory), through a static per-device scratch array: no device or host allocation.  Waits for the
+// stream.  Not timed by crx_timing (no events are created).
+hipError_t checksum_noalloc(const uint32_t *frame, uint32_t lead, uint64_t n, hipStream_t s, uint64_t *out);
 
 // Host-side timing of launches (events on the launch stream), enabled by crx_timing_enable.
 void timing_begin(hipStream_t s);

@@ -8,6 +8,9 @@
 // histograms are scanned per tensor afterwards, so a slab's ranks become tensor-wide ranks.
 #include "kernels.h"
 
+#include <algorithm>
+#include <mutex>
+
 namespace crx {
 namespace {
 
@@ -1010,7 +1013,7 @@ __global__ __launch_bounds__(256) void k_range_sums(const unsigned long long *v,
     if (threadIdx.x == 0) out[blockIdx.x] = total;
 }
 
-// Full checksum of one tensor: each workgroup sums a contiguous range.
+// Full checksum of one tensor: each workgroup sums a contiguous range into partial[blockIdx.x].
 __global__ __launch_bounds__(256) void k_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial,
                                                   uint32_t n_parts) {
     __shared__ unsigned long long sh[256];
@@ -1027,6 +1030,16 @@ __global__ __launch_bounds__(256) void k_checksum(const uint32_t *frame, uint32_
     unsigned long long total;
     block_exclusive_sum(s, sh, &total);
     if (threadIdx.x == 0) partial[blockIdx.x] = total;
+}
+
+// One workgroup: *out = part[0] + ... + part[n - 1] (mod 2^64).
+__global__ __launch_bounds__(256) void k_sum_parts(const unsigned long long *part, uint32_t n, unsigned long long *out) {
+    __shared__ unsigned long long sh[4];
+    unsigned long long s = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += 256) s += part[i];
+    unsigned long long total;
+    block_exclusive_sum(s, sh, &total);
+    if (threadIdx.x == 0) *out = total;
 }
 
 // ================================================================== apply: block decode
@@ -1884,6 +1897,52 @@ void launch_scatter(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
 void launch_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial, uint32_t n_parts,
                      hipStream_t s) {
     CRX_LAUNCH("checksum", k_checksum, n_parts, 256, s, frame, lead, n, partial, n_parts);
+}
+
+// ================================================================== allocation-free checksum
+// The scratch memory of checksum_noalloc: k_checksum's partial sums and their total, in a static
+// device array (each device holds its own copy until the process ends) instead of memory from the
+// caller's allocator.  Every call overwrites what it reads, so nothing needs clearing between calls;
+// calls that overlap on one device share the array and race.
+constexpr uint32_t kNoAllocParts = 2048;
+static __device__ __align__(256) unsigned long long scratch[kNoAllocParts + 1];
+
+// The array's device address on the current device, looked up once per device with that device
+// current.  In host code `scratch` names a host-side stand-in, not device memory: kernels and copies
+// are given this address instead.
+static hipError_t scratch_address(unsigned long long **out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static unsigned long long *addr[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!addr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        addr[dev] = static_cast<unsigned long long *>(p);
+    }
+    *out = addr[dev];
+    return hipSuccess;
+}
+
+hipError_t checksum_noalloc(const uint32_t *frame, uint32_t lead, uint64_t n, hipStream_t s, uint64_t *out) {
+    unsigned long long *sc = nullptr;
+    hipError_t e = scratch_address(&sc);
+    if (e != hipSuccess) return e;
+    const uint64_t words = (n + lead + 1) >> 1;
+    const uint32_t parts = (uint32_t)std::min<uint64_t>(kNoAllocParts, (words + 65535) / 65536);
+    hipLaunchKernelGGL(k_checksum, dim3(parts), dim3(256), 0, s, frame, lead, n, reinterpret_cast<uint64_t *>(sc),
+                       parts);
+    hipLaunchKernelGGL(k_sum_parts, dim3(1), dim3(256), 0, s, sc, parts, sc + kNoAllocParts);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = hipMemcpyAsync(out, sc + kNoAllocParts, sizeof(uint64_t), hipMemcpyDeviceToHost, s);
+    if (e != hipSuccess) return e;
+    return hipStreamSynchronize(s);
 }
 
 }  // namespace crx

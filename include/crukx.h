@@ -166,6 +166,15 @@ void crx_encoded_free(crx_encoded *e);
  * over n 16-bit patterns, as a deterministic device reduction. */
 int32_t crx_checksum(const uint16_t *data, uint64_t n, void *stream, crx_alloc_fn alloc, void *alloc_ctx,
                      uint64_t *out, char *err, uint64_t errlen);
+/* crx_checksum without any allocation: no counterpart in the reference.  For callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * per-workgroup partial sums live in a static device array of 2049 u64 (16 KiB per device, held
+ * until the process ends) instead of memory from an allocator, and the result goes to *out (host
+ * memory) through a plain copy; the call waits for `stream`.  n must be below 2^32 (as for
+ * crx_checksum; CRX_INVALID otherwise).  Calls that overlap on one device share that array and
+ * race: serialize them. */
+int32_t crx_checksum_noalloc(const uint16_t *data, uint64_t n, void *stream, uint64_t *out, char *err,
+                             uint64_t errlen);
 
 /* ------------------------------------------------------------------ host helpers
  * codec.huffman_lengths (codec.py:71-98): code lengths limited to 17 bits. */
