@@ -5,6 +5,7 @@ size-independent properties are checked:
 - every chained step applies exactly (receiver == sender's new state, bit for bit);
 - sender cache == receiver cache, and cached checksums equal a full recomputation;
 - the change-density / step-size sweep (rho in {0.5, 1, 2, 3}%, P(|k| = 1) in {0.95, 0.87, 0.70});
+- the 7B shape at rho = 1% and 2% over two chained steps;
 - 32B shape with edge values (+-0, subnormals, +-max-finite) injected at 1e-4 density and smaller
   slabs: single-byte corruptions across the header, the block table and the payload either raise
   with the receiver unchanged or (if the flip happens to be harmless) apply exactly.
@@ -86,19 +87,22 @@ def test_qwen25_1_5b_density_and_step_size_sweep(rho):
         del cur
 
 
-def test_qwen25_7b_two_percent_chained():
-    """The 7B shape at rho = 2% (the 1% case runs in the benchmark), device-resident bytes."""
+@pytest.mark.parametrize("rho", [0.01, 0.02])
+def test_qwen25_7b_chained(rho):
+    """The 7B shape (the benchmark's workload at rho = 1%, and at 2%), two chained steps with both
+    caches, device-resident bytes."""
     shapes = workloads.qwen25_shapes("qwen2.5-7b")
     assert workloads.numel(shapes) == 7_615_616_512 and len(shapes) == 339
     prev = workloads.make_weights(shapes, seed=0, device="cuda")
     recv = {k: v.clone() for k, v in prev.items()}
     send, rc = {}, {}
     for s in range(1, 3):
-        cur = workloads.make_step(prev, s, rho=0.02)
+        cur = workloads.make_step(prev, s, rho=rho)
         buf = crukx_sync.encode_update_device(prev, cur, send)
         stats = crukx_sync.apply_update(recv, buf, rc)
         assert _equal(recv, cur), s
-        _say(f"7b 2% step {s}: {stats.changed} changes, {buf.numel()} bytes")
+        assert abs(stats.changed / workloads.numel(shapes) - rho) < 0.02 * rho
+        _say(f"7b rho {rho} step {s}: {stats.changed} changes, {buf.numel()} bytes")
         del prev
         prev = cur
     assert send == {k: v[0] for k, v in rc.items()}
