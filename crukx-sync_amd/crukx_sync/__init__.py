@@ -1,19 +1,20 @@
-"""crukx-sync on MI355X: exact, compact bf16 weight updates for RL weight sync.
+"""crukx-sync on MI355X: the exact, compact bf16 weight-update codec, computed in gfx950 kernels.
 
-    update = encode_update(prev, cur)   # trainer: dicts of name -> bf16 torch tensors
-    apply_update(weights, update)       # worker: writes the new values into `weights` in place
+    update = encode_update(prev, cur)   # trainer side: name -> bf16 tensor mappings in, bytes out
+    apply_update(weights, update)       # worker side: the new values land in `weights`, in place
 
-Same public API, wire format (version 2) and all-or-nothing semantics as the reference
-(Crukx-dev/crukx-sync, src/crukx_sync/__init__.py): nothing is written unless the whole update
-decodes and every tensor's checksum verifies. The work runs in hand-written gfx950 kernels.
+The names, arguments, errors, wire format (version 2) and all-or-nothing rule are those of the
+reference (Crukx-dev/crukx-sync, src/crukx_sync/__init__.py): an update either decodes and matches
+every tensor's checksum, or it raises and the weights keep their old values.
 
-For per-step sync, pass a `checksums` dict on each side and keep it between steps: checksums are
-then updated from the changed elements only instead of re-reading every tensor.
-- Sender: a wrong cache produces an update the receiver rejects (CorruptUpdate), never wrong weights.
-- Receiver: a cached checksum is used only while the tensor's `_version` is unchanged since this
-  library last wrote it; any PyTorch in-place op bumps it and forces a full re-check. Writes that
-  bypass PyTorch's version counter (raw pointers, some collective libraries) are not detected, so
-  drop the receiver cache if weights can change that way.
+Checksum caches (optional, one dict per side, kept by the caller from one update to the next):
+- With a cache the sender derives each new checksum from the old one plus the changed elements, and
+  the receiver checks against a cached value instead of reading all of its weights again.
+- A stale or wrong sender cache cannot corrupt a receiver: the update it yields fails to verify.
+- The receiver trusts an entry only while the tensor's PyTorch `_version` equals the one recorded
+  after this library's own write. In-place PyTorch ops move `_version`, so they are noticed; writes
+  that go around PyTorch (raw device pointers, some communication libraries) are not, and callers
+  that update weights that way should start from an empty receiver cache.
 
 Device-resident variant (no host round trip of the bytes): `encode_update_device` returns the same
 bytes as a uint8 tensor on the GPU, and `apply_update` accepts such a tensor.

@@ -12,6 +12,7 @@ device (there is no CPU implementation in the product, and without a HIP device 
 from __future__ import annotations
 
 import ctypes
+import threading
 import weakref
 from collections.abc import Mapping
 
@@ -286,19 +287,29 @@ def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
 # address).  They are used only with the same slab size and a checksum-cache hit for the tensor (the
 # same trust rule), and let apply skip its full read of those weights (crx_apply_cached).
 _hist = {}
+# Guards _hist across threads.  Reentrant: a weakref callback that drops an entry can run inside a
+# locked region when a garbage collection happens there.
+_hist_lock = threading.RLock()
 
 
 def _hist_lookup(t):
-    e = _hist.get(id(t))
+    with _hist_lock:
+        e = _hist.get(id(t))
     if e is None or e[0]() is not t:
         return None
     return e
 
 
+def _hist_forget(key):
+    with _hist_lock:
+        _hist.pop(key, None)
+
+
 def _hist_store(t, buf, slab, dev):
+    """Record counts for t (the caller holds _hist_lock)."""
     key = id(t)
     e = _hist.get(key)
-    ref = e[0] if e is not None and e[0]() is t else weakref.ref(t, lambda _r, key=key: _hist.pop(key, None))
+    ref = e[0] if e is not None and e[0]() is t else weakref.ref(t, lambda _r, key=key: _hist_forget(key))
     _hist[key] = (ref, t._version, buf, slab, dev, buf.data_ptr())
 
 
@@ -371,9 +382,9 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     hist_in, hist_out, bufs = [], [], []
     if keep:
         fresh = []  # tensors without usable counts: one allocation, sliced per tensor
-        hg = _hist.get
-        for i, (a, c, v) in enumerate(zip(targets, cache, vers)):
-            e = hg(id(a)) if c is not None else None
+        with _hist_lock:
+            found = [_hist.get(id(a)) if c is not None else None for a, c in zip(targets, cache)]
+        for i, (a, e, v) in enumerate(zip(targets, found, vers)):
             if e is not None and e[0]() is a and e[1] == v and e[3] == slab and e[4] == dev:
                 bufs.append(e[2])
                 hist_in.append(e[5])
@@ -400,8 +411,13 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     ws.check()
     ws.release()
     if rc != _native.OK:
-        for a in targets:  # their counts may be half-updated
-            _hist.pop(id(a), None)
+        with _hist_lock:
+            for a in targets:  # their counts may be half-updated
+                _hist.pop(id(a), None)
+        if rc == _native.DEVICE and staged is targets:
+            # a runtime error may come after the verified writes were enqueued: the weights may have
+            # changed, so cached checksums of them must no longer be trusted (a new _version does that)
+            torch.autograd.graph.increment_version(targets)
     _native.raise_for(rc, err)
     if staged is targets:
         torch.autograd.graph.increment_version(targets)  # in place, like index_put_: bumps _version
@@ -409,8 +425,9 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
         for a, s in zip(targets, staged):
             a.copy_(s)  # an in-place op: bumps the tensor's version
     if keep:
-        for a, buf in zip(targets, bufs):
-            _hist_store(a, buf, slab, dev)
+        with _hist_lock:
+            for a, buf in zip(targets, bufs):
+                _hist_store(a, buf, slab, dev)
     if checksums is not None:  # record the version after our own write
         checksums.update({name: (c, t._version) for name, c, t in zip(names, header_chk, targets)})
     return changed.value

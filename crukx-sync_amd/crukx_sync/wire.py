@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import struct
+import threading
 from dataclasses import dataclass, field
 
 MAGIC = b"CRXS"
@@ -270,7 +271,9 @@ def parse(data) -> ParsedUpdate:
     return ParsedUpdate(h.value, buf)
 
 
-_prefix_hint = [0]
+# header bytes the last device-resident parse of this thread needed (updates of a run have headers of
+# about the same size): a hint, kept per thread so concurrent callers do not share it
+_prefix_hint = threading.local()
 
 
 def _parse_tensor(t, L, err):
@@ -283,7 +286,7 @@ def _parse_tensor(t, L, err):
     total = t.numel()
     if total == 0:
         return parse(b"")
-    have = min(total, max(1 << 16, _prefix_hint[0]))
+    have = min(total, max(1 << 16, getattr(_prefix_hint, "n", 0)))
     while True:
         # the leading bytes and the last byte, through pinned host memory
         host = torch.empty(have + 1, dtype=torch.uint8, pin_memory=True)
@@ -298,5 +301,5 @@ def _parse_tensor(t, L, err):
             have = min(total, max(need.value + 64, 2 * have))
             continue
         _native.raise_for(rc, err)
-        _prefix_hint[0] = have  # updates of a run have headers of about the same size
+        _prefix_hint.n = have
         return ParsedUpdate(h.value, host, dev_bytes=t)

@@ -115,16 +115,17 @@ struct HostClock {
 };
 
 // ------------------------------------------------------------------ auxiliary stream
-// One extra stream per device (default priority, created on first use, kept for the process) for
-// work of a call that can overlap the caller's stream.  A Fork makes it wait for everything enqueued
-// on the caller's stream so far; join() makes the caller's stream wait for what was enqueued on it.
-hipStream_t aux_stream() {
+// One extra stream per device and caller stream (default priority, created on first use, kept for
+// the process) for work of a call that can overlap the caller's stream: calls on different caller
+// streams never wait for each other through it.  A Fork makes it wait for everything enqueued on the
+// caller's stream so far; join() makes the caller's stream wait for what was enqueued on it.
+hipStream_t aux_stream(hipStream_t caller) {
     static std::mutex mu;
-    static std::map<int, hipStream_t> streams;
+    static std::map<std::pair<int, hipStream_t>, hipStream_t> streams;
     int dev = 0;
     HIP_OK(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lk(mu);
-    hipStream_t &st = streams[dev];
+    hipStream_t &st = streams[{dev, caller}];
     if (!st) HIP_OK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
     return st;
 }
@@ -133,7 +134,7 @@ struct Fork {
     hipStream_t main, aux;
     hipEvent_t ev[2] = {nullptr, nullptr};
     bool joined = false;
-    explicit Fork(hipStream_t s) : main(s), aux(aux_stream()) {
+    explicit Fork(hipStream_t s) : main(s), aux(aux_stream(s)) {
         HIP_OK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
         HIP_OK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
         HIP_OK(hipEventRecord(ev[0], main));
@@ -358,10 +359,13 @@ ArenaHint g_apply_hint, g_encode_hint;
 // copy from or to pageable memory is staged by the runtime and holds the host thread until it is
 // done).  Uploads are copied in when issued; downloads land in the arena and are copied out by
 // sync(), which every call runs before it reads them.  One arena per host thread; its memory is
-// reused only after the stream it served was synchronized (or its last copy waited for).
+// reused only after the stream it served was synchronized (or its last copy waited for).  The
+// blocks only grow and are never freed: hipHostFree waits for the whole device, which would hold a
+// call until work it left on its stream (apply's writes) had finished.
 struct PinnedStage {
-    std::vector<std::pair<uint8_t *, uint64_t>> blocks;  // the last one is in use
-    uint64_t used = 0;
+    std::vector<std::pair<uint8_t *, uint64_t>> blocks;  // each twice the size of the one before
+    size_t cur = 0;                                      // the block in use
+    uint64_t used = 0;                                   // bytes handed out from it
     struct Out {
         void *dst;
         const uint8_t *src;
@@ -374,14 +378,17 @@ struct PinnedStage {
 
     uint8_t *get(uint64_t n) {
         n = (n + 63) & ~uint64_t(63);
-        if (blocks.empty() || used + n > blocks.back().second) {
+        while (cur < blocks.size() && used + n > blocks[cur].second) {
+            ++cur;
+            used = 0;
+        }
+        if (cur == blocks.size()) {
             const uint64_t size = std::max<uint64_t>({n, uint64_t(4) << 20, blocks.empty() ? 0 : 2 * blocks.back().second});
             uint8_t *p = nullptr;
             HIP_OK(hipHostMalloc(reinterpret_cast<void **>(&p), size, hipHostMallocDefault));
             blocks.emplace_back(p, size);
-            used = 0;
         }
-        uint8_t *p = blocks.back().first + used;
+        uint8_t *p = blocks[cur].first + used;
         used += n;
         return p;
     }
@@ -394,7 +401,7 @@ struct PinnedStage {
         if (pending) HIP_OK(hipEventSynchronize(ev));
         pending = false;
     }
-    // after the stream is synchronized: deliver the downloads, keep only the largest block
+    // after the stream is synchronized: deliver the downloads, reuse the blocks from the first
     void finish() {
         wait();
         for (const Out &o : out) std::memcpy(o.dst, o.src, o.n);
@@ -409,10 +416,7 @@ struct PinnedStage {
         restart();
     }
     void restart() {
-        while (blocks.size() > 1) {
-            (void)hipHostFree(blocks.front().first);
-            blocks.erase(blocks.begin());
-        }
+        cur = 0;
         used = 0;
     }
 };

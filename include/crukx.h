@@ -98,9 +98,12 @@ uint64_t crx_update_total_changes(const crx_update *u);
  * `numels[i]` elements; `has_cache[i]`/`cache_vals[i]` give a trusted old checksum (else one is
  * computed from the weights).  `payload_dev` is NULL to upload the payload (and block table) from
  * the parsed host bytes, or the address of the payload inside a device-resident copy of the whole
- * update (the block table, which precedes the payload, is read from there too).  On any status but
- * CRX_OK nothing is written; on CRX_OK the writes are enqueued on `stream` (later work on it sees
- * them).
+ * update (the block table, which precedes the payload, is read from there too).  On CRX_CORRUPT,
+ * CRX_INVALID and CRX_NOMEM nothing is written; on CRX_OK the writes are enqueued on `stream` (later
+ * work on it sees them).  CRX_DEVICE (a HIP runtime error) leaves the weights unspecified: the
+ * writes are enqueued behind the device's own verdict before the host has read it, so a runtime
+ * error after that point cannot tell whether they ran.  Treat the weights, and any checksum cached
+ * for them, as unknown then.
  * `*changed` receives the number of changed elements. */
 int32_t crx_apply(const crx_update *u, const uint8_t *payload_dev, uint16_t *const *targets,
                   const uint64_t *numels, const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab,
