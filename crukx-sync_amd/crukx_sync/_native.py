@@ -71,6 +71,7 @@ SIGNATURES = {
     "crx_rice_candidates": (None, [_u64, _u64, _vp]),
     "crx_rice_choose": (_i32, [_u64, _vp, _vp]),
     "crx_timing_enable": (None, [_i32]),
+    "crx_timing_only": (None, [_cp]),
     "crx_timing_reset": (None, []),
     "crx_timing_read": (_i32, [_cp, _u64]),
 }
@@ -168,7 +169,9 @@ def ptr_array(values):
     return (ctypes.c_void_p * max(len(values), 1))(*values)
 
 
-def timing(enable: bool) -> None:
+def timing(enable: bool, only: list[str] | None = None) -> None:
+    """Per-launch kernel timing on or off; `only` limits it to the named kernels."""
+    lib().crx_timing_only(",".join(only).encode() if only else None)
     lib().crx_timing_enable(1 if enable else 0)
 
 

@@ -79,9 +79,20 @@ void timing_collect(bool wait) {
 }
 }  // namespace
 
-void timing_begin(hipStream_t s) {
+// the kernel names crx_timing_only selected (under g_tmu; empty: every kernel)
+std::vector<std::string> g_only;
+
+bool timed(const char *name) {  // under g_tmu
+    if (g_only.empty()) return true;
+    for (const std::string &n : g_only)
+        if (n == name) return true;
+    return false;
+}
+
+void timing_begin(const char *name, hipStream_t s) {
     if (!g_timing) return;
     std::lock_guard<std::mutex> lk(g_tmu);
+    if (!timed(name)) return;
     hipEvent_t e = take_event();
     if (!e) return;
     (void)hipEventRecord(e, s);
@@ -91,7 +102,7 @@ void timing_begin(hipStream_t s) {
 void timing_end(const char *name, hipStream_t s) {
     if (!g_timing) return;
     std::lock_guard<std::mutex> lk(g_tmu);
-    if (!g_open) return;
+    if (!g_open || !timed(name)) return;
     hipEvent_t e = take_event();
     if (!e) return;
     (void)hipEventRecord(e, s);
@@ -1407,6 +1418,22 @@ int32_t crx_rice_choose(uint64_t count, const int32_t cand[3], const uint64_t sh
 }
 
 void crx_timing_enable(int32_t on) { g_timing = on != 0; }
+
+void crx_timing_only(const char *names) {
+    std::lock_guard<std::mutex> lk(g_tmu);
+    g_only.clear();
+    if (!names) return;
+    std::string cur;
+    for (const char *c = names;; ++c) {
+        if (*c == ',' || *c == 0) {
+            if (!cur.empty()) g_only.push_back(cur);
+            cur.clear();
+            if (!*c) break;
+        } else {
+            cur += *c;
+        }
+    }
+}
 
 void crx_timing_reset(void) {
     timing_collect(true);

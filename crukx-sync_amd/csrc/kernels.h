@@ -231,8 +231,9 @@ void launch_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t 
 // stream.  Not timed by crx_timing (no events are created).
 hipError_t checksum_noalloc(const uint32_t *frame, uint32_t lead, uint64_t n, hipStream_t s, uint64_t *out);
 
-// Host-side timing of launches (events on the launch stream), enabled by crx_timing_enable.
-void timing_begin(hipStream_t s);
+// Host-side timing of launches (events on the launch stream), enabled by crx_timing_enable and
+// limited to the kernels named by crx_timing_only.  timing_begin and timing_end bracket one launch.
+void timing_begin(const char *name, hipStream_t s);
 void timing_end(const char *name, hipStream_t s);
 
 }  // namespace crx

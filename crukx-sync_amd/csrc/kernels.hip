@@ -25,13 +25,27 @@ static_assert(kRankCopies == 2 || kRankCopies == 4 || kRankCopies == 8, "kRankCo
 constexpr int kScanRows = 16;   // rows per batch of the apply histogram pass
 constexpr int kSelectRows = 12; // ... of the select pass (fewer registers: occupancy)
 
-// splitmix64(i) | 1: the per-position checksum weight (docs/FORMAT.md:61-64).
-__device__ __forceinline__ uint64_t weight(uint64_t i) {
-    uint64_t z = (i + 1) * kGolden;
+// splitmix64(i) | 1: the per-position checksum weight (docs/FORMAT.md:61-64).  mix_weight takes
+// z = (i + 1) * golden, so that streaming passes can step z by a constant instead of multiplying.
+__device__ __forceinline__ uint64_t mix_weight(uint64_t z) {
     z = (z ^ (z >> 30)) * kMix1;
     z = (z ^ (z >> 27)) * kMix2;
     return (z ^ (z >> 31)) | 1ULL;
 }
+__device__ __forceinline__ uint64_t weight(uint64_t i) { return mix_weight((i + 1) * kGolden); }
+
+// sum of u * w mod 2^64 over 16-bit u: the products with the low word of w are summed in 64 bits, with
+// the high word mod 2^32 in 32 bits, and combined once at the end (two 32-bit multiplies per element
+// instead of a 16 x 64-bit product).
+struct WeightedSum {
+    uint64_t lo = 0;
+    uint32_t hi = 0;
+    __device__ __forceinline__ void add(uint32_t u, uint64_t w) {
+        lo += (uint64_t)u * (uint32_t)w;
+        hi += u * (uint32_t)(w >> 32);
+    }
+    __device__ __forceinline__ uint64_t total() const { return lo + ((uint64_t)hi << 32); }
+};
 
 __device__ __forceinline__ uint32_t lane() { return __lane_id(); }
 // 64-bit integer min (the generic min template of the HIP headers goes through double precision)
@@ -246,7 +260,11 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
     const uint64_t rcap = a.rec_base ? ~0ULL : a.rec_per_slab;
     uint64_t written = 0;
     uint32_t cnt = 0;
-    uint64_t dacc = 0, facc = 0;
+    uint64_t dacc = 0;
+    WeightedSum full;  // cold: checksum of new
+    // cold: z = (index + 1) * golden of this lane's first element in the current row (element index
+    // 2 * first word - lead + offset, computed in 64 bits: it is -1 for the pad before an odd start)
+    uint64_t z = COLD ? (uint64_t)(2 * (int64_t)sl.first - (int64_t)td.lead + 2 * ln + 1) * kGolden : 0;
     stream_rows<kRankRows, 2, 0, kStreamNT>(sl, src, [&](uint32_t r, uint32_t o, uint32_t nw) {
         // exponents; lanes outside the slab count into slot 256 and never change
         uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF, x = o ^ nw, n = nw;
@@ -300,9 +318,10 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
         }
         atomicAdd(&hall[kRankCopies * k0 + rep], 1u);
         atomicAdd(&hall[kRankCopies * k1 + rep], 1u);
-        if (COLD) {
-            const uint32_t f = r * kRow + 2 * ln;
-            facc += (uint64_t)(n & 0xFFFF) * weight(sl.base + f) + (uint64_t)(n >> 16) * weight(sl.base + f + 1);
+        if (COLD) {  // elements outside the slab were zeroed in n
+            full.add(n & 0xFFFF, mix_weight(z));
+            full.add(n >> 16, mix_weight(z + kGolden));
+            z += (uint64_t)kRow * kGolden;
         }
         if (cnt > kChgCap - kRow) {
             flush_changes(a, sl, meta, vals, hchg, cnt, rbase, rcap, written, dacc);
@@ -316,7 +335,7 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
         a.hchg[(uint64_t)tau * 256 + k] = hchg[k];
     }
     dacc = wave_sum(dacc);
-    facc = wave_sum(facc);
+    const uint64_t facc = wave_sum(full.total());
     if (ln == 0) {
         a.delta[tau] = dacc;
         a.full[tau] = facc;
@@ -348,7 +367,9 @@ template <bool COLD>
 __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau, const Slab &sl, uint32_t *hall) {
     const uint32_t ln = lane(), rep = ln & (kHistCopies - 1);
     const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
-    uint64_t facc = 0;
+    WeightedSum full;  // cold: checksum of the weights
+    // cold: z = (index + 1) * golden of this lane's first element in the current row
+    uint64_t z = COLD ? (uint64_t)(2 * (int64_t)sl.first - (int64_t)td.lead + 2 * ln + 1) * kGolden : 0;
     stream_rows<kScanRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
         const uint32_t f = r * kRow + 2 * ln;
         uint32_t k0 = (o >> 7) & 0xFF, k1 = (o >> 23) & 0xFF, v = o;
@@ -365,8 +386,9 @@ __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau,
         atomicAdd(&hall[k0 * kHistCopies + rep], 1u);
         atomicAdd(&hall[k1 * kHistCopies + rep], 1u);
         if (COLD) {
-            facc += (uint64_t)(v & 0xFFFF) * weight(sl.base + f);
-            facc += (uint64_t)(v >> 16) * weight(sl.base + f + 1);
+            full.add(v & 0xFFFF, mix_weight(z));
+            full.add(v >> 16, mix_weight(z + kGolden));
+            z += (uint64_t)kRow * kGolden;
         }
     });
     wave_fence();
@@ -381,7 +403,7 @@ __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau,
         a.hall[(uint64_t)tau * 256 + k] = sum;
         if (out) out[k] = sum;
     }
-    facc = wave_sum(facc);
+    const uint64_t facc = wave_sum(full.total());
     if (ln == 0) a.full[tau] = facc;
 }
 
@@ -1020,15 +1042,18 @@ __global__ __launch_bounds__(256) void k_checksum(const uint32_t *frame, uint32_
     const uint64_t words = (n + lead + 1) >> 1;
     const uint64_t per = (words + n_parts - 1) / n_parts;
     const uint64_t wb = (uint64_t)blockIdx.x * per, we = min(wb + per, words);
-    unsigned long long s = 0;
-    for (uint64_t d = wb + threadIdx.x; d < we; d += 256) {
+    WeightedSum acc;
+    // z = (index + 1) * golden of the thread's first element of word d, stepped with d
+    uint64_t z = (uint64_t)(2 * (int64_t)(wb + threadIdx.x) - (int64_t)lead + 1) * kGolden;
+    for (uint64_t d = wb + threadIdx.x; d < we; d += 256, z += 512 * kGolden) {
         const uint32_t o = frame[d];
         const int64_t i0 = (int64_t)(2 * d) - (int64_t)lead;
-        if (i0 >= 0 && i0 < (int64_t)n) s += (uint64_t)(o & 0xFFFF) * weight((uint64_t)i0);
-        if (i0 + 1 >= 0 && i0 + 1 < (int64_t)n) s += (uint64_t)(o >> 16) * weight((uint64_t)i0 + 1);
+        const uint32_t u0 = i0 >= 0 ? o & 0xFFFF : 0u, u1 = i0 + 1 < (int64_t)n ? o >> 16 : 0u;
+        acc.add(u0, mix_weight(z));
+        acc.add(u1, mix_weight(z + kGolden));
     }
     unsigned long long total;
-    block_exclusive_sum(s, sh, &total);
+    block_exclusive_sum(acc.total(), sh, &total);
     if (threadIdx.x == 0) partial[blockIdx.x] = total;
 }
 
@@ -1758,7 +1783,7 @@ inline uint32_t grid1(uint64_t n, uint32_t per) { return (uint32_t)((n + per - 1
 #define CRX_LAUNCH(name, kernel, grid, block, stream, ...)                                   \
     do {                                                                                     \
         if ((grid) > 0) {                                                                    \
-            timing_begin(stream);                                                            \
+            timing_begin(name, stream);                                                      \
             hipLaunchKernelGGL(kernel, dim3(grid), dim3(block), 0, stream, __VA_ARGS__);     \
             timing_end(name, stream);                                                        \
         }                                                                                    \
@@ -1844,7 +1869,7 @@ void launch_scan_u32(const uint32_t *in, uint64_t n, unsigned long long *out, un
 void launch_verdict(uint32_t n, const unsigned long long *delta, const uint64_t *full, const int32_t *has,
                     const uint64_t *cached, const uint64_t *want, const unsigned int *bad, unsigned int *ok,
                     hipStream_t s) {
-    timing_begin(s);
+    timing_begin("verdict", s);
     hipLaunchKernelGGL(k_verdict, dim3(1), dim3(256), 0, s, n, delta, full, has, cached, want, bad, ok);
     timing_end("verdict", s);
 }
@@ -1862,7 +1887,7 @@ void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint6
 void launch_decode(const DecodeArgs &a, hipStream_t s) {
     const uint32_t grid = grid1(a.n_blocks, 64), lds = decode_lds_bytes(a.lds_pay_words, a.n_syms);
     if (!grid) return;
-    timing_begin(s);
+    timing_begin("decode", s);
     if (a.n_syms <= kDecSyms) hipLaunchKernelGGL(k_decode<true>, dim3(grid), dim3(64), lds, s, a);
     else hipLaunchKernelGGL(k_decode<false>, dim3(grid), dim3(64), lds, s, a);
     timing_end("decode", s);

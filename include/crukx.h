@@ -194,6 +194,9 @@ int32_t crx_rice_choose(uint64_t count, const int32_t cand[3], const uint64_t sh
  * When enabled, each kernel launch is bracketed by HIP events on its stream and the durations
  * accumulate per kernel name.  crx_timing_read writes "name calls total_ms\n" lines. */
 void crx_timing_enable(int32_t on);
+/* Limits the timing to the kernels named in `names` (comma-separated); NULL or "" times every kernel.
+ * Host phases ("host:...") are recorded whenever timing is enabled. */
+void crx_timing_only(const char *names);
 void crx_timing_reset(void);
 int32_t crx_timing_read(char *buf, uint64_t len);
 
