@@ -900,9 +900,9 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
             blk += n_blocks(g.count);
         }
     const uint64_t G = groups.size(), B = blk;
-    std::vector<uint32_t> tensor_blk(T + 1, (uint32_t)B);  // first block of each tensor (its changes are contiguous)
-    for (int64_t gi = (int64_t)G - 1; gi >= 0; --gi) tensor_blk[groups[gi].tensor] = groups[gi].blk_base;
-    for (int64_t t = (int64_t)T - 1; t >= 0; --t) tensor_blk[t] = std::min(tensor_blk[t], tensor_blk[t + 1]);
+    std::vector<uint32_t> tensor_chg(T + 1, (uint32_t)C);  // first change of each tensor (its changes are contiguous)
+    for (int64_t gi = (int64_t)G - 1; gi >= 0; --gi) tensor_chg[groups[gi].tensor] = groups[gi].elem_base;
+    for (int64_t t = (int64_t)T - 1; t >= 0; --t) tensor_chg[t] = std::min(tensor_chg[t], tensor_chg[t + 1]);
 
     hc.mark("apply_tables");
     // what the decoder needs goes first: it starts while the rest is enqueued
@@ -964,10 +964,12 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     int32_t *d_gof = ar.get<int32_t>((uint64_t)T * 256);
     h2d(d_gof, group_of.data(), group_of.size(), s);
     uint32_t *local = ar.get<uint32_t>(C);
-    unsigned long long *pv = ar.get<unsigned long long>(C);
-    unsigned long long *tdelta = ar.get<unsigned long long>(T), *bdelta = ar.get<unsigned long long>(B);
-    uint32_t *tblk = ar.get<uint32_t>(T + 1);
-    h2d(tblk, tensor_blk.data(), T + 1, s);
+    unsigned long long *rec = ar.get<unsigned long long>(C);  // the select pass's records, slab by slab
+    uint32_t *pn = ar.get<uint32_t>(C);                       // offset in the slab | new bits << 16
+    uint32_t *rstart = ar.get<uint32_t>((uint64_t)tiles + 1);
+    uint64_t *sdelta = ar.get<uint64_t>(tiles), *tdelta = ar.get<uint64_t>(T);
+    uint32_t *tchg = ar.get<uint32_t>(T + 1);
+    h2d(tchg, tensor_chg.data(), T + 1, s);
     uint32_t *lb = ar.get<uint32_t>((uint64_t)(tiles + 1) * 256);  // row tiles: read, never used
 
     // pass A: slabs of tensors without cached counts are streamed (their counts, and old checksums
@@ -992,17 +994,18 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     fork.join();
     hc.mark("apply_pass_a");
 
-    BlockArgs ba{d_groups, (uint32_t)G, slab, binfo, d_descs, sizes, blk_prefix, local, dz, pv, bdelta, bad, B, nullptr};
+    BlockArgs ba{d_groups, (uint32_t)G, slab, binfo, d_descs, sizes, blk_prefix, local, dz, bad, B};
     launch_local_fix(ba, B, s);
     uint2 *more = ar.get<uint2>(3 * (uint64_t)tiles);  // at most 3 windows after the first per slab
     unsigned int *n_more = ar.get<unsigned int>(1);
     zero(n_more, 1, s);
-    SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, pv, bad, more, n_more,
-                  std::min(1024u, 3 * tiles)};
+    SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, rec, rstart, tchg, bad, more,
+                  n_more, std::min(1024u, 3 * tiles)};
     launch_locate(sa, tiles, s);
     launch_select(sa, tiles, C > kSelectDenseTargets * tiles, s);
-    launch_verify(ba, B, s);
-    launch_range_sums(bdelta, tblk, T, tdelta, s);
+    SlabArgs sla{d_descs, sd.tile_tensor, slab, rstart, rec, dz, pn, sdelta, bad, nullptr, (uint32_t)C};
+    launch_verify(sla, tiles, s);
+    launch_tensor_sums(d_descs, T, sdelta, tdelta, s);
     // the verdict on the device too, and the scatter behind it: it writes only if the update verifies,
     // and the host waits for the verdict's data, not for the writes
     std::vector<uint64_t> want(T), cached(T, 0);
@@ -1018,17 +1021,17 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     h2d(d_want, want.data(), T, s);
     h2d(d_cached, cached.data(), T, s);
     h2d(d_has, has.data(), T, s);
-    launch_verdict(T, tdelta, t_full, d_has, d_cached, d_want, bad, ok, s);
+    launch_verdict(T, reinterpret_cast<const unsigned long long *>(tdelta), t_full, d_has, d_cached, d_want, bad, ok,
+                   s);
     hc.mark("apply_launch");
 
     unsigned int hbad = 0;
-    std::vector<unsigned long long> hdelta(T);
-    std::vector<uint64_t> hfull(T);
+    std::vector<uint64_t> hdelta(T), hfull(T);
     d2h(&hbad, bad, 1, s);
     d2h(hdelta.data(), tdelta, T, s);
     d2h(hfull.data(), t_full, T, s);
-    ba.ok = ok;
-    launch_scatter(ba, B, s);
+    sla.ok = ok;
+    launch_scatter(sla, tiles, s);
     t_stage.finish();  // the downloads above (enqueued before the scatter) have arrived
     hc.mark("apply_wait_verify");
     // the reference's verdict (codec.py:598-604,696-712): the group-size check first, then any

@@ -148,11 +148,29 @@ struct SelectArgs {
     const int32_t *group_of;        // [tensor][256] group index or -1
     const GroupDev *groups;
     const uint32_t *local;          // group-local index of every change
-    unsigned long long *pv;         // [changes] (in-row offset << 16 | old bits) | row's element index << 32
+    // [changes] the select pass's records, slab by slab (each slab's in row order): change index | offset
+    // in the slab << 32 | old bits << 48
+    unsigned long long *rec;
+    uint32_t *rstart;               // [tiles + 1] first record of each slab (written by k_locate)
+    const uint32_t *tchg;           // [tensors + 1] first change of each tensor
     unsigned int *bad;              // kBadUnplaced: a slab's targets were not all found
     uint2 *more;                    // [3 tiles] (slab, first exponent) of windows after a slab's first
     unsigned int *n_more;           // their number (zero before k_locate)
     uint32_t n_front;               // listed windows taken by the front blocks of the select pass
+};
+
+struct SlabArgs {                   // per-slab kernels over the select pass's records (one workgroup per slab)
+    const TensorDesc *descs;
+    const uint32_t *tile_tensor;
+    uint32_t slab;
+    const uint32_t *rstart;              // [tiles + 1]
+    const unsigned long long *rec;       // [changes] as SelectArgs::rec
+    const unsigned long long *dz;        // [changes] decoder output: zz in the low 32 bits
+    uint32_t *pn;                        // [changes] offset in the slab | new bits << 16 (k_verify)
+    uint64_t *sdelta;                    // [tiles] checksum delta of each slab's changes
+    unsigned int *bad;
+    const unsigned int *ok;              // k_scatter writes only when *ok: the device's verdict (k_verdict)
+    uint32_t n_changes;
 };
 
 struct BlockArgs {                  // per-block kernels over the change list (one workgroup per block)
@@ -164,11 +182,8 @@ struct BlockArgs {                  // per-block kernels over the change list (o
     const unsigned long long *blk_prefix;
     uint32_t *local;                // [changes] group-local index (written by k_local_fix)
     const unsigned long long *dz;   // [changes] decoder output: zz | (block-relative local << 32)
-    unsigned long long *pv;         // [changes] the select pass's output, then element index | new bits << 32 (k_verify)
-    unsigned long long *bdelta;     // [blocks] checksum delta of each block's changes
     unsigned int *bad;
     uint64_t n_blocks;
-    const unsigned int *ok;         // k_scatter writes only when *ok: the device's verdict (k_verdict)
 };
 
 void launch_enc_rank(const EncRankArgs &a, uint32_t tiles, hipStream_t s);
@@ -198,14 +213,11 @@ uint64_t scan_parts(uint64_t n);
 void launch_scan_u64(const unsigned long long *in, uint64_t n, unsigned long long *out, unsigned long long *part,
                      hipStream_t s);
 void launch_scan_u32(const uint32_t *in, uint64_t n, unsigned long long *out, unsigned long long *part, hipStream_t s);
-// out[t] = sum of v[begin[t] .. begin[t + 1])
 // ok = 1 iff *bad is 0 and every tensor's old checksum (cached[t] where has[t], else full[t]) plus
 // its delta equals want[t]; 0 otherwise.  One workgroup.
 void launch_verdict(uint32_t n, const unsigned long long *delta, const uint64_t *full, const int32_t *has,
                     const uint64_t *cached, const uint64_t *want, const unsigned int *bad, unsigned int *ok,
                     hipStream_t s);
-void launch_range_sums(const unsigned long long *v, const uint32_t *begin, uint32_t n, unsigned long long *out,
-                       hipStream_t s);
 void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint64_t *per_tile, uint64_t *out,
                         hipStream_t s);
 void launch_decode(const DecodeArgs &a, hipStream_t s);
@@ -222,8 +234,10 @@ void launch_tile_map(const TensorDesc *descs, uint32_t n_tensors, uint32_t *tile
 // dense: the larger LDS target list (for updates averaging over kSelectDenseTargets changes per slab)
 constexpr uint64_t kSelectDenseTargets = 800;
 void launch_select(const SelectArgs &a, uint32_t tiles, bool dense, hipStream_t s);
-void launch_verify(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
-void launch_scatter(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
+// New values and checksum deltas of every slab's records (one workgroup per slab).
+void launch_verify(const SlabArgs &a, uint32_t tiles, hipStream_t s);
+// The verified writes, slab by slab, each slab's in row order (one workgroup per slab).
+void launch_scatter(const SlabArgs &a, uint32_t tiles, hipStream_t s);
 void launch_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial, uint32_t n_parts,
                      hipStream_t s);
 // The full checksum of n 16-bit elements (frame words, lead as in TensorDesc) into *out (host

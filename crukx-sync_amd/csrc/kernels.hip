@@ -1024,17 +1024,6 @@ __global__ __launch_bounds__(256) void k_tensor_sums(const TensorDesc *descs, co
     if (threadIdx.x == 0) out[blockIdx.x] = total;
 }
 
-__global__ __launch_bounds__(256) void k_range_sums(const unsigned long long *v, const uint32_t *begin,
-                                                   unsigned long long *out) {
-    __shared__ unsigned long long sh[4];
-    const uint32_t b = begin[blockIdx.x], e = begin[blockIdx.x + 1];
-    unsigned long long s = 0;
-    for (uint32_t i = b + threadIdx.x; i < e; i += 256) s += v[i];
-    unsigned long long total;
-    block_exclusive_sum(s, sh, &total);
-    if (threadIdx.x == 0) out[blockIdx.x] = total;
-}
-
 // Full checksum of one tensor: each workgroup sums a contiguous range into partial[blockIdx.x].
 __global__ __launch_bounds__(256) void k_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial,
                                                   uint32_t n_parts) {
@@ -1289,8 +1278,10 @@ __global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
     __shared__ uint4 arg[kLocTiles * 256];     // searches, packed: (target, next, group, slot = 256 u + exponent)
     __shared__ uint32_t res[kLocTiles * 256];  // per slot: the first change at or past the slab (kNone: no group)
     __shared__ uint8_t has[kLocTiles * 256];   // per slot: the slab holds at least one of its changes
+    __shared__ uint32_t before[kLocTiles];     // per slab: its tensor's changes positioned before it
     if (*a.bad) return;
     const uint32_t ln = lane();
+    if (ln < kLocTiles) before[ln] = 0;
     // slab u of the wavefront, exponents ln + 64 q: those with a group are packed into consecutive
     // entries, so that the lower-bound searches (one per lane) take as few load instructions as the
     // slabs have groups
@@ -1319,10 +1310,11 @@ __global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
         const bool on = i0 + ln < n_act;
         uint4 x = make_uint4(0u, 0u, 0u, 0u);
         uint32_t lo = 0, hi = 0, end = 0, vhi = kNone;  // vhi: local[hi] once hi has moved
+        uint32_t gbase = 0;
         if (on) {
             x = arg[i0 + ln];
             const GroupDev gr = a.groups[x.z];
-            lo = gr.elem_base;
+            lo = gbase = gr.elem_base;
             hi = end = gr.elem_base + gr.count;
         }
         while (__any(lo < hi)) {
@@ -1339,12 +1331,18 @@ __global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
         if (on) {  // x.y, the count before the next slab, is kNone for a tensor's last slab
             res[x.w] = lo;
             has[x.w] = lo < end && (x.y == kNone || vhi < x.y);
+            atomicAdd(&before[x.w >> 8], lo - gbase);  // the group's changes before the slab
         }
     }
     wave_fence();
     for (uint32_t u = 0; u < kLocTiles; ++u) {
         const uint32_t tau = blockIdx.x * kLocTiles + u;
         if (tau >= tiles) break;
+        // the slab's records follow those of the slabs before it: of earlier tensors, then of its own
+        if (ln == 0) {
+            a.rstart[tau] = a.tchg[a.tile_tensor[tau]] + before[u];
+            if (tau + 1 == tiles) a.rstart[tiles] = a.tchg[a.n_tensors];
+        }
         uint64_t w[4];  // bit ln of w[q]: exponent ln + 64 q has targets in this slab
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1431,7 +1429,7 @@ struct SelectLds {
     uint32_t cnt[(kWin + kSpare) * kSelCopies];  // running counts, kSelCopies copies (by lane)
     alignas(16) uint16_t list[CAP];                // slab ranks of the window's targets, per exponent in order
     union {
-        uint32_t slot[2 * kRow];  // streaming: in-row rank -> (in-row offset << 16) | bits; [kRow, 2 kRow): per lane
+        uint32_t slot[2 * kRow];  // streaming: in-row rank -> record high word; [kRow, 2 kRow): per lane
         uint4 info[kWin];         // set-up, per window exponent: {list begin, list end, change index - list
                                   // index, exponent count before the slab}
     };
@@ -1439,10 +1437,11 @@ struct SelectLds {
 
 template <uint32_t CAP, bool LDS_LIST>
 __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase, SelectLds<CAP> &S,
-                            uint32_t nxt, uint32_t ci, const uint32_t cend, const uint32_t jofs, const uint32_t pre_k) {
+                            uint32_t nxt, uint32_t ci, const uint32_t cend, const uint32_t jofs, const uint32_t pre_k,
+                            uint32_t j) {
     // lane e, for window exponent e: nxt = slab rank of its next target (kFar: none left), ci = that
     // target's change index, cend = the end of its changes, jofs = change index - list index (LDS
-    // list), pre_k = its count before the slab (HBM list)
+    // list), pre_k = its count before the slab (HBM list).  j: the window's next record.
     const uint32_t ln = lane(), rep4 = (ln & (kSelCopies - 1)) * 4u;
     const uint32_t kb = (kbase << 7) * 0x10001u, sp = ((kWin + ln / kSelCopies) << 7) * 0x10001u;
     char *const cnt = reinterpret_cast<char *>(S.cnt);
@@ -1451,9 +1450,14 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
         if (LDS_LIST) return S.list[min(c - jo, CAP - 1)];
         return a.local[c] - pr;
     };
-    auto put = [&](uint32_t c, uint32_t r, uint32_t w) {  // w = (in-row offset << 16) | bits
-        a.pv[c] = (unsigned long long)w | ((unsigned long long)(sl.base + r * kRow) << 32);
+    // Found targets become records, stored in the order found (rows in order) from record j on: the
+    // change index c and the element's high word h = offset in the slab | bits << 16.  (Staging them
+    // in LDS for one coalesced store per 64 measured slower than these sequential single stores: select
+    // 4.84 -> 5.14 ms at 1% changed, 7.45 -> 8.8 ms at 2%.)
+    auto record = [&](uint32_t c, uint32_t h) -> unsigned long long {
+        return (unsigned long long)c | ((unsigned long long)h << 32);
     };
+
     uint32_t prev = 0;  // exponent ln's count before the row
     const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
     stream_rows<kSelectRows, 1, kStreamNT, kStreamNT>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
@@ -1474,8 +1478,9 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
         if (!H) return;
         wave_fence();
         const uint32_t c0 = c.x, c1 = c.y;
-        // this lane's elements as published: (in-row offset << 16) | bits
-        const uint32_t w0 = ((2 * ln) << 16) | (o & 0xFFFFu), w1 = ((2 * ln + 1) << 16) | (o >> 16);
+        // this lane's elements as records' high words: offset in the slab | bits << 16
+        const uint32_t f0 = r * kRow + 2 * ln - sl.f_lo;
+        const uint32_t w0 = f0 | (o << 16), w1 = (f0 + 1) | (o & 0xFFFF0000u);
         const uint32_t q = nxt - seen;  // in-row rank of the next target, for the exponents in H
         const bool hit = s > nxt;       // this lane's exponent is in H
         do {  // the next target of each exponent with targets in this row
@@ -1488,8 +1493,9 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
             const uint32_t rr0 = __builtin_amdgcn_mbcnt_hi((uint32_t)(M1 >> 32),
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)M1, mbcnt(M0)));
             const uint32_t rr1 = add_bit(rr0, M0);
-            const bool t0 = m0 && rr0 == qk, t1 = m1 && rr1 == qk;  // one element of the row
-            if (t0 || t1) put(ck, r, t1 ? w1 : w0);
+            const bool t0 = m0 && rr0 == qk, t1 = m1 && rr1 == qk;  // exactly one element of the row
+            if (t0 || t1) a.rec[j] = record(ck, t1 ? w1 : w0);
+            ++j;
             clear_bit(H, k);
         } while (H);
         if (hit) {  // every exponent that had one: its next target, lane-parallel
@@ -1516,12 +1522,13 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
             S.slot[m1 ? rr1 : kRow + ln] = w1;
             wave_fence();
             uint32_t n, tl;
-            do {  // one target per lane (64 more if all lanes take one)
-                const uint32_t j = ck + ln;
-                tl = j < ke ? target(j, jo, pr) : (uint32_t)kFar;
+            do {  // one target per lane (64 more if all lanes take one); the takers are lanes 0 .. n-1
+                const uint32_t c = ck + ln;
+                tl = c < ke ? target(c, jo, pr) : (uint32_t)kFar;
                 const bool take = tl < after;
                 n = (uint32_t)__popcll(ballot(take));
-                if (take) put(j, r, S.slot[tl - seen_k]);
+                if (take) a.rec[j + ln] = record(c, S.slot[tl - seen_k]);
+                j += n;
                 ck += n;
             } while (n == 64);
             const uint32_t tc = rdlane(tl, n);  // the first target not taken, or kFar
@@ -1575,6 +1582,12 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
     for (int o = 32; o > 0; o >>= 1) klo = min(klo, (uint32_t)__shfl_xor(klo, o, 64));
     const uint32_t kbase = kfirst < 256 ? kfirst : klo;
     if (kbase >= 256) return;  // no targets in this slab
+    // the window's records follow the slab's records of lower exponents (other windows)
+    uint32_t below = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) below += 4 * ln + q < kbase ? n4[q] : 0u;
+    for (int o = 32; o > 0; o >>= 1) below += (uint32_t)__shfl_xor(below, o, 64);
+    const uint32_t jbase = a.rstart[tau] + below;
     const Slab sl = slab_of(td, local_tile, a.slab);
     {
         uint32_t nw[4], mine = 0;
@@ -1658,8 +1671,8 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
         for (uint32_t i = ln; i < (kWin + kSpare) * kSelCopies; i += 64) S.cnt[i] = 0;
         wave_fence();
         const uint32_t c_first = inf.x + inf.z, c_end = inf.y + inf.z;  // change indices
-        if (in_lds) select_slab<CAP, true>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w);
-        else select_slab<CAP, false>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w);
+        if (in_lds) select_slab<CAP, true>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, jbase);
+        else select_slab<CAP, false>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, jbase);
     }
 }
 
@@ -1692,59 +1705,57 @@ __global__ __launch_bounds__(64) void k_select_more(SelectArgs a) {
     }
 }
 
-// new = (old + unzigzag(zz)) mod 2^16; checksum delta per tensor (codec.py:698-700).
-__global__ __launch_bounds__(256) void k_verify(BlockArgs a) {
-    __shared__ unsigned long long sh[kBlocksPerWG][256];
-    const uint32_t s = threadIdx.x;
+// new = (old + unzigzag(zz)) mod 2^16 and the checksum delta (codec.py:698-700), slab by slab over the
+// select pass's records; the exponent counts of elements that move between binades are updated.
+constexpr uint32_t kVerifyPer = 4;  // records per thread with their loads in flight together
+
+__global__ __launch_bounds__(256) void k_verify(SlabArgs a) {
+    __shared__ unsigned long long sh[4];
+    const uint32_t tau = blockIdx.x, tid = threadIdx.x;
     if (*a.bad) {  // positions were not computed: deltas of zero, so the verdict is deterministic
-        const uint64_t b = (uint64_t)blockIdx.x * kBlocksPerWG + s;
-        if (s < kBlocksPerWG && b < a.n_blocks) a.bdelta[b] = 0;
+        if (tid == 0) a.sdelta[tau] = 0;
         return;
     }
-    BlockInfo r[kBlocksPerWG];
-    unsigned long long pv[kBlocksPerWG];
-    uint32_t zz[kBlocksPerWG];
+    const uint32_t r0 = a.rstart[tau], r1 = a.rstart[tau + 1];
+    const TensorDesc td = a.descs[a.tile_tensor[tau]];
+    const uint32_t lt = tau - td.tile_begin;
+    const uint32_t first = lt * a.slab;  // tensor index of the slab's first element
+    uint32_t *const h = td.hist_out ? td.hist_out + (uint64_t)lt * 256 : nullptr;
+    unsigned long long d = 0;
+    for (uint32_t b = r0; b < r1; b += 256 * kVerifyPer) {
+        unsigned long long rc[kVerifyPer], z[kVerifyPer];
 #pragma unroll
-    for (uint32_t u = 0; u < kBlocksPerWG; ++u) r[u] = block_info(a, (uint64_t)blockIdx.x * kBlocksPerWG + u);
-#pragma unroll
-    for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
-        if (s < r[u].cnt) {
-            pv[u] = a.pv[(uint64_t)r[u].eb + s];
-            zz[u] = (uint32_t)a.dz[(uint64_t)r[u].eb + s];
+        for (uint32_t u = 0; u < kVerifyPer; ++u) {
+            const uint32_t i = b + tid + 256 * u;
+            rc[u] = i < r1 ? a.rec[i] : 0ULL;
         }
-    }
 #pragma unroll
-    for (uint32_t u = 0; u < kBlocksPerWG; ++u) {
-        unsigned long long d = 0;
-        const uint32_t lo = (uint32_t)pv[u];  // (in-row offset << 16) | old bits; row start << 32
-        const uint32_t p = (uint32_t)(pv[u] >> 32) + (lo >> 16);
-        if (s < r[u].cnt) {  // every change was placed: the select pass flags a slab that missed one
-            {
-                const int32_t delta = (int32_t)(zz[u] >> 1) ^ -(int32_t)(zz[u] & 1);
-                const uint32_t old = lo & 0xFFFFu;
+        for (uint32_t u = 0; u < kVerifyPer; ++u) {
+            const uint32_t i = b + tid + 256 * u;
+            z[u] = i < r1 && (uint32_t)rc[u] < a.n_changes ? a.dz[(uint32_t)rc[u]] : 0ULL;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kVerifyPer; ++u) {
+            const uint32_t i = b + tid + 256 * u;
+            if (i < r1) {
+                if ((uint32_t)rc[u] >= a.n_changes) atomicOr(a.bad, kBadUnplaced);  // never for found targets
+                const uint32_t zz = (uint32_t)z[u];
+                const uint32_t off = (uint32_t)(rc[u] >> 32) & 0xFFFFu, old = (uint32_t)(rc[u] >> 48);
+                const int32_t delta = (int32_t)(zz >> 1) ^ -(int32_t)(zz & 1);
                 const uint32_t nu = (uint32_t)((int32_t)old + delta) & 0xFFFF;
-                d = (uint64_t)((int64_t)nu - (int64_t)old) * weight(p);
-                a.pv[(uint64_t)r[u].eb + s] = p | ((unsigned long long)nu << 32);
+                d += (uint64_t)((int64_t)nu - (int64_t)old) * weight(first + off);
+                a.pn[i] = off | (nu << 16);
                 const uint32_t eo = (old >> 7) & 0xFF, en = (nu >> 7) & 0xFF;
-                if (eo != en) {  // the element moves between exponent counts of its slab
-                    uint32_t *h = a.descs[r[u].tensor].hist_out;
-                    if (h) {
-                        h += (uint64_t)(p / a.slab) * 256;
-                        atomicSub(&h[eo], 1u);
-                        atomicAdd(&h[en], 1u);
-                    }
+                if (eo != en && h) {  // the element moves between exponent counts of its slab
+                    atomicSub(&h[eo], 1u);
+                    atomicAdd(&h[en], 1u);
                 }
             }
         }
-        sh[u][s] = d;
     }
-    __syncthreads();
-    // wavefront u sums block u's deltas
-    const uint32_t w = s >> 6, ln = lane();
-    const unsigned long long *v = &sh[w][4 * ln];
-    const unsigned long long t = wave_sum(v[0] + v[1] + v[2] + v[3]);
-    const uint64_t b = (uint64_t)blockIdx.x * kBlocksPerWG + w;
-    if (ln == 0 && b < a.n_blocks) a.bdelta[b] = t;
+    unsigned long long total;
+    block_exclusive_sum(d, sh, &total);
+    if (tid == 0) a.sdelta[tau] = total;
 }
 
 // The host's verdict (codec.py:598-604,696-712), computed on the device as well so that the scatter
@@ -1763,15 +1774,20 @@ __global__ __launch_bounds__(256) void k_verdict(uint32_t n, const unsigned long
     if (threadIdx.x == 0) *ok = (miss == 0 && *bad == 0) ? 1u : 0u;
 }
 
-// One workgroup per block: the stores are bound by HBM partial writes, and more blocks per workgroup
-// measured slower.  Nothing is written unless the device's verdict is ok.
-__global__ __launch_bounds__(256) void k_scatter(BlockArgs a) {
+// The verified writes, one workgroup per slab: its records are in row order, so the stores of a
+// wavefront go to ascending addresses and changes that share a 64-byte unit of HBM are written close
+// together in time.  Nothing is written unless the device's verdict is ok.
+__global__ __launch_bounds__(256) void k_scatter(SlabArgs a) {
     if (!*a.ok) return;
-    const BlockInfo r = block_info(a, blockIdx.x);
-    const uint32_t s = threadIdx.x;
-    if (s < r.cnt) {
-        const unsigned long long pv = a.pv[(uint64_t)r.eb + s];
-        a.descs[r.tensor].base[(uint32_t)pv] = (uint16_t)(pv >> 32);
+    const uint32_t tau = blockIdx.x;
+    const uint32_t r0 = a.rstart[tau], r1 = a.rstart[tau + 1];
+    const TensorDesc td = a.descs[a.tile_tensor[tau]];
+    const uint64_t first = (uint64_t)(tau - td.tile_begin) * a.slab;
+    const uint32_t extent = (uint32_t)min64(a.slab, td.numel - first);  // offsets of verified records lie below
+    uint16_t *const base = td.base + first;
+    for (uint32_t i = r0 + threadIdx.x; i < r1; i += 256) {
+        const uint32_t v = a.pn[i];
+        if ((v & 0xFFFFu) < extent) base[v & 0xFFFFu] = (uint16_t)(v >> 16);
     }
 }
 
@@ -1874,11 +1890,6 @@ void launch_verdict(uint32_t n, const unsigned long long *delta, const uint64_t 
     timing_end("verdict", s);
 }
 
-void launch_range_sums(const unsigned long long *v, const uint32_t *begin, uint32_t n, unsigned long long *out,
-                       hipStream_t s) {
-    CRX_LAUNCH("range_sums", k_range_sums, n, 256, s, v, begin, out);
-}
-
 void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint64_t *per_tile, uint64_t *out,
                         hipStream_t s) {
     CRX_LAUNCH("tensor_sums", k_tensor_sums, n_tensors, 256, s, descs, per_tile, out);
@@ -1911,13 +1922,9 @@ void launch_select(const SelectArgs &a, uint32_t tiles, bool dense, hipStream_t 
     }
 }
 
-void launch_verify(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
-    CRX_LAUNCH("verify", k_verify, grid1(n_blocks, kBlocksPerWG), 256, s, a);
-}
+void launch_verify(const SlabArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("verify", k_verify, tiles, 256, s, a); }
 
-void launch_scatter(const BlockArgs &a, uint64_t n_blocks, hipStream_t s) {
-    CRX_LAUNCH("scatter", k_scatter, (uint32_t)n_blocks, 256, s, a);
-}
+void launch_scatter(const SlabArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("scatter", k_scatter, tiles, 256, s, a); }
 
 void launch_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial, uint32_t n_parts,
                      hipStream_t s) {
