@@ -996,11 +996,11 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
 
     BlockArgs ba{d_groups, (uint32_t)G, slab, binfo, d_descs, sizes, blk_prefix, local, dz, bad, B};
     launch_local_fix(ba, B, s);
-    uint2 *more = ar.get<uint2>(3 * (uint64_t)tiles);  // at most 3 windows after the first per slab
+    uint2 *more = ar.get<uint2>((uint64_t)kSelMoreWindows * tiles);  // windows after the first, per slab
     unsigned int *n_more = ar.get<unsigned int>(1);
     zero(n_more, 1, s);
     SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, rec, rstart, tchg, bad, more,
-                  n_more, std::min(1024u, 3 * tiles)};
+                  n_more, (uint32_t)std::min<uint64_t>(1024, (uint64_t)kSelMoreWindows * tiles)};
     launch_locate(sa, tiles, s);
     launch_select(sa, tiles, C > kSelectDenseTargets * tiles, s);
     SlabArgs sla{d_descs, sd.tile_tensor, slab, rstart, rec, dz, pn, sdelta, bad, nullptr, (uint32_t)C};

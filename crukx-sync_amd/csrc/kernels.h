@@ -231,6 +231,10 @@ void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
 void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s);
 // tile_tensor[tile] = tensor of every slab of the layout
 void launch_tile_map(const TensorDesc *descs, uint32_t n_tensors, uint32_t *tile_tensor, hipStream_t s);
+// Exponents per window of the select pass (a slab is streamed once per window holding targets), and
+// the most windows a slab can need after its first.
+constexpr uint32_t kSelWin = 64;
+constexpr uint32_t kSelMoreWindows = 256 / kSelWin - 1;
 // dense: the larger LDS target list (for updates averaging over kSelectDenseTargets changes per slab)
 constexpr uint64_t kSelectDenseTargets = 800;
 void launch_select(const SelectArgs &a, uint32_t tiles, bool dense, hipStream_t s);

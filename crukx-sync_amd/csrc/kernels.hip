@@ -1272,7 +1272,6 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
 // number of same-exponent elements before the slab.  Also lists the slab's exponent windows after
 // its first one (the select pass streams the slab once per window): windows of kSelWin exponents,
 // each starting at the lowest exponent with targets past the previous window.
-constexpr uint32_t kSelWin = 64;
 constexpr uint32_t kLocTiles = 2;  // slabs per wavefront: their searches share the lanes
 __global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
     __shared__ uint4 arg[kLocTiles * 256];     // searches, packed: (target, next, group, slot = 256 u + exponent)
