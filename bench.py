@@ -95,7 +95,7 @@ def main():
         ", ".join(f"{n} {ms:.3f}" for n, ms in sorted(res["kernels"].items(), key=lambda x: -x[1])[:8]))
 
     dom, avg_ms = res["dominant"], res["dominant_ms"]
-    alg = alg_bytes(dom, N)
+    alg = alg_bytes(dom, N, res["changes"])
     achieved = alg / (avg_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -111,7 +111,7 @@ def main():
     detail["bytes_per_change"] = round(res["update_bytes"] / max(res["changes"], 1), 4)
     detail["whole_update_alg_gbs"] = round(whole, 1)
     detail["whole_update_frac"] = round(whole / HBM_PEAK_GBS, 4)
-    detail["streaming_kernels"] = {k: {"ms": round(v, 4), "frac": round(alg_bytes(k, N) / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    detail["streaming_kernels"] = {k: {"ms": round(v, 4), "frac": round(alg_bytes(k, N, res["changes"]) / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
                                    for k, v in res["kernels"].items() if k in STREAMING}
     detail["kernels_ms_per_step"] = {n: round(ms, 4) for n, ms in sorted(res["kernels"].items())}
     detail["cold_breakdown_ms"] = res["cold_breakdown"]
@@ -142,9 +142,10 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-def alg_bytes(kernel: str, n: int) -> int:
-    """Algorithmic HBM bytes of one launch of a streaming kernel: the weights it must read."""
-    return {"enc_rank": 4 * n, "select": 2 * n, "apply_hist": 2 * n}[kernel]
+def alg_bytes(kernel: str, n: int, changes: int) -> int:
+    """Algorithmic HBM bytes of one launch of a streaming kernel: the weights it must read, and for the
+    select pass (which writes the new bits of the slabs it streams in one window) 2 bytes per change."""
+    return {"enc_rank": 4 * n, "select": 2 * n + 2 * changes, "apply_hist": 2 * n}[kernel]
 
 
 class Run:
@@ -275,8 +276,8 @@ def other_config(torch, dev, workload, rho, args, base=None):
     out = {"weights": n, "rho": rho, "ms_per_step": round(res["ms_step"], 3), "encode_ms": res["encode_ms"],
            "apply_ms": res["apply_ms"], "cold2_encode_ms": res["cold2_encode_ms"],
            "cold2_apply_ms": res["cold2_apply_ms"], "changes": res["changes"], "update_bytes": res["update_bytes"],
-           "dominant": dom, "dominant_frac": round(alg_bytes(dom, n) / (res["dominant_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-           "streaming_kernels": {k: {"ms": round(v, 4), "frac": round(alg_bytes(k, n) / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+           "dominant": dom, "dominant_frac": round(alg_bytes(dom, n, res["changes"]) / (res["dominant_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "streaming_kernels": {k: {"ms": round(v, 4), "frac": round(alg_bytes(k, n, res["changes"]) / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
                                  for k, v in res["kernels"].items() if k in STREAMING},
            "kernels_ms_per_step": {k: round(v, 4) for k, v in sorted(res["kernels"].items()) if not k.startswith("host:")}}
     log(f"[bench] {workload} rho={rho}: {out['ms_per_step']:.3f} ms/step (encode {out['encode_ms']:.3f}, "

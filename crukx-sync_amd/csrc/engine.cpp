@@ -999,15 +999,10 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     uint2 *more = ar.get<uint2>((uint64_t)kSelMoreWindows * tiles);  // windows after the first, per slab
     unsigned int *n_more = ar.get<unsigned int>(1);
     zero(n_more, 1, s);
-    SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, rec, rstart, tchg, bad, more,
-                  n_more, (uint32_t)std::min<uint64_t>(1024, (uint64_t)kSelMoreWindows * tiles)};
-    launch_locate(sa, tiles, s);
-    launch_select(sa, tiles, C > kSelectDenseTargets * tiles, s);
-    SlabArgs sla{d_descs, sd.tile_tensor, slab, rstart, rec, dz, pn, sdelta, bad, nullptr, (uint32_t)C};
-    launch_verify(sla, tiles, s);
-    launch_tensor_sums(d_descs, T, sdelta, tdelta, s);
-    // the verdict on the device too, and the scatter behind it: it writes only if the update verifies,
-    // and the host waits for the verdict's data, not for the writes
+    uint8_t *multi = ar.get<uint8_t>(tiles);
+    uint32_t *done = ar.get<uint32_t>(tiles);
+    // the verdict's inputs, set up before the select pass writes anything: between its writes and the
+    // commit that can undo them, the host only launches
     std::vector<uint64_t> want(T), cached(T, 0);
     std::vector<int32_t> has(T, 0);
     for (uint32_t t = 0; t < T; ++t) {
@@ -1021,8 +1016,22 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     h2d(d_want, want.data(), T, s);
     h2d(d_cached, cached.data(), T, s);
     h2d(d_has, has.data(), T, s);
+    SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, rec, rstart, tchg, bad, more,
+                  n_more, (uint32_t)std::min<uint64_t>(1024, (uint64_t)kSelMoreWindows * tiles), dz, sdelta, multi,
+                  done, (uint32_t)C};
+    launch_locate(sa, tiles, s);
+    // slabs streamed in one window are written through by the select pass, before the verdict: the
+    // commit below undoes those writes if the update does not verify
+    launch_select(sa, tiles, C > kSelectDenseTargets * tiles, s);
+    SlabArgs sla{d_descs, sd.tile_tensor, slab, rstart, rec, dz, pn, sdelta, bad, nullptr, (uint32_t)C, multi, done};
+    launch_verify(sla, tiles, s);
+    launch_tensor_sums(d_descs, T, sdelta, tdelta, s);
+    // the verdict on the device too, and the commit behind it (the remaining writes if the update
+    // verifies, the undoing of the select pass's if not); the host waits for the verdict's data only
     launch_verdict(T, reinterpret_cast<const unsigned long long *>(tdelta), t_full, d_has, d_cached, d_want, bad, ok,
                    s);
+    sla.ok = ok;
+    launch_commit(sla, tiles, s);  // next to the verdict: nothing on the host can fail in between
     hc.mark("apply_launch");
 
     unsigned int hbad = 0;
@@ -1030,9 +1039,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     d2h(&hbad, bad, 1, s);
     d2h(hdelta.data(), tdelta, T, s);
     d2h(hfull.data(), t_full, T, s);
-    sla.ok = ok;
-    launch_scatter(sla, tiles, s);
-    t_stage.finish();  // the downloads above (enqueued before the scatter) have arrived
+    t_stage.finish();  // the downloads above (behind the commit, which exits at once when the update verifies)
     hc.mark("apply_wait_verify");
     // the reference's verdict (codec.py:598-604,696-712): the group-size check first, then any
     // checksum mismatch (naming up to three tensors), then any other inconsistency

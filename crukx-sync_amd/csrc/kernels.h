@@ -154,9 +154,17 @@ struct SelectArgs {
     uint32_t *rstart;               // [tiles + 1] first record of each slab (written by k_locate)
     const uint32_t *tchg;           // [tensors + 1] first change of each tensor
     unsigned int *bad;              // kBadUnplaced: a slab's targets were not all found
-    uint2 *more;                    // [3 tiles] (slab, first exponent) of windows after a slab's first
+    uint2 *more;                    // [kSelMoreWindows tiles] (slab, first exponent) of windows after a slab's first
     unsigned int *n_more;           // their number (zero before k_locate)
     uint32_t n_front;               // listed windows taken by the front blocks of the select pass
+    // A slab streamed in one window is written by its select wave once its records are complete:
+    // new bits, checksum delta and exponent moves (k_commit undoes the writes if the update does not
+    // verify).  Slabs with more windows (multi, set by k_locate) are left to k_verify and k_commit.
+    const unsigned long long *dz;   // [changes] decoder output: zz in the low 32 bits
+    uint64_t *sdelta;               // [tiles] checksum delta of each single-window slab's changes
+    uint8_t *multi;                 // [tiles] the slab has more than one window (k_locate)
+    uint32_t *done;                 // [tiles] records written through by the select pass (zeroed by k_locate)
+    uint32_t n_changes;
 };
 
 struct SlabArgs {                   // per-slab kernels over the select pass's records (one workgroup per slab)
@@ -169,8 +177,10 @@ struct SlabArgs {                   // per-slab kernels over the select pass's r
     uint32_t *pn;                        // [changes] offset in the slab | new bits << 16 (k_verify)
     uint64_t *sdelta;                    // [tiles] checksum delta of each slab's changes
     unsigned int *bad;
-    const unsigned int *ok;              // k_scatter writes only when *ok: the device's verdict (k_verdict)
+    const unsigned int *ok;              // the device's verdict (k_verdict), read by k_commit
     uint32_t n_changes;
+    const uint8_t *multi;                // [tiles] as SelectArgs::multi
+    const uint32_t *done;                // [tiles] as SelectArgs::done
 };
 
 struct BlockArgs {                  // per-block kernels over the change list (one workgroup per block)
@@ -238,10 +248,12 @@ constexpr uint32_t kSelMoreWindows = 256 / kSelWin - 1;
 // dense: the larger LDS target list (for updates averaging over kSelectDenseTargets changes per slab)
 constexpr uint64_t kSelectDenseTargets = 800;
 void launch_select(const SelectArgs &a, uint32_t tiles, bool dense, hipStream_t s);
-// New values and checksum deltas of every slab's records (one workgroup per slab).
+// New values and checksum deltas of the records of slabs with more than one window (one workgroup
+// per slab; the select pass did the others' already).
 void launch_verify(const SlabArgs &a, uint32_t tiles, hipStream_t s);
-// The verified writes, slab by slab, each slab's in row order (one workgroup per slab).
-void launch_scatter(const SlabArgs &a, uint32_t tiles, hipStream_t s);
+// After the device's verdict (one workgroup per slab): if the update verifies, the writes of slabs
+// with more than one window; if not, the old bits back where the select pass wrote.
+void launch_commit(const SlabArgs &a, uint32_t tiles, hipStream_t s);
 void launch_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial, uint32_t n_parts,
                      hipStream_t s);
 // The full checksum of n 16-bit elements (frame words, lead as in TensorDesc) into *out (host

@@ -23,7 +23,7 @@ constexpr int kChgCap = 256;    // changes the rank pass buffers in LDS; a flush
 constexpr uint32_t kRankCopies = 4;  // copies of each exponent count in the rank pass (2, 4 or 8; 4 measured best)
 static_assert(kRankCopies == 2 || kRankCopies == 4 || kRankCopies == 8, "kRankCopies");
 constexpr int kScanRows = 16;   // rows per batch of the apply histogram pass
-constexpr int kSelectRows = 12; // ... of the select pass (fewer registers: occupancy)
+constexpr int kSelectRows = 8;  // ... of the select pass (fewer registers: occupancy)
 
 // splitmix64(i) | 1: the per-position checksum weight (docs/FORMAT.md:61-64).  mix_weight takes
 // z = (i + 1) * golden, so that streaming passes can step z by a constant instead of multiplying.
@@ -1278,8 +1278,13 @@ __global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
     __shared__ uint32_t res[kLocTiles * 256];  // per slot: the first change at or past the slab (kNone: no group)
     __shared__ uint8_t has[kLocTiles * 256];   // per slot: the slab holds at least one of its changes
     __shared__ uint32_t before[kLocTiles];     // per slab: its tensor's changes positioned before it
-    if (*a.bad) return;
     const uint32_t ln = lane();
+    // nothing written through yet, whether or not the select pass runs (k_commit reads these)
+    if (ln < kLocTiles && blockIdx.x * kLocTiles + ln < tiles) {
+        a.done[blockIdx.x * kLocTiles + ln] = 0;
+        a.multi[blockIdx.x * kLocTiles + ln] = 0;
+    }
+    if (*a.bad) return;
     if (ln < kLocTiles) before[ln] = 0;
     // slab u of the wavefront, exponents ln + 64 q: those with a group are packed into consecutive
     // entries, so that the lower-bound searches (one per lane) take as few load instructions as the
@@ -1359,7 +1364,10 @@ __global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
             uint32_t kb = first_at(0);
             while (kb < 256 - kSelWin) {
                 kb = first_at(kb + kSelWin);
-                if (kb < 256) a.more[atomicAdd(a.n_more, 1u)] = make_uint2(tau, kb);
+                if (kb < 256) {
+                    a.more[atomicAdd(a.n_more, 1u)] = make_uint2(tau, kb);
+                    a.multi[tau] = 1;
+                }
             }
         }
     }
@@ -1377,10 +1385,13 @@ __global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
 // stable in-row rank, and the lane holding the element whose rank matches the target records it;
 // then the lanes of all those exponents read their next targets together.  A row with more targets
 // of one exponent publishes that exponent's elements in LDS by rank and takes the rest one per lane.
+// A slab streamed in one window is then written through by its wave (write_through).
 //
-// The pass is bound by instruction issue: about 15 vector instructions per target and 10 per row
-// (six packed-16-bit and address operations, two LDS atomics, one LDS read and one compare), with
-// the LDS footprint setting occupancy.
+// Cost (7.6e9 weights, 1% changed, counters per 128-element row): 35 vector and 31 scalar
+// instructions, 4.3 LDS instructions; LDS bank and address conflicts of the atomics stall about a
+// third of the time each.  Fewer vector instructions alone (42 -> 35 per row with the split-halves
+// layout) or fewer conflicts alone (8 copies) left the time unchanged: issue, LDS and latency are
+// all near their limits, with the LDS footprint setting occupancy.
 // targets per window held in LDS (a multiple of 1024; more are read from HBM): the smaller list keeps
 // the footprint small (occupancy) for sparse updates, the larger one serves denser updates
 constexpr uint32_t kTgtCapSparse = 1024, kTgtCapDense = 2048;
@@ -1429,20 +1440,51 @@ struct SelectLds {
     alignas(16) uint16_t list[CAP];                // slab ranks of the window's targets, per exponent in order
     union {
         uint32_t slot[2 * kRow];  // streaming: in-row rank -> record high word; [kRow, 2 kRow): per lane
-        uint4 info[kWin];         // set-up, per window exponent: {list begin, list end, change index - list
+        uint4 info[64];           // set-up, per lane (its window exponent; zero past kWin): {list begin, list end, change index - list
                                   // index, exponent count before the slab}
     };
 };
 
+// Streams the slab's rows like stream_rows (U rows per batch, the next batch in flight), but lane l
+// holds elements l and l + 64 of each row (two 16-bit loads into the halves of one register, as
+// lo | hi << 16).  Within a row the 64 low elements then come before the 64 high ones, each half in
+// lane order, so the rank of an element among the row's elements of one kind needs the ballot of its
+// own half only.
+template <int U, int CPOL, typename Body>
+__device__ __forceinline__ void stream_halves(const Slab &sl, const Rsrc &src, Body &&body) {
+    const uint32_t lb = lane() * 2u;
+    u16x2 cur[U], nxt[U];
+    auto load = [&](u16x2(&dst)[U], uint32_t base) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            dst[u].x = __builtin_amdgcn_raw_buffer_load_b16(src, base + u * 256u, 0, CPOL);
+            dst[u].y = __builtin_amdgcn_raw_buffer_load_b16(src, base + u * 256u + 128u, 0, CPOL);
+        }
+    };
+    load(cur, lb);
+    for (uint32_t r0 = 0; r0 < sl.nrows; r0 += U) {
+        load(nxt, (r0 + U) * 256u + lb);
+#pragma unroll
+        for (int u = 0; u < U; ++u) body(r0 + u, __builtin_bit_cast(uint32_t, cur[u]));
+#pragma unroll
+        for (int u = 0; u < U; ++u) cur[u] = nxt[u];
+    }
+}
+
 template <uint32_t CAP, bool LDS_LIST>
-__device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase, SelectLds<CAP> &S,
+__device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase, SelectLds<CAP> &S,
                             uint32_t nxt, uint32_t ci, const uint32_t cend, const uint32_t jofs, const uint32_t pre_k,
                             uint32_t j) {
     // lane e, for window exponent e: nxt = slab rank of its next target (kFar: none left), ci = that
     // target's change index, cend = the end of its changes, jofs = change index - list index (LDS
-    // list), pre_k = its count before the slab (HBM list).  j: the window's next record.
-    const uint32_t ln = lane(), rep4 = (ln & (kSelCopies - 1)) * 4u;
-    const uint32_t kb = (kbase << 7) * 0x10001u, sp = ((kWin + ln / kSelCopies) << 7) * 0x10001u;
+    // list), pre_k = its count before the slab (HBM list).  j (uniform): the window's next record.
+    const uint32_t ln = lane();
+    // Per 16-bit half, an element's key is (window index << 7) + (its lane's copy << 5): the counter's
+    // byte offset << kCntShift, so one shift gives the address.  Exponents below the window wrap past
+    // the spare's key (the copy term is below 128), those above it are clamped to the spare's.
+    const uint32_t rep = (ln & (kSelCopies - 1)) << (kCntShift + 2);
+    const uint32_t kb = (((kbase << 7) - rep) & 0xFFFFu) * 0x10001u;
+    const uint32_t sp = (((kWin + ln / kSelCopies) << 7) + rep) * 0x10001u;
     char *const cnt = reinterpret_cast<char *>(S.cnt);
     // slab rank of the target with change index c (below its exponent's end)
     auto target = [&](uint32_t c, uint32_t jo, uint32_t pr) -> uint32_t {
@@ -1458,42 +1500,41 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
     };
 
     uint32_t prev = 0;  // exponent ln's count before the row
-    const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
-    stream_rows<kSelectRows, 1, kStreamNT, kStreamNT>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
-        // window index << 7 of both elements (16-bit halves); outside the window or the slab: the spare
+    stream_halves<kSelectRows, kStreamNT>(sl, slab_rsrc(td.frame, sl), [&](uint32_t r, uint32_t o) {
+        // both elements' keys; outside the window or the slab: the spare's
         u16x2 c = __builtin_elementwise_min(as16(o & 0x7F807F80u) - as16(kb), as16(sp));
+        const uint32_t f = r * kRow + ln;  // the low element's offset; the high one's is f + 64
         if (!row_full(sl, r)) {
-            const uint32_t f = r * kRow + 2 * ln;
             if (f < sl.f_lo || f >= sl.f_hi) c.x = as16(sp).x;
-            if (f + 1 < sl.f_lo || f + 1 >= sl.f_hi) c.y = as16(sp).y;
+            if (f + 64 < sl.f_lo || f + 64 >= sl.f_hi) c.y = as16(sp).y;
         }
-        const uint32_t ad = __builtin_bit_cast(uint32_t, c >> (unsigned short)kCntShift);
-        atomicAdd(reinterpret_cast<uint32_t *>(cnt + and_or(ad, 0xFFFFu, rep4)), 1u);
-        atomicAdd(reinterpret_cast<uint32_t *>(cnt + ((ad >> 16) | rep4)), 1u);
+        const uint32_t key = __builtin_bit_cast(uint32_t, c);
+        atomicAdd(reinterpret_cast<uint32_t *>(cnt + ((key & 0xFFFFu) >> kCntShift)), 1u);
+        atomicAdd(reinterpret_cast<uint32_t *>(cnt + (key >> (16 + kCntShift))), 1u);
         const uint32_t s = sel_count(S.cnt, ln);  // exponent ln's count up to the row's end
         const uint32_t seen = prev;
         prev = s;
         uint64_t H = ballot(s > nxt);
         if (!H) return;
         wave_fence();
-        const uint32_t c0 = c.x, c1 = c.y;
+        // window index << 7 of both elements (the copy term cleared)
+        const uint32_t kx = key & 0xFF80FF80u, c0 = kx & 0xFFFFu, c1 = kx >> 16;
         // this lane's elements as records' high words: offset in the slab | bits << 16
-        const uint32_t f0 = r * kRow + 2 * ln - sl.f_lo;
-        const uint32_t w0 = f0 | (o << 16), w1 = (f0 + 1) | (o & 0xFFFF0000u);
+        const uint32_t w0 = (f - sl.f_lo) | (o << 16), w1 = (f + 64 - sl.f_lo) | (o & 0xFFFF0000u);
         const uint32_t q = nxt - seen;  // in-row rank of the next target, for the exponents in H
         const bool hit = s > nxt;       // this lane's exponent is in H
-        do {  // the next target of each exponent with targets in this row
-            const uint32_t k = (uint32_t)__builtin_ctzll(H);
+        do {  // the next target of each exponent with targets in this row: exactly one element
+            const uint32_t k = (uint32_t)__builtin_ctzll(H), kk = k << 7;
             const uint32_t qk = rdlane(q, k), ck = rdlane(ci, k);
-            const bool m0 = c0 == (k << 7), m1 = c1 == (k << 7);
-            const uint64_t M0 = ballot(m0), M1 = ballot(m1);
-            // in-row rank of this lane's first element among exponent k's (the second's is one more
-            // when the first is one of them)
-            const uint32_t rr0 = __builtin_amdgcn_mbcnt_hi((uint32_t)(M1 >> 32),
-                                     __builtin_amdgcn_mbcnt_lo((uint32_t)M1, mbcnt(M0)));
-            const uint32_t rr1 = add_bit(rr0, M0);
-            const bool t0 = m0 && rr0 == qk, t1 = m1 && rr1 == qk;  // exactly one element of the row
-            if (t0 || t1) a.rec[j] = record(ck, t1 ? w1 : w0);
+            const bool m0 = c0 == kk;
+            const uint64_t M0 = ballot(m0);
+            const uint32_t n0 = (uint32_t)__popcll(M0);  // exponent k's low elements in the row
+            if (qk < n0) {  // a low element: the one whose rank among them is qk
+                if (m0 && mbcnt(M0) == qk) a.rec[j] = record(ck, w0);
+            } else {        // a high element: rank qk - n0 among the high ones
+                const bool m1 = c1 == kk;
+                if (m1 && mbcnt(ballot(m1)) == qk - n0) a.rec[j] = record(ck, w1);
+            }
             ++j;
             clear_bit(H, k);
         } while (H);
@@ -1513,10 +1554,8 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
             const uint32_t jo = LDS_LIST ? rdlane(jofs, k) : 0u, pr = LDS_LIST ? 0u : rdlane(pre_k, k);
             uint32_t ck = rdlane(ci, k);
             const bool m0 = c0 == (k << 7), m1 = c1 == (k << 7);
-            const uint64_t M0 = ballot(m0), M1 = ballot(m1);
-            const uint32_t rr0 = __builtin_amdgcn_mbcnt_hi((uint32_t)(M1 >> 32),
-                                     __builtin_amdgcn_mbcnt_lo((uint32_t)M1, mbcnt(M0)));
-            const uint32_t rr1 = add_bit(rr0, M0);
+            const uint64_t M0 = ballot(m0);
+            const uint32_t rr0 = mbcnt(M0), rr1 = (uint32_t)__popcll(M0) + mbcnt(ballot(m1));  // in-row ranks
             S.slot[m0 ? rr0 : kRow + ln] = w0;
             S.slot[m1 ? rr1 : kRow + ln] = w1;
             wave_fence();
@@ -1524,7 +1563,7 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
             do {  // one target per lane (64 more if all lanes take one); the takers are lanes 0 .. n-1
                 const uint32_t c = ck + ln;
                 tl = c < ke ? target(c, jo, pr) : (uint32_t)kFar;
-                const bool take = tl < after;
+                const bool take = c < ke && tl < after;  // never past the exponent's own targets
                 n = (uint32_t)__popcll(ballot(take));
                 if (take) a.rec[j + ln] = record(c, S.slot[tl - seen_k]);
                 j += n;
@@ -1542,6 +1581,65 @@ __device__ __forceinline__ void select_slab(const SelectArgs &a, const TensorDes
     // every target of this window's exponents is found once its rank is passed: one still pending
     // lies past the slab's elements of its exponent (never so when the local indices were in range)
     if (ci < cend) atomicOr(a.bad, kBadUnplaced);
+    return j;  // past the window's last record
+}
+
+// The writes of a slab streamed in one window, by its select wave once the window's records [r0, r1)
+// are stored (those of a window not fully placed are the ones found): new = (old + unzigzag(zz)) mod
+// 2^16 (codec.py:698-700) over the receiver's bits, the slab's checksum delta, and the exponent counts
+// of elements that move between binades.  The update is not verified yet: k_commit puts the old bits
+// back (they are in the records) if it does not verify, so a failed apply leaves the weights as they
+// were, as the reference's verify-then-write does (codec.py:703-707).  Writing here, while the other
+// waves of the chip are still streaming, takes the partial-sector writes off a pass of their own.
+constexpr uint32_t kWritePer = 2;  // records per lane with their loads in flight together (registers: occupancy)
+
+__device__ void write_through(const SelectArgs &a, const TensorDesc &td, uint32_t tau, uint32_t lt, uint32_t r0,
+                              uint32_t r1) {
+    // this wave's record stores are complete, and its loads below see them
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    const uint32_t ln = lane();
+    const uint64_t first = (uint64_t)lt * a.slab;  // tensor index of the slab's first element
+    const uint32_t extent = (uint32_t)min64(a.slab, td.numel - first);  // offsets of found targets lie below
+    uint16_t *const base = td.base + first;
+    uint32_t *const h = td.hist_out ? td.hist_out + (uint64_t)lt * 256 : nullptr;
+    unsigned long long d = 0;
+    for (uint32_t b = r0; b < r1; b += 64 * kWritePer) {
+        unsigned long long rc[kWritePer], z[kWritePer];
+#pragma unroll
+        for (uint32_t u = 0; u < kWritePer; ++u) {
+            const uint32_t i = b + ln + 64 * u;
+            rc[u] = i < r1 ? a.rec[i] : 0ULL;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kWritePer; ++u) {
+            const uint32_t i = b + ln + 64 * u;
+            z[u] = i < r1 && (uint32_t)rc[u] < a.n_changes ? a.dz[(uint32_t)rc[u]] : 0ULL;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kWritePer; ++u) {
+            const uint32_t i = b + ln + 64 * u;
+            if (i < r1) {
+                if ((uint32_t)rc[u] >= a.n_changes) atomicOr(a.bad, kBadUnplaced);  // never for found targets
+                const uint32_t zz = (uint32_t)z[u];
+                const uint32_t off = (uint32_t)(rc[u] >> 32) & 0xFFFFu, old = (uint32_t)(rc[u] >> 48);
+                const int32_t delta = (int32_t)(zz >> 1) ^ -(int32_t)(zz & 1);
+                const uint32_t nu = (uint32_t)((int32_t)old + delta) & 0xFFFF;
+                if (off < extent) base[off] = (uint16_t)nu;
+                d += (uint64_t)((int64_t)nu - (int64_t)old) * weight(first + off);
+                const uint32_t eo = (old >> 7) & 0xFF, en = (nu >> 7) & 0xFF;
+                if (eo != en && h) {  // the element moves between exponent counts of its slab
+                    atomicSub(&h[eo], 1u);
+                    atomicAdd(&h[en], 1u);
+                }
+            }
+        }
+    }
+    d = wave_sum(d);
+    if (ln == 0) {
+        a.sdelta[tau] = d;
+        a.done[tau] = r1 - r0;
+    }
 }
 
 // One window of one slab: exponents [kfirst, kfirst + kWin), or from the slab's lowest exponent with
@@ -1580,7 +1678,10 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
     }
     for (int o = 32; o > 0; o >>= 1) klo = min(klo, (uint32_t)__shfl_xor(klo, o, 64));
     const uint32_t kbase = kfirst < 256 ? kfirst : klo;
-    if (kbase >= 256) return;  // no targets in this slab
+    if (kbase >= 256) {  // no targets in this slab: nothing to write, a checksum delta of zero
+        if (kfirst == 256 && ln == 0) a.sdelta[tau] = 0;
+        return;
+    }
     // the window's records follow the slab's records of lower exponents (other windows)
     uint32_t below = 0;
 #pragma unroll
@@ -1670,8 +1771,11 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
         for (uint32_t i = ln; i < (kWin + kSpare) * kSelCopies; i += 64) S.cnt[i] = 0;
         wave_fence();
         const uint32_t c_first = inf.x + inf.z, c_end = inf.y + inf.z;  // change indices
-        if (in_lds) select_slab<CAP, true>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, jbase);
-        else select_slab<CAP, false>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, jbase);
+        const uint32_t j = __builtin_amdgcn_readfirstlane(jbase);  // uniform: kept in a scalar register
+        const uint32_t jend = in_lds ? select_slab<CAP, true>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j)
+                                     : select_slab<CAP, false>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j);
+        // a slab streamed once (its first window is its only one) is written now
+        if (kfirst == 256 && !a.multi[tau]) write_through(a, td, tau, local_tile, j, jend);
     }
 }
 
@@ -1711,10 +1815,11 @@ constexpr uint32_t kVerifyPer = 4;  // records per thread with their loads in fl
 __global__ __launch_bounds__(256) void k_verify(SlabArgs a) {
     __shared__ unsigned long long sh[4];
     const uint32_t tau = blockIdx.x, tid = threadIdx.x;
-    if (*a.bad) {  // positions were not computed: deltas of zero, so the verdict is deterministic
+    if (*a.bad) {  // positions were not all computed: deltas of zero, so the verdict is deterministic
         if (tid == 0) a.sdelta[tau] = 0;
         return;
     }
+    if (!a.multi[tau]) return;  // streamed in one window: the select pass wrote its delta
     const uint32_t r0 = a.rstart[tau], r1 = a.rstart[tau + 1];
     const TensorDesc td = a.descs[a.tile_tensor[tau]];
     const uint32_t lt = tau - td.tile_begin;
@@ -1773,20 +1878,32 @@ __global__ __launch_bounds__(256) void k_verdict(uint32_t n, const unsigned long
     if (threadIdx.x == 0) *ok = (miss == 0 && *bad == 0) ? 1u : 0u;
 }
 
-// The verified writes, one workgroup per slab: its records are in row order, so the stores of a
-// wavefront go to ascending addresses and changes that share a 64-byte unit of HBM are written close
-// together in time.  Nothing is written unless the device's verdict is ok.
-__global__ __launch_bounds__(256) void k_scatter(SlabArgs a) {
-    if (!*a.ok) return;
-    const uint32_t tau = blockIdx.x;
-    const uint32_t r0 = a.rstart[tau], r1 = a.rstart[tau + 1];
-    const TensorDesc td = a.descs[a.tile_tensor[tau]];
-    const uint64_t first = (uint64_t)(tau - td.tile_begin) * a.slab;
-    const uint32_t extent = (uint32_t)min64(a.slab, td.numel - first);  // offsets of verified records lie below
-    uint16_t *const base = td.base + first;
-    for (uint32_t i = r0 + threadIdx.x; i < r1; i += 256) {
-        const uint32_t v = a.pn[i];
-        if ((v & 0xFFFFu) < extent) base[v & 0xFFFFu] = (uint16_t)(v >> 16);
+// After the device's verdict, one workgroup per slab.  A slab with more than one window: its writes,
+// if the update verifies (its records are in row order per window, so the stores of a wavefront go to
+// ascending addresses).  A slab the select pass wrote through: if the update does not verify, its old
+// bits back from the records, so that the weights are as they were.
+__global__ __launch_bounds__(256) void k_commit(SlabArgs a, uint32_t tiles) {
+    const bool ok = *a.ok != 0;
+    for (uint32_t tau = blockIdx.x; tau < tiles; tau += gridDim.x) {
+        const bool multi = a.multi[tau] != 0;
+        if (multi != ok) continue;  // verified and written through, or not verified and never written
+        const uint32_t r0 = a.rstart[tau], r1 = multi ? a.rstart[tau + 1] : r0 + a.done[tau];
+        const TensorDesc td = a.descs[a.tile_tensor[tau]];
+        const uint64_t first = (uint64_t)(tau - td.tile_begin) * a.slab;
+        const uint32_t extent = (uint32_t)min64(a.slab, td.numel - first);  // offsets of found targets lie below
+        uint16_t *const base = td.base + first;
+        if (multi) {
+            for (uint32_t i = r0 + threadIdx.x; i < r1; i += 256) {
+                const uint32_t v = a.pn[i];
+                if ((v & 0xFFFFu) < extent) base[v & 0xFFFFu] = (uint16_t)(v >> 16);
+            }
+        } else {  // done is zero unless the select pass wrote the slab (k_locate clears it): an empty loop then
+            for (uint32_t i = r0 + threadIdx.x; i < r1; i += 256) {
+                const unsigned long long rc = a.rec[i];
+                const uint32_t off = (uint32_t)(rc >> 32) & 0xFFFFu;
+                if (off < extent) base[off] = (uint16_t)(rc >> 48);
+            }
+        }
     }
 }
 
@@ -1923,7 +2040,9 @@ void launch_select(const SelectArgs &a, uint32_t tiles, bool dense, hipStream_t 
 
 void launch_verify(const SlabArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("verify", k_verify, tiles, 256, s, a); }
 
-void launch_scatter(const SlabArgs &a, uint32_t tiles, hipStream_t s) { CRX_LAUNCH("scatter", k_scatter, tiles, 256, s, a); }
+void launch_commit(const SlabArgs &a, uint32_t tiles, hipStream_t s) {
+    CRX_LAUNCH("commit", k_commit, std::min<uint32_t>(tiles, 2048), 256, s, a, tiles);  // slabs strided over the grid
+}
 
 void launch_checksum(const uint32_t *frame, uint32_t lead, uint64_t n, uint64_t *partial, uint32_t n_parts,
                      hipStream_t s) {

@@ -253,6 +253,29 @@ def test_receiver_exponent_counts_carried_across_updates():
         codec._SLAB = old_slab
 
 
+@pytest.mark.parametrize("name", ["rl_200k", "every_element_arbitrary", "three_tensors", "edges",
+                                  "distinct_residuals_200k"])
+def test_rejected_update_leaves_the_weights_as_they_were(name):
+    """A receiver one mantissa bit away from the sender's old weights (same exponent counts, so every
+    target is found and the select pass writes it through before the verdict): the update is rejected
+    by the HIP path and by the oracle, and the weights come back bit for bit, in slabs streamed in one
+    window and in slabs streamed in several (every_element_arbitrary)."""
+    old, new = _scen()[name]
+    upd = crukx_sync.encode_update(_cuda(old), _cuda(new), {})
+    big = max(old, key=lambda k: old[k].numel())
+    recv = {k: v.clone() for k, v in old.items()}
+    flat = recv[big].view(-1).view(torch.int16)
+    flat[flat.numel() // 2] ^= 1  # lowest mantissa bit: the exponent, and so every count, is unchanged
+    ref = {k: v.clone() for k, v in recv.items()}
+    with pytest.raises(oracle.OracleCorrupt):
+        oracle.apply_update(ref, upd)
+    dev = _cuda(recv)
+    with pytest.raises(crukx_sync.CorruptUpdate):
+        crukx_sync.apply_update(dev, upd)
+    for k in recv:
+        assert torch.equal(dev[k].cpu().view(torch.int16), recv[k].view(torch.int16)), k
+
+
 @pytest.mark.parametrize("rho", [0.005, 0.02, 0.025, 0.1, 0.6, "mixed"])
 def test_change_densities_across_target_list_sizes(rho):
     """Slabs with a few hundred to tens of thousands of changes (the select pass keeps up to a fixed
