@@ -41,6 +41,11 @@ def bits16(name: str, t: torch.Tensor) -> torch.Tensor:
 
 
 _DTYPES16 = (torch.bfloat16, torch.int16)
+# The kernels index a tensor's elements and an update's changes in 32 bits: larger inputs are refused
+# with ValueError before any device work (the reference has no such limit).
+_LIMIT = 1 << 32
+_TOO_LONG = "tensors of 2^32 or more elements are not supported"
+_TOO_MANY = "2^32 or more changes in one update are not supported"
 
 
 def _check16(name: str, t) -> torch.Tensor:
@@ -67,6 +72,8 @@ def _hip_device(dev: torch.device) -> torch.device:
 def checksum(a: torch.Tensor) -> int:
     """sum(u_i * w_i) mod 2^64 over the uint16 bits u_i, w_i = splitmix64(i) | 1 (codec.py:61-68)."""
     a = bits16("tensor", a)
+    if a.numel() >= _LIMIT:
+        raise ValueError(_TOO_LONG)
     dev = _hip_device(a.device)
     if a.device != dev:
         a = a.to(dev)
@@ -243,6 +250,8 @@ def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
             a, b = _check16(name, a), _check16(name, b)  # raise, or pass tensor subclasses
         if a.shape != b.shape:
             raise ValueError(f"{name}: old and new differ in shape")
+        if a.numel() >= _LIMIT:
+            raise ValueError(f"{name}: {_TOO_LONG}")
         A.append(a)
         B.append(b)
     src = _device_of(A + B, "all tensors must be on one device")
@@ -350,7 +359,11 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
             t = _check16(name, t)  # raises, or passes a tensor subclass
         if t.numel() != numel:
             raise ValueError(f"{name}: update is for {numel} elements, receiver has {t.numel()}")
+        if numel >= _LIMIT:
+            raise ValueError(f"{name}: {_TOO_LONG}")
         targets.append(t)
+    if u.total_changes >= _LIMIT:
+        raise ValueError(_TOO_MANY)
     src = _device_of(targets, "all updated tensors must be on one device")
     dev = _hip_device(src)
     staged = [a.to(dev) for a in targets] if src != dev else targets

@@ -92,23 +92,40 @@ def test_hostile_headers_fail_in_parse():
             crukx_sync.apply_update({"w": a.clone()}, h)
 
 
-def test_hostile_counts_are_rejected_before_allocating():
-    out = bytearray(b"CRXS\x02")
-    wire.write_varint(out, 1)
-    out += b"\x00\x01\x02\x01"
-    wire.write_varint(out, 1)
-    wire.write_varint(out, 1)
-    out += b"w"
-    wire.write_varint(out, 1 << 22)
-    out += bytes(8)
-    wire.write_varint(out, 1)
-    out += b"\x00"
-    wire.write_varint(out, 1 << 22)
-    out += b"\x00"
-    out += bytes(4 * ((1 << 22) // 256))
-    wire.write_varint(out, 0)
-    with pytest.raises(crukx_sync.CorruptUpdate):
-        crukx_sync.apply_update({"w": torch.zeros(1 << 22, dtype=torch.int16)}, bytes(out))
+def test_a_count_the_block_table_cannot_back_is_refused_by_the_parser():
+    """A group claiming all 2^22 elements of a tensor, with zero-bit blocks: the block table alone
+    refutes it (two bits per change at least), so nothing is sized by the count."""
+    n = 1 << 22
+    u = wire.Update([wire.Table(0, [0], [1])], [wire.TensorHeader("w", n, 0, [wire.Group(0, n, 0)])],
+                    [0] * wire.n_blocks(n), b"")
+    with pytest.raises(crukx_sync.CorruptUpdate, match="block shorter than its symbols could be"):
+        crukx_sync.apply_update({"w": torch.zeros(n, dtype=torch.int16)}, wire.serialize(u))
+
+
+def test_inputs_past_the_32_bit_limits_raise_before_device_work():
+    """Tensors of 2^32 elements and updates of 2^32 changes are refused with ValueError before any
+    device work (this host has no device: device work would raise RuntimeError).  The big tensors
+    are allocated and never touched."""
+    big = torch.empty(1 << 32, dtype=torch.int16)
+    one = wire.Update([wire.Table(0, [0], [1])], [wire.TensorHeader("w", 1 << 32, 0, [wire.Group(0, 1, 0)])],
+                      [2], b"\x00")
+    for call in (lambda: crukx_sync.apply_update({"w": big}, wire.serialize(one)),
+                 lambda: crukx_sync.encode_update({"w": big}, {"w": big}),
+                 lambda: codec.checksum(big)):
+        with pytest.raises(ValueError, match=r"2\^32 or more elements"):
+            call()
+    del big
+    # 2^32 changes over two tensors of 2^31 elements: 2^23 blocks of 512 bits each (two bits a change)
+    half = 1 << 31
+    nb = wire.n_blocks(half)
+    g = wire.Group(0, half, 0)
+    u = wire.Update([wire.Table(0, [0], [1])], [wire.TensorHeader("a", half, 0, [g]), wire.TensorHeader("b", half, 0, [g])],
+                    [512] * (2 * nb), bytes(2 * nb * 64))
+    upd = wire.serialize(u)
+    del u
+    recv = {"a": torch.empty(half, dtype=torch.int16), "b": torch.empty(half, dtype=torch.int16)}
+    with pytest.raises(ValueError, match=r"2\^32 or more changes"):
+        crukx_sync.apply_update(recv, upd)
 
 
 @pytest.mark.parametrize("name", ["rl_200k", "many_tensors", "slab_4097", "extreme", "three_tensors"])

@@ -2,12 +2,13 @@
 
 The oracle is the parity checker for the HIP path, so it is pinned here first: SplitMix64's
 published seed-0 outputs, the vectors the reference itself wrote (tests/golden/make_golden.py),
-Kraft/prefix properties, hand-built hostile updates (the reference's tests/test_roundtrip.py
-cases), and the single-byte-flip invariant.
+Kraft/prefix properties, the malformed updates of the reference's tests (as data, in
+tests/golden/hostile_headers.json), and the single-byte-flip invariant.
 """
 
 import hashlib
 import json
+import os
 
 import numpy as np
 import pytest
@@ -136,29 +137,10 @@ def test_chained_updates_with_caches(golden, chain):
     assert send == recv
 
 
-def _varint(v):
-    out = bytearray()
-    while v >= 0x80:
-        out.append((v & 0x7F) | 0x80)
-        v >>= 7
-    out.append(v)
-    return bytes(out)
-
-
 def hostile_updates():
-    """The hand-built malformed updates of the reference's tests (tests/test_roundtrip.py:109-135)."""
-    def upd(tables, tail):
-        return b"CRXS\x02" + tables + _varint(1) + _varint(1) + b"w" + _varint(100) + bytes(8) + tail
-    one = b"\x01\x00\x01\x02\x01"
-    return [
-        upd(b"\x01\x00" + b"\xff" * 9 + b"\x7f", b""),                 # varint >= 2^63
-        upd(one, b"\x01\x00" + b"\x01\x00" + _varint(1 << 62) + b"\x00"),  # huge count
-        upd(one, b"\x01\x00\x05\x1f"),                                  # rice_r = 31
-        upd(one, b"\x00"),                                              # zero groups
-        upd(b"\x01\x00\x02\x01\x01\x02\x01", b""),                      # Kraft overflow
-        upd(one, b"\x02\x00\x05\x00\x00\x05\x00"),                      # duplicate exponent
-        upd(b"\x01\x00\x01\x02\x01", b"\x01\x07\x05\x00"),              # group without a table
-    ]
+    """The malformed updates of the reference's own tests, as data (tests/golden/hostile_headers.json)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "hostile_headers.json")
+    return [bytes.fromhex(c["hex"]) for c in json.load(open(path))["cases"]]
 
 
 def test_hostile_headers_are_rejected():
