@@ -15,7 +15,8 @@ import torch
 
 from .wire import CorruptUpdate
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcrukx_hip.so")
+# the in-tree build, or another build of the library named by CRX_LIBRARY (e.g. to compare versions)
+LIB_PATH = os.environ.get("CRX_LIBRARY") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcrukx_hip.so")
 ABI_VERSION = 1
 OK, CORRUPT, INVALID, DEVICE, NOMEM = 0, 1, 2, 3, 4
 
