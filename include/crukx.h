@@ -21,8 +21,9 @@
  *     keeps until the process ends.  Copies of an update's bytes between device memory and
  *     pageable host memory go through 64 MiB of pinned buffers (allocated once per process) on up
  *     to four threads that the call starts and joins.  Work runs on `stream` (a hipStream_t).
- *     Results are final on return; crx_apply's writes (gated on the device by the verdict) and
- *     crx_encoded_write's device copies are left ordered on `stream`, so the buffers `alloc`
+ *     Results are final on return; crx_apply's last writes (or the undoing of its writes, as the
+ *     device's verdict decides) and crx_encoded_write's device copies are left ordered on `stream`,
+ *     so the buffers `alloc`
  *     handed out must stay usable by work already on `stream` after the call (a stream-ordered
  *     allocator such as torch's caching allocator does this).  Everything else is complete on
  *     return.
@@ -93,17 +94,22 @@ uint64_t crx_update_total_changes(const crx_update *u);
 /* ------------------------------------------------------------------ apply (device)
  * Replaces codec.apply (src/crukx_sync/codec.py:578-717) including the block decoder
  * (codec.py:504-575, _triton.py:33-106): decode every block, locate every change in the stable
- * exponent order of the receiver's old weights, verify each tensor's checksum, and only then
- * write.  `targets[i]` is the receiver tensor for update tensor i (crx_update_tensor order) with
- * `numels[i]` elements; `has_cache[i]`/`cache_vals[i]` give a trusted old checksum (else one is
- * computed from the weights).  `payload_dev` is NULL to upload the payload (and block table) from
- * the parsed host bytes, or the address of the payload inside a device-resident copy of the whole
- * update (the block table, which precedes the payload, is read from there too).  On CRX_CORRUPT,
- * CRX_INVALID and CRX_NOMEM nothing is written; on CRX_OK the writes are enqueued on `stream` (later
- * work on it sees them).  CRX_DEVICE (a HIP runtime error) leaves the weights unspecified: the
- * writes are enqueued behind the device's own verdict before the host has read it, so a runtime
- * error after that point cannot tell whether they ran.  Treat the weights, and any checksum cached
- * for them, as unknown then.
+ * exponent order of the receiver's old weights and verify each tensor's checksum; the weights end
+ * written only if the update verifies, as with the reference's verify-then-write (codec.py:703-707).
+ * The pass that locates the changes writes most of them as it goes, before the verdict; a kernel
+ * after the device's verdict makes the remaining writes if the update verifies, and otherwise puts
+ * the old bits back (from the located changes), so later work on `stream` sees either all of the
+ * update or none of it.  `targets[i]` is the receiver tensor for update tensor i (crx_update_tensor
+ * order) with `numels[i]` elements (below 2^32; the update's changes too: CRX_INVALID otherwise);
+ * the tensors must not overlap.  `has_cache[i]`/`cache_vals[i]` give a trusted old checksum (else
+ * one is computed from the weights).  `payload_dev` is NULL to upload the payload (and block table)
+ * from the parsed host bytes, or the address of the payload inside a device-resident copy of the
+ * whole update (the block table, which precedes the payload, is read from there too).  On
+ * CRX_INVALID and CRX_NOMEM nothing is written; on CRX_CORRUPT the weights end as they were (for a
+ * checksum mismatch, after the undo enqueued on `stream`); on CRX_OK the remaining writes are
+ * enqueued on `stream`.  CRX_DEVICE (a HIP runtime error) leaves the weights unspecified: some writes
+ * may have run and their undo may not.  Treat the weights, and any checksum cached for them, as
+ * unknown then.
  * `*changed` receives the number of changed elements. */
 int32_t crx_apply(const crx_update *u, const uint8_t *payload_dev, uint16_t *const *targets,
                   const uint64_t *numels, const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab,
@@ -118,7 +124,7 @@ int32_t crx_apply(const crx_update *u, const uint8_t *payload_dev, uint16_t *con
  * the library cannot check its size, so counts recorded with another slab size read out of bounds;
  * hist_out[i] (or NULL)
  * receives the counts after this update (it may equal hist_in[i]).  On any status but CRX_OK the
- * weights are untouched but hist_out may hold partial results: discard them.  No counterpart in
+ * weights end as with crx_apply but hist_out may hold partial results: discard them.  No counterpart in
  * the reference (its analogue is the checksum cache, codec.py:457-460,713-716). */
 int32_t crx_apply_cached(const crx_update *u, const uint8_t *payload_dev, uint16_t *const *targets,
                          const uint64_t *numels, const int32_t *has_cache, const uint64_t *cache_vals,
