@@ -73,10 +73,12 @@ def encode_update_device(old: Mapping[str, torch.Tensor], new: Mapping[str, torc
 
 
 def apply_update(weights: Mapping[str, torch.Tensor], update, checksums: dict | None = None) -> UpdateStats:
-    """Write the update into `weights` in place; on any error nothing is written. `update` is the
-    bytes from encode_update or the uint8 tensor from encode_update_device. Errors are raised before
-    anything is written; the writes themselves are ordered on the current stream, like any in-place
-    torch operation on the weights."""
+    """Write the update into `weights` in place; on any error the weights end as they were. `update`
+    is the bytes from encode_update or the uint8 tensor from encode_update_device. Most changes are
+    written while they are located, before the update's checksums are verified, and put back if the
+    update does not verify; the last writes (or that undoing) are ordered on the current stream, like
+    any in-place torch operation on the weights, so later work on that stream sees all of the update
+    or none of it."""
     u = parse(update)
     with torch.no_grad():
         changed = codec.apply(weights, u, checksums)

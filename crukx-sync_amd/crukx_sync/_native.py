@@ -162,6 +162,27 @@ def u64_array(values):
     return (ctypes.c_uint64 * max(len(values), 1))(*[v & 0xFFFFFFFFFFFFFFFF for v in values])
 
 
+def view_u64(arr):
+    """A ctypes u64 array over an array.array('Q') (no copy; the array must not grow while in use)."""
+    if not len(arr):
+        arr.append(0)
+    return (ctypes.c_uint64 * len(arr)).from_buffer(arr)
+
+
+def view_ptr(arr):
+    """A ctypes pointer array over an array.array('Q') of addresses (no copy)."""
+    if not len(arr):
+        arr.append(0)
+    return (ctypes.c_void_p * len(arr)).from_buffer(arr)
+
+
+def view_i32(arr):
+    """A ctypes int32 array over an array.array('i') (no copy)."""
+    if not len(arr):
+        arr.append(0)
+    return (ctypes.c_int32 * len(arr)).from_buffer(arr)
+
+
 def i32_array(values):
     return (ctypes.c_int32 * max(len(values), 1))(*values)
 

@@ -12,6 +12,7 @@ device (there is no CPU implementation in the product, and without a HIP device 
 from __future__ import annotations
 
 import ctypes
+from array import array
 import threading
 import weakref
 from collections.abc import Mapping
@@ -241,8 +242,13 @@ def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
     names = list(old)
     if not names:
         return Update([], []), {}
+    # one pass over the tensors: checks, element counts, devices, pointers and cached checksums
     A, B = [], []
+    numels, pa, pb, vals = array("Q"), array("Q"), array("Q"), array("Q")
+    has = array("i")
+    devs = set()
     T16 = torch.Tensor
+    cg = checksums.get if checksums is not None else None
     for name in names:
         a, b = old[name], new[name]
         if (type(a) is not T16 or type(b) is not T16 or a.dtype not in _DTYPES16 or b.dtype not in _DTYPES16
@@ -250,39 +256,44 @@ def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
             a, b = _check16(name, a), _check16(name, b)  # raise, or pass tensor subclasses
         if a.shape != b.shape:
             raise ValueError(f"{name}: old and new differ in shape")
-        if a.numel() >= _LIMIT:
+        k = a.numel()
+        if k >= _LIMIT:
             raise ValueError(f"{name}: {_TOO_LONG}")
         A.append(a)
         B.append(b)
-    src = _device_of(A + B, "all tensors must be on one device")
-    dev = _hip_device(src)
+        numels.append(k)
+        devs.add(a.get_device())
+        devs.add(b.get_device())
+        pa.append(a.data_ptr())
+        pb.append(b.data_ptr())
+        c = cg(name) if cg is not None else None
+        has.append(0 if c is None else 1)
+        vals.append(0 if c is None else c & _MASK64)
+    if len(devs) == 1 and next(iter(devs)) >= 0:  # all on one GPU
+        src = dev = A[0].device
+    else:
+        src = _device_of(A + B, "all tensors must be on one device")
+        dev = _hip_device(src)
     if src != dev:
         A, B = [a.to(dev) for a in A], [b.to(dev) for b in B]
-    pa, pb = [a.data_ptr() for a in A], [b.data_ptr() for b in B]
+        pa, pb = array("Q", [a.data_ptr() for a in A]), array("Q", [b.data_ptr() for b in B])
     if any((x | y) & 3 for x, y in zip(pa, pb)):  # the kernels read 32-bit words
         A = [a if a.data_ptr() & 3 == 0 else a.clone() for a in A]
         B = [b if b.data_ptr() & 3 == 0 else b.clone() for b in B]
-        pa, pb = [a.data_ptr() for a in A], [b.data_ptr() for b in B]
-    numels = [a.numel() for a in A]
-    if checksums is None:
-        has, vals = [0] * len(names), [0] * len(names)
-    else:
-        cached = [checksums.get(n) for n in names]
-        has = [0 if c is None else 1 for c in cached]
-        vals = [0 if c is None else c & _MASK64 for c in cached]
+        pa, pb = array("Q", [a.data_ptr() for a in A]), array("Q", [b.data_ptr() for b in B])
     n = len(names)
     L = _native.lib()
     ws = _native.Workspace(dev)
     err = _native.errbuf()
     h = ctypes.c_void_p()
     with torch.cuda.device(dev):
-        rc = L.crx_encode(n, _native.ptr_array(pa), _native.ptr_array(pb), _native.u64_array(numels),
-                          _native.i32_array(has), _native.u64_array(vals), int(_SLAB),
+        rc = L.crx_encode(n, _native.view_ptr(pa), _native.view_ptr(pb), _native.view_u64(numels),
+                          _native.view_i32(has), _native.view_u64(vals), int(_SLAB),
                           _native.stream_of(dev), ws.fn, None, ctypes.byref(h), err, 512)
     ws.check()
     _native.raise_for(rc, err)
     upd = EncodedUpdate(h.value, names, dev, ws)
-    upd._numels = numels
+    upd._numels = list(numels)
     present, chk = (ctypes.c_int32 * n)(), (ctypes.c_uint64 * n)()
     L.crx_encoded_checksums(h.value, present, chk)
     new_checksums = {name: chk[t] for t, name in enumerate(names) if present[t]}
@@ -348,8 +359,11 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     names, numels, header_chk = u.headers()
     if not names:
         return 0
-    targets = []
+    # one pass over the receiver's tensors: checks, devices, versions and trusted cached checksums
+    targets, vers, devs = [], [], set()
+    has, vals = array("i"), array("Q")
     get = weights.get if isinstance(weights, dict) else None
+    cg = checksums.get if checksums is not None else None
     T16 = torch.Tensor
     for name, numel in zip(names, numels):
         t = get(name) if get is not None else (weights[name] if name in weights else None)
@@ -362,23 +376,22 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
         if numel >= _LIMIT:
             raise ValueError(f"{name}: {_TOO_LONG}")
         targets.append(t)
+        devs.add(t.get_device())
+        v = t._version
+        vers.append(v)
+        hit = cg(name) if cg is not None else None
+        ok = isinstance(hit, tuple) and hit[1] == v
+        has.append(1 if ok else 0)
+        vals.append(hit[0] & _MASK64 if ok else 0)
     if u.total_changes >= _LIMIT:
         raise ValueError(_TOO_MANY)
-    src = _device_of(targets, "all updated tensors must be on one device")
-    dev = _hip_device(src)
+    if len(devs) == 1 and next(iter(devs)) >= 0:  # all on one GPU
+        src = dev = targets[0].device
+    else:
+        src = _device_of(targets, "all updated tensors must be on one device")
+        dev = _hip_device(src)
     staged = [a.to(dev) for a in targets] if src != dev else targets
     n = len(names)
-    vers = [t._version for t in targets]
-    if checksums is not None:
-        cg = checksums.get
-        cache = []
-        for name, v in zip(names, vers):
-            hit = cg(name)
-            cache.append(hit[0] if isinstance(hit, tuple) and hit[1] == v else None)
-    else:
-        cache = [None] * n
-    has = [0 if c is None else 1 for c in cache]
-    vals = [0 if c is None else c & _MASK64 for c in cache]
     L = _native.lib()
     payload_dev = 0
     if u._dev_bytes is not None:  # the whole update in device memory: payload and block table read there
@@ -396,7 +409,7 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     if keep:
         fresh = []  # tensors without usable counts: one allocation, sliced per tensor
         with _hist_lock:
-            found = [_hist.get(id(a)) if c is not None else None for a, c in zip(targets, cache)]
+            found = [_hist.get(id(a)) if c else None for a, c in zip(targets, has)]
         for i, (a, e, v) in enumerate(zip(targets, found, vers)):
             if e is not None and e[0]() is a and e[1] == v and e[3] == slab and e[4] == dev:
                 bufs.append(e[2])
@@ -415,11 +428,10 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
                 hist_out[i] = base + 4 * at
                 at += w
     with torch.cuda.device(dev):
-        rc = L.crx_apply_cached(u.handle, payload_dev or None, _native.ptr_array([a.data_ptr() for a in staged]),
-                                _native.u64_array(numels), _native.i32_array(has),
-                                _native.u64_array(vals),
-                                _native.ptr_array(hist_in) if keep else None,
-                                _native.ptr_array(hist_out) if keep else None,
+        rc = L.crx_apply_cached(u.handle, payload_dev or None, _native.view_ptr(array("Q", [a.data_ptr() for a in staged])),
+                                _native.view_u64(array("Q", numels)), _native.view_i32(has), _native.view_u64(vals),
+                                _native.view_ptr(array("Q", hist_in)) if keep else None,
+                                _native.view_ptr(array("Q", hist_out)) if keep else None,
                                 slab, _native.stream_of(dev), ws.fn, None, ctypes.byref(changed), err, 512)
     ws.check()
     ws.release()
@@ -439,8 +451,13 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
             a.copy_(s)  # an in-place op: bumps the tensor's version
     if keep:
         with _hist_lock:
+            hg = _hist.get
             for a, buf in zip(targets, bufs):
-                _hist_store(a, buf, slab, dev)
+                e = hg(id(a))
+                if e is not None and e[2] is buf and e[0]() is a:  # the same counts: a new version only
+                    _hist[id(a)] = (e[0], a._version, buf, slab, dev, e[5])
+                else:
+                    _hist_store(a, buf, slab, dev)
     if checksums is not None:  # record the version after our own write
         checksums.update({name: (c, t._version) for name, c, t in zip(names, header_chk, targets)})
     return changed.value

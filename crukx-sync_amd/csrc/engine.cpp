@@ -546,39 +546,80 @@ struct crx_encoded {
     uint64_t payload_len = 0;
     const uint8_t *d_payload = nullptr;
     uint64_t total_changes = 0;
+    // the serialised header, built once for crx_encoded_size and crx_encoded_write (with the names it
+    // was built for: a call with other names builds it again)
+    std::mutex hdr_mu;
+    std::vector<uint8_t> hdr;
+    std::vector<std::string> hdr_names;
+    bool hdr_valid = false;
 };
 
 namespace crx {
 namespace {
 
+// LEB128 varint at p (at most 10 bytes); returns the end
+inline uint8_t *varint_at(uint8_t *p, uint64_t v) {
+    while (v >= 0x80) {
+        *p++ = (uint8_t)(v | 0x80);
+        v >>= 7;
+    }
+    *p++ = (uint8_t)v;
+    return p;
+}
+
+// The header (wire.py:64-85): magic, version, tables, then the tensors with changes.  Written through
+// a pointer into a buffer sized for the longest varints, then cut to length.
 void write_header(const crx_encoded &e, const char *const *names, const uint64_t *name_lens, std::vector<uint8_t> &out) {
-    out.clear();
-    out.insert(out.end(), {'C', 'R', 'X', 'S', kVersion});
-    put_varint(out, e.tables.size());
+    uint64_t cap = 5 + 10 + 10;
+    for (const Table &t : e.tables) cap += 1 + 10 + 11 * t.symbols.size();
+    for (int32_t t = 0; t < e.n; ++t)
+        if (e.present[t]) cap += 10 + name_lens[t] + 10 + 8 + 10 + 12 * e.groups[t].size();
+    out.resize(cap);
+    uint8_t *p = out.data();
+    *p++ = 'C', *p++ = 'R', *p++ = 'X', *p++ = 'S', *p++ = kVersion;
+    p = varint_at(p, e.tables.size());
     for (const Table &t : e.tables) {
-        out.push_back((uint8_t)t.exponent);
-        put_varint(out, t.symbols.size());
+        *p++ = (uint8_t)t.exponent;
+        p = varint_at(p, t.symbols.size());
         for (size_t k = 0; k < t.symbols.size(); ++k) {
-            put_varint(out, t.symbols[k]);
-            out.push_back(t.lengths[k]);
+            p = varint_at(p, t.symbols[k]);
+            *p++ = t.lengths[k];
         }
     }
     uint64_t n_present = 0;
     for (int32_t t = 0; t < e.n; ++t) n_present += e.present[t] ? 1 : 0;
-    put_varint(out, n_present);
+    p = varint_at(p, n_present);
     for (int32_t t = 0; t < e.n; ++t) {
         if (!e.present[t]) continue;
-        put_varint(out, name_lens[t]);
-        out.insert(out.end(), names[t], names[t] + name_lens[t]);
-        put_varint(out, e.numel[t]);
-        for (int k = 0; k < 8; ++k) out.push_back((uint8_t)(e.checksum[t] >> (8 * k)));
-        put_varint(out, e.groups[t].size());
+        p = varint_at(p, name_lens[t]);
+        std::memcpy(p, names[t], name_lens[t]);
+        p += name_lens[t];
+        p = varint_at(p, e.numel[t]);
+        for (int k = 0; k < 8; ++k) *p++ = (uint8_t)(e.checksum[t] >> (8 * k));
+        p = varint_at(p, e.groups[t].size());
         for (const Group &g : e.groups[t]) {
-            out.push_back((uint8_t)g.exponent);
-            put_varint(out, g.count);
-            out.push_back((uint8_t)g.rice);
+            *p++ = (uint8_t)g.exponent;
+            p = varint_at(p, g.count);
+            *p++ = (uint8_t)g.rice;
         }
     }
+    out.resize((uint64_t)(p - out.data()));
+}
+
+// The header for these names, copied from the handle's when that was built for the same names (a copy:
+// another thread may rebuild the handle's for other names).
+std::vector<uint8_t> header_of(crx_encoded &e, const char *const *names, const uint64_t *name_lens) {
+    std::lock_guard<std::mutex> lock(e.hdr_mu);
+    bool same = e.hdr_valid && e.hdr_names.size() == (size_t)e.n;
+    for (int32_t t = 0; same && t < e.n; ++t)
+        same = e.hdr_names[t].size() == name_lens[t] && std::memcmp(e.hdr_names[t].data(), names[t], name_lens[t]) == 0;
+    if (!same) {
+        write_header(e, names, name_lens, e.hdr);
+        e.hdr_names.assign(e.n, std::string());
+        for (int32_t t = 0; t < e.n; ++t) e.hdr_names[t].assign(names[t], name_lens[t]);
+        e.hdr_valid = true;
+    }
+    return e.hdr;
 }
 
 // Python's repr() of a str, for names quoted in messages as the reference's f-strings do: single
@@ -1285,8 +1326,7 @@ void crx_encoded_checksums(const crx_encoded *e, int32_t *present, uint64_t *che
 uint64_t crx_encoded_total_changes(const crx_encoded *e) { return e->total_changes; }
 
 uint64_t crx_encoded_size(const crx_encoded *e, const char *const *names, const uint64_t *name_lens) {
-    std::vector<uint8_t> hdr;
-    write_header(*e, names, name_lens, hdr);
+    const std::vector<uint8_t> hdr = header_of(*const_cast<crx_encoded *>(e), names, name_lens);
     std::vector<uint8_t> pl;
     put_varint(pl, e->payload_len);
     return hdr.size() + 4 * e->n_blocks + pl.size() + e->payload_len;
@@ -1296,8 +1336,8 @@ int32_t crx_encoded_write(const crx_encoded *e, const char *const *names, const 
                           int32_t dst_on_device, void *stream, char *err, uint64_t errlen) {
     return guarded(err, errlen, [&] {
         hipStream_t s = (hipStream_t)stream;
-        std::vector<uint8_t> hdr, pl;
-        write_header(*e, names, name_lens, hdr);
+        const std::vector<uint8_t> hdr = header_of(*const_cast<crx_encoded *>(e), names, name_lens);
+        std::vector<uint8_t> pl;
         put_varint(pl, e->payload_len);
         const hipMemcpyKind from_dev = dst_on_device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
         const uint64_t off_bt = hdr.size(), off_pl = off_bt + 4 * e->n_blocks, off_pay = off_pl + pl.size();

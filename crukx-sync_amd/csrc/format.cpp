@@ -91,23 +91,20 @@ bool valid_utf8(const uint8_t *s, uint64_t n) {
 
 // The sum of n little-endian u32 (block table entries), and whether any is below `lo`: plain
 // loops the compiler vectorises.
-uint64_t sum_u32(const uint8_t *p, uint64_t n) {
+// The sum of n little-endian u32 at p, and whether any of them is below lo, in one vectorised pass
+// (an AVX2 clone is chosen at load time where the host has AVX2).
+__attribute__((target_clones("avx2", "default")))
+void sum_and_any_below(const uint8_t *p, uint64_t n, uint32_t lo, uint64_t &sum, bool &below) {
     uint64_t s = 0;
-    for (uint64_t k = 0; k < n; ++k) {
-        uint32_t v;
-        std::memcpy(&v, p + 4 * k, 4);
-        s += v;
-    }
-    return s;
-}
-bool any_below(const uint8_t *p, uint64_t n, uint32_t lo) {
     uint32_t f = 0;
     for (uint64_t k = 0; k < n; ++k) {
         uint32_t v;
         std::memcpy(&v, p + 4 * k, 4);
+        s += v;
         f |= v < lo;
     }
-    return f != 0;
+    sum += s;
+    below |= f != 0;
 }
 
 inline uint64_t sat_add(uint64_t a, uint64_t b, uint64_t cap) {  // the reference's ints do not wrap
@@ -230,8 +227,7 @@ void parse(const uint8_t *data, uint64_t avail, uint64_t total, uint8_t last, Up
         for (const Group &g : t.groups) {
             changes += g.count;
             const uint64_t nb = n_blocks(g.count), full = g.count / kBlock;
-            total_bits += sum_u32(u.block_table + 4 * b, full);
-            if (any_below(u.block_table + 4 * b, full, kBlock * (2 + (uint32_t)g.rice))) short_block = true;
+            sum_and_any_below(u.block_table + 4 * b, full, kBlock * (2 + (uint32_t)g.rice), total_bits, short_block);
             if (nb > full) {
                 const uint32_t v = u.block_bits(b + full);
                 total_bits += v;
