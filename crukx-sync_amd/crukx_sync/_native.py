@@ -24,6 +24,8 @@ ALLOC_FN = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64)
 
 _lib = None
 _lock = threading.Lock()
+_meta = None
+_meta_tried = False
 
 # name -> (restype, argtypes), exactly the declarations of include/crukx.h
 _u8p, _u32p, _u64p, _i32p, _i64p = (ctypes.POINTER(t) for t in
@@ -160,6 +162,24 @@ def stream_of(device: torch.device) -> int:
 
 def u64_array(values):
     return (ctypes.c_uint64 * max(len(values), 1))(*[v & 0xFFFFFFFFFFFFFFFF for v in values])
+
+
+def tensor_meta():
+    """The batched tensor-metadata helper (crx_tensor_meta.so next to this file, built with the library),
+    or None: the Python layer then reads the same fields tensor by tensor."""
+    global _meta, _meta_tried
+    if not _meta_tried:
+        with _lock:
+            if not _meta_tried:
+                path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "crx_tensor_meta.so")
+                if os.path.exists(path):
+                    import importlib.util
+                    spec = importlib.util.spec_from_file_location("crx_tensor_meta", path)
+                    mod = importlib.util.module_from_spec(spec)
+                    spec.loader.exec_module(mod)
+                    _meta = mod
+                _meta_tried = True
+    return _meta
 
 
 def view_u64(arr):

@@ -242,6 +242,10 @@ def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
     names = list(old)
     if not names:
         return Update([], []), {}
+    fast = _encode_inputs(names, old, new, checksums)
+    if fast is not None:
+        A, B, numels, pa, pb, has, vals, dev = fast
+        return _encode_call(names, A, B, numels, pa, pb, has, vals, dev)
     # one pass over the tensors: checks, element counts, devices, pointers and cached checksums
     A, B = [], []
     numels, pa, pb, vals = array("Q"), array("Q"), array("Q"), array("Q")
@@ -277,6 +281,41 @@ def encode(old: Mapping[str, torch.Tensor], new: Mapping[str, torch.Tensor],
     if src != dev:
         A, B = [a.to(dev) for a in A], [b.to(dev) for b in B]
         pa, pb = array("Q", [a.data_ptr() for a in A]), array("Q", [b.data_ptr() for b in B])
+    return _encode_call(names, A, B, numels, pa, pb, has, vals, dev)
+
+
+def _encode_inputs(names, old, new, checksums):
+    """The encoder's inputs from the batched metadata helper, when every tensor is regular (bf16 or
+    int16, contiguous, shapes equal, under the size limit, all on one GPU); None otherwise, and the
+    checks then run tensor by tensor to raise their exact errors."""
+    M = _native.tensor_meta()
+    if M is None:
+        return None
+    A = [old[n] for n in names]
+    B = [new[n] for n in names]
+    try:
+        ma, mb = M.meta(A), M.meta(B)
+        same = M.same_shapes(A, B)
+    except (TypeError, RuntimeError):  # not all tensors
+        return None
+    n = len(names)
+    fa, fb, numels = array("i", ma[3]), array("i", mb[3]), array("Q", ma[1])
+    if not same or fa.count(3) != n or fb.count(3) != n or max(numels) >= _LIMIT:
+        return None
+    devs = set(array("i", ma[2])) | set(array("i", mb[2]))
+    if len(devs) != 1 or next(iter(devs)) < 0:
+        return None
+    if checksums is None:
+        has, vals = array("i", bytes(4 * n)), array("Q", bytes(8 * n))
+    else:
+        cached = [checksums.get(nm) for nm in names]
+        has = array("i", [0 if c is None else 1 for c in cached])
+        vals = array("Q", [0 if c is None else c & _MASK64 for c in cached])
+    return A, B, numels, array("Q", ma[0]), array("Q", mb[0]), has, vals, A[0].device
+
+
+def _encode_call(names, A, B, numels, pa, pb, has, vals, dev):
+    """crx_encode on checked inputs (A, B: the tensors on `dev`; pa, pb, numels, has, vals: packed arrays)."""
     if any((x | y) & 3 for x, y in zip(pa, pb)):  # the kernels read 32-bit words
         A = [a if a.data_ptr() & 3 == 0 else a.clone() for a in A]
         B = [b if b.data_ptr() & 3 == 0 else b.clone() for b in B]
@@ -325,6 +364,35 @@ def _hist_forget(key):
         _hist.pop(key, None)
 
 
+def _apply_inputs(names, numels, weights, checksums):
+    """The receiver's tensors, versions and trusted cached checksums from the batched metadata helper,
+    when every tensor is present and regular (bf16 or int16, contiguous, the update's element count,
+    under the size limit, all on one GPU); None otherwise, and the checks then run tensor by tensor to
+    raise their exact errors."""
+    M = _native.tensor_meta()
+    if M is None or not isinstance(weights, dict):
+        return None
+    get = weights.get
+    targets = [get(n) for n in names]
+    try:
+        m = M.meta(targets)
+    except (TypeError, RuntimeError):  # a missing name (None) or not a tensor
+        return None
+    n = len(names)
+    if array("i", m[3]).count(3) != n or array("Q", m[1]) != array("Q", numels) or max(numels) >= _LIMIT:
+        return None
+    devs = set(array("i", m[2]))
+    if len(devs) != 1 or next(iter(devs)) < 0:
+        return None
+    vers = array("Q", m[4])
+    if checksums is None:
+        return targets, vers, array("i", bytes(4 * n)), array("Q", bytes(8 * n))
+    hits = [checksums.get(nm) for nm in names]
+    ok = [isinstance(h, tuple) and h[1] == v for h, v in zip(hits, vers)]
+    return (targets, vers, array("i", [1 if o else 0 for o in ok]),
+            array("Q", [h[0] & _MASK64 if o else 0 for h, o in zip(hits, ok)]))
+
+
 def _hist_store(t, buf, slab, dev):
     """Record counts for t (the caller holds _hist_lock)."""
     key = id(t)
@@ -359,30 +427,34 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     names, numels, header_chk = u.headers()
     if not names:
         return 0
-    # one pass over the receiver's tensors: checks, devices, versions and trusted cached checksums
-    targets, vers, devs = [], [], set()
-    has, vals = array("i"), array("Q")
-    get = weights.get if isinstance(weights, dict) else None
-    cg = checksums.get if checksums is not None else None
-    T16 = torch.Tensor
-    for name, numel in zip(names, numels):
-        t = get(name) if get is not None else (weights[name] if name in weights else None)
-        if t is None:
-            raise ValueError(f"update has tensor {name!r} that the receiver does not have")
-        if type(t) is not T16 or t.dtype not in _DTYPES16 or not t.is_contiguous():
-            t = _check16(name, t)  # raises, or passes a tensor subclass
-        if t.numel() != numel:
-            raise ValueError(f"{name}: update is for {numel} elements, receiver has {t.numel()}")
-        if numel >= _LIMIT:
-            raise ValueError(f"{name}: {_TOO_LONG}")
-        targets.append(t)
-        devs.add(t.get_device())
-        v = t._version
-        vers.append(v)
-        hit = cg(name) if cg is not None else None
-        ok = isinstance(hit, tuple) and hit[1] == v
-        has.append(1 if ok else 0)
-        vals.append(hit[0] & _MASK64 if ok else 0)
+    fast = _apply_inputs(names, numels, weights, checksums)
+    if fast is not None:
+        targets, vers, has, vals = fast
+        devs = {targets[0].get_device()}
+    else:  # one pass over the receiver's tensors: checks, devices, versions and trusted cached checksums
+        targets, vers, devs = [], [], set()
+        has, vals = array("i"), array("Q")
+        get = weights.get if isinstance(weights, dict) else None
+        cg = checksums.get if checksums is not None else None
+        T16 = torch.Tensor
+        for name, numel in zip(names, numels):
+            t = get(name) if get is not None else (weights[name] if name in weights else None)
+            if t is None:
+                raise ValueError(f"update has tensor {name!r} that the receiver does not have")
+            if type(t) is not T16 or t.dtype not in _DTYPES16 or not t.is_contiguous():
+                t = _check16(name, t)  # raises, or passes a tensor subclass
+            if t.numel() != numel:
+                raise ValueError(f"{name}: update is for {numel} elements, receiver has {t.numel()}")
+            if numel >= _LIMIT:
+                raise ValueError(f"{name}: {_TOO_LONG}")
+            targets.append(t)
+            devs.add(t.get_device())
+            v = t._version
+            vers.append(v)
+            hit = cg(name) if cg is not None else None
+            ok = isinstance(hit, tuple) and hit[1] == v
+            has.append(1 if ok else 0)
+            vals.append(hit[0] & _MASK64 if ok else 0)
     if u.total_changes >= _LIMIT:
         raise ValueError(_TOO_MANY)
     if len(devs) == 1 and next(iter(devs)) >= 0:  # all on one GPU
@@ -449,15 +521,17 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     else:
         for a, s in zip(targets, staged):
             a.copy_(s)  # an in-place op: bumps the tensor's version
+    M = _native.tensor_meta()
+    after = array("Q", M.versions(targets)) if M is not None else [t._version for t in targets]
     if keep:
         with _hist_lock:
             hg = _hist.get
-            for a, buf in zip(targets, bufs):
+            for a, buf, v in zip(targets, bufs, after):
                 e = hg(id(a))
                 if e is not None and e[2] is buf and e[0]() is a:  # the same counts: a new version only
-                    _hist[id(a)] = (e[0], a._version, buf, slab, dev, e[5])
+                    _hist[id(a)] = (e[0], v, buf, slab, dev, e[5])
                 else:
                     _hist_store(a, buf, slab, dev)
     if checksums is not None:  # record the version after our own write
-        checksums.update({name: (c, t._version) for name, c, t in zip(names, header_chk, targets)})
+        checksums.update({name: (c, v) for name, c, v in zip(names, header_chk, after)})
     return changed.value

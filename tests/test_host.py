@@ -191,3 +191,26 @@ def test_no_silent_cpu_fallback():
     b[3] = 1.0
     with pytest.raises(RuntimeError, match="HIP"):
         crukx_sync.encode_update({"w": a}, {"w": b})
+
+
+def test_tensor_metadata_helper_agrees_with_the_tensors():
+    """The batched metadata helper (crukx_sync/crx_tensor_meta.so) returns what the tensors report one by
+    one: address, element count, device, dtype/contiguity flags, version; and pairwise shape equality."""
+    from array import array
+    M = _native.tensor_meta()
+    if M is None:
+        pytest.skip("the helper is built by __graft_entry__.build()")
+    base = torch.arange(100, dtype=torch.int16)
+    ts = [torch.zeros(7, dtype=torch.bfloat16), base, base[3:50], base.view(10, 10).t(), torch.zeros(5),
+          torch.ones(2, 3, dtype=torch.int16)]
+    ts[1].add_(1)  # a version counter above zero
+    ptr, numel, dev, flags, ver = M.meta(ts)
+    ptr, numel, ver = array("Q", ptr), array("Q", numel), array("Q", ver)
+    dev, flags = array("i", dev), array("i", flags)
+    for i, t in enumerate(ts):
+        assert ptr[i] == t.data_ptr() and numel[i] == t.numel() and dev[i] == t.get_device() and ver[i] == t._version
+        assert flags[i] == (1 if t.dtype in (torch.bfloat16, torch.int16) else 0) | (2 if t.is_contiguous() else 0)
+    assert array("Q", M.versions(ts)) == ver
+    assert M.same_shapes(ts, [t.clone() for t in ts]) and not M.same_shapes(ts[:2], ts[1:3])
+    with pytest.raises(TypeError):
+        M.meta([ts[0], None])
