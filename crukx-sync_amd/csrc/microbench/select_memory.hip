@@ -11,6 +11,9 @@
 //   read + 128 B lines   during the stream, every 128-byte line holding a target stored whole (all 64
 //                        lanes of the half-row), new bits for the targets, old bits for the rest
 //   read + 64 B / 32 B   the same for the 64-byte half-line or 32-byte sector holding a target
+//   read, load+2 B at end  the end-of-slab writes, each preceded by a load of its element (all the
+//                        slab's loads first), so the line is in L2 when the partial write reaches it
+//   read, xor at end     the end-of-slab writes as 32-bit atomic XORs of (old ^ new) into the word
 // Build and run: make -C crukx-sync_amd/csrc microbench && crukx-sync_amd/csrc/_build/select_memory
 #include <hip/hip_runtime.h>
 
@@ -47,7 +50,7 @@ __device__ __forceinline__ uint32_t target_at(uint32_t slab, uint32_t i) {
     return i * kStretch + h % kStretch;
 }
 
-enum Mode { kRead, kReadEndWrites, kEndWritesOnly, kLines128, kLines64, kSectors32 };
+enum Mode { kRead, kReadEndWrites, kEndWritesOnly, kLines128, kLines64, kSectors32, kReadEndLoadStore, kReadEndXor };
 
 template <int MODE>
 __global__ __launch_bounds__(64) void k_stream(uint16_t *w, uint32_t *out) {
@@ -72,7 +75,7 @@ __global__ __launch_bounds__(64) void k_stream(uint16_t *w, uint32_t *out) {
 #pragma unroll
             for (uint32_t u = 0; u < kBatch; ++u) {
                 acc = acc * 3 + (clo[u] | ((uint32_t)chi[u] << 16));
-                if (MODE >= kLines128) {
+                if (MODE >= kLines128 && MODE <= kSectors32) {
                     const uint32_t x0 = (r0 + u) * 128 + ln, x1 = x0 + 64;
                     const bool t0 = x0 < n && is_target(slab, x0), t1 = x1 < n && is_target(slab, x1);
                     const uint64_t b0 = __ballot(t0), b1 = __ballot(t1);
@@ -95,6 +98,28 @@ __global__ __launch_bounds__(64) void k_stream(uint16_t *w, uint32_t *out) {
         for (uint32_t i = ln; i < kPerSlab; i += 64) {
             const uint32_t x = target_at(slab, i);
             if (x < n) w[first + x] = (uint16_t)(acc | 1);
+        }
+    }
+    if (MODE == kReadEndLoadStore) {
+        constexpr uint32_t kPer = (kPerSlab + 63) / 64;  // targets per lane
+        uint16_t old[kPer];
+#pragma unroll
+        for (uint32_t q = 0; q < kPer; ++q) {  // every load before any store
+            const uint32_t i = ln + 64 * q, x = i < kPerSlab ? target_at(slab, i) : n;
+            old[q] = x < n ? w[first + x] : (uint16_t)0;
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < kPer; ++q) {
+            const uint32_t i = ln + 64 * q, x = i < kPerSlab ? target_at(slab, i) : n;
+            if (x < n) w[first + x] = (uint16_t)(old[q] + 1);
+        }
+    }
+    if (MODE == kReadEndXor) {
+        uint32_t *const w32 = reinterpret_cast<uint32_t *>(w);
+        for (uint32_t i = ln; i < kPerSlab; i += 64) {
+            const uint32_t x = target_at(slab, i);
+            const uint64_t e = first + x;  // the element's word and half
+            if (x < n) atomicXor(&w32[e >> 1], 1u << (16 * (uint32_t)(e & 1)));
         }
     }
     if (ln == 0) out[slab] = acc;
@@ -139,6 +164,10 @@ int main() {
     std::printf("read + 64 B half-lines %7.3f ms\n", run<kLines64>(w, out));
     std::fflush(stdout);
     std::printf("read + 32 B sectors    %7.3f ms\n", run<kSectors32>(w, out));
+    std::fflush(stdout);
+    std::printf("read, load+2 B at end  %7.3f ms\n", run<kReadEndLoadStore>(w, out));
+    std::fflush(stdout);
+    std::printf("read, xor at end       %7.3f ms\n", run<kReadEndXor>(w, out));
     std::fflush(stdout);
     CHECK(hipDeviceSynchronize());
     CHECK(hipFree(w));
