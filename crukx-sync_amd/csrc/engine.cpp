@@ -1013,11 +1013,12 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     h2d(tchg, tensor_chg.data(), T + 1, s);
     uint32_t *lb = ar.get<uint32_t>((uint64_t)(tiles + 1) * 256);  // row tiles: read, never used
 
-    // pass A: slabs of tensors without cached counts are streamed (their counts, and old checksums
-    // when cold); cached counts are read by the scan in place (copied only to a separate hist_out)
+    // pass A: slabs of tensors without cached counts are streamed for their counts (and the even rows
+    // of old checksums not cached: the select pass sums the rest as it streams the weights); cached
+    // counts are read by the scan in place (copied only to a separate hist_out)
     std::vector<uint32_t> hist_list;
     for (const TensorDesc &d : L.descs) {
-        const bool cached = d.hist_in && !d.cold;
+        const bool cached = d.hist_in != nullptr;
         if (!cached || (d.hist_out && d.hist_out != d.hist_in))
             for (uint32_t i = 0; i < d.n_tiles; ++i) hist_list.push_back(d.tile_begin + i);
     }
@@ -1031,7 +1032,6 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
         launch_hist(ha, (uint32_t)hist_list.size(), s);
     }
     launch_scan_tables(d_descs, hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, sizes, s);
-    launch_tensor_sums(d_descs, T, full, t_full, s);
     fork.join();
     hc.mark("apply_pass_a");
 
@@ -1059,14 +1059,17 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     h2d(d_has, has.data(), T, s);
     SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, rec, rstart, tchg, bad, more,
                   n_more, (uint32_t)std::min<uint64_t>(1024, (uint64_t)kSelMoreWindows * tiles), dz, sdelta, multi,
-                  done, (uint32_t)C};
+                  done, (uint32_t)C, full};
     launch_locate(sa, tiles, s);
     // slabs streamed in one window are written through by the select pass, before the verdict: the
     // commit below undoes those writes if the update does not verify
-    launch_select(sa, tiles, C > kSelectDenseTargets * tiles, s);
+    bool any_cold = false;
+    for (const TensorDesc &d : L.descs) any_cold |= d.cold != 0;
+    launch_select(sa, tiles, C > kSelectDenseTargets * tiles, any_cold, s);
     SlabArgs sla{d_descs, sd.tile_tensor, slab, rstart, rec, dz, pn, sdelta, bad, nullptr, (uint32_t)C, multi, done};
     launch_verify(sla, tiles, s);
     launch_tensor_sums(d_descs, T, sdelta, tdelta, s);
+    launch_tensor_sums(d_descs, T, full, t_full, s);  // the select pass summed the cold slabs
     // the verdict on the device too, and the commit behind it (the remaining writes if the update
     // verifies, the undoing of the select pass's if not); the host waits for the verdict's data only
     launch_verdict(T, reinterpret_cast<const unsigned long long *>(tdelta), t_full, d_has, d_cached, d_want, bad, ok,

@@ -82,7 +82,7 @@ struct HistArgs {
     const uint32_t *tile_tensor;
     uint32_t n_tensors, slab;
     uint32_t *hall;                 // [tiles][256]
-    uint64_t *full;                 // [tiles]
+    uint64_t *full;                 // [tiles] cold slabs: the even rows' part of the old checksum
     const uint32_t *list;           // the slabs to process (one workgroup each), or null for all
 };
 
@@ -165,6 +165,10 @@ struct SelectArgs {
     uint8_t *multi;                 // [tiles] the slab has more than one window (k_locate)
     uint32_t *done;                 // [tiles] records written through by the select pass (zeroed by k_locate)
     uint32_t n_changes;
+    // [tiles] each slab's weighted sum for its tensor's checksum when the tensor is cold (no cached
+    // checksum), else 0: completed by the slab's first window, which reads the weights before any
+    // write (to the histogram pass's sum of the even rows, when that pass streamed the slab)
+    uint64_t *full;
 };
 
 struct SlabArgs {                   // per-slab kernels over the select pass's records (one workgroup per slab)
@@ -245,9 +249,10 @@ void launch_tile_map(const TensorDesc *descs, uint32_t n_tensors, uint32_t *tile
 // the most windows a slab can need after its first.
 constexpr uint32_t kSelWin = 64;
 constexpr uint32_t kSelMoreWindows = 256 / kSelWin - 1;
-// dense: the larger LDS target list (for updates averaging over kSelectDenseTargets changes per slab)
+// dense: the larger LDS target list (for updates averaging over kSelectDenseTargets changes per slab);
+// any_cold: some tensor has no cached checksum (its slabs' sums go to SelectArgs::full)
 constexpr uint64_t kSelectDenseTargets = 800;
-void launch_select(const SelectArgs &a, uint32_t tiles, bool dense, hipStream_t s);
+void launch_select(const SelectArgs &a, uint32_t tiles, bool dense, bool any_cold, hipStream_t s);
 // New values and checksum deltas of the records of slabs with more than one window (one workgroup
 // per slab; the select pass did the others' already).
 void launch_verify(const SlabArgs &a, uint32_t tiles, hipStream_t s);

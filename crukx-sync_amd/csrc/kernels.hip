@@ -360,18 +360,43 @@ __global__ __launch_bounds__(64) void k_enc_rank(EncRankArgs a) {
 
 // ================================================================== apply: histogram pass
 // 8 copies of every exponent's count, copy = lane & 7, so the atomics of a row rarely collide.  Lanes
-// outside the slab count into exponent slot 256.  16 copies collide less (a counting-only pass: 5.85
-// against 5.57 TB/s), but the cold pass, which also sums the old checksum, is bound by that
-// arithmetic and gains from the occupancy half the LDS allows (7.6e9 weights: 6.9 -> 6.3 ms); the
-// counting-only pass runs only for tensors with a cached checksum and no cached counts.
+// outside the slab count into exponent slot 256.  The old weights' checksum, when not cached, is
+// needed only by the verdict; it is arithmetic-bound and this pass is bound by its atomics, the select
+// pass by memory, so the two split it: this pass sums a slab's even rows, the select pass its odd
+// rows (all of them when this pass does not stream the slab: its counts are cached).
 constexpr uint32_t kHistCopies = 8;
+
+// The weighted sum of a cold slab's weights for its tensor's checksum (codec.py:61-68), over its odd
+// rows (odd) or all of them: one stream of the slab, for slabs the select pass does not stream (no
+// targets, or an update already rejected).
+__device__ uint64_t cold_sum(const TensorDesc &td, const Slab &sl, bool odd) {
+    const uint32_t ln = lane();
+    const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
+    WeightedSum acc;
+    // z = (index + 1) * golden of this lane's first element in the current row
+    uint64_t z = (uint64_t)(2 * (int64_t)sl.first - (int64_t)td.lead + 2 * ln + 1) * kGolden;
+    stream_rows<kScanRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
+        uint32_t v = o;
+        if (!row_full(sl, r)) {
+            const uint32_t f = r * kRow + 2 * ln;
+            if (f < sl.f_lo || f >= sl.f_hi) v &= 0xFFFF0000u;
+            if (f + 1 < sl.f_lo || f + 1 >= sl.f_hi) v &= 0xFFFFu;
+        }
+        if (!odd || (r & 1u)) {
+            acc.add(v & 0xFFFF, mix_weight(z));
+            acc.add(v >> 16, mix_weight(z + kGolden));
+        }
+        z += (uint64_t)kRow * kGolden;
+    });
+    return wave_sum(acc.total());
+}
 
 template <bool COLD>
 __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau, const Slab &sl, uint32_t *hall) {
     const uint32_t ln = lane(), rep = ln & (kHistCopies - 1);
     const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
-    WeightedSum full;  // cold: checksum of the weights
-    // cold: z = (index + 1) * golden of this lane's first element in the current row
+    WeightedSum full;  // COLD: the even rows' part of the old checksum
+    // COLD: z = (index + 1) * golden of this lane's first element in the current row
     uint64_t z = COLD ? (uint64_t)(2 * (int64_t)sl.first - (int64_t)td.lead + 2 * ln + 1) * kGolden : 0;
     stream_rows<kScanRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
         const uint32_t f = r * kRow + 2 * ln;
@@ -389,8 +414,10 @@ __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau,
         atomicAdd(&hall[k0 * kHistCopies + rep], 1u);
         atomicAdd(&hall[k1 * kHistCopies + rep], 1u);
         if (COLD) {
-            full.add(v & 0xFFFF, mix_weight(z));
-            full.add(v >> 16, mix_weight(z + kGolden));
+            if (!(r & 1u)) {
+                full.add(v & 0xFFFF, mix_weight(z));
+                full.add(v >> 16, mix_weight(z + kGolden));
+            }
             z += (uint64_t)kRow * kGolden;
         }
     });
@@ -406,15 +433,17 @@ __device__ void hist_slab(const HistArgs &a, const TensorDesc &td, uint32_t tau,
         a.hall[(uint64_t)tau * 256 + k] = sum;
         if (out) out[k] = sum;
     }
-    const uint64_t facc = wave_sum(full.total());
-    if (ln == 0) a.full[tau] = facc;
+    if (COLD) {
+        const uint64_t facc = wave_sum(full.total());
+        if (ln == 0) a.full[tau] = facc;
+    }
 }
 
 __global__ __launch_bounds__(64) void k_hist(HistArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t hall[257 * kHistCopies];
     const uint32_t tau = a.list ? a.list[blockIdx.x] : blockIdx.x;
     const TensorDesc td = a.descs[a.tile_tensor[tau]];
-    if (td.hist_in && !td.cold) {  // counts recorded by the previous update: copied to a separate hist_out
+    if (td.hist_in) {  // counts recorded by the previous update: copied to a separate hist_out
         const uint64_t at = (uint64_t)(tau - td.tile_begin) * 256;
         for (uint32_t k = lane(); k < 256; k += 64) td.hist_out[at + k] = td.hist_in[at + k];
         return;
@@ -435,7 +464,7 @@ constexpr uint32_t kScanBatch = 32;  // = kScanTiles: a chunk in one batch
 // Per-slab counts of slab t of a chunk's tensor: the receiver's cached counts when the apply uses
 // them (the histogram pass skipped those slabs), else the table being scanned.
 __device__ __forceinline__ const uint32_t *scan_src(const TensorDesc &td, const uint32_t *h, uint32_t t) {
-    return (td.hist_in && !td.cold) ? td.hist_in + (uint64_t)(t - td.tile_begin) * 256 : h + (uint64_t)t * 256;
+    return td.hist_in ? td.hist_in + (uint64_t)(t - td.tile_begin) * 256 : h + (uint64_t)t * 256;
 }
 
 __global__ __launch_bounds__(256) void k_scan_sum(const TensorDesc *descs, const uint32_t *h, const ScanChunk *ch,
@@ -1474,13 +1503,16 @@ __device__ __forceinline__ void stream_halves(const Slab &sl, const Rsrc &src, B
     }
 }
 
-template <uint32_t CAP, bool LDS_LIST>
+template <uint32_t CAP, bool LDS_LIST, bool COLD>
 __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase, SelectLds<CAP> &S,
                             uint32_t nxt, uint32_t ci, const uint32_t cend, const uint32_t jofs, const uint32_t pre_k,
-                            uint32_t j) {
+                            uint32_t j, uint64_t &fsum) {
     // lane e, for window exponent e: nxt = slab rank of its next target (kFar: none left), ci = that
     // target's change index, cend = the end of its changes, jofs = change index - list index (LDS
     // list), pre_k = its count before the slab (HBM list).  j (uniform): the window's next record.
+    // COLD: the stream also sums the slab's weights for the tensor's checksum (codec.py:61-68) into
+    // fsum, as it reads them before any write (the verdict's input when no checksum is cached): the odd
+    // rows when the histogram pass streamed the slab (it summed the even ones), else every row.
     const uint32_t ln = lane();
     // Per 16-bit half, an element's key is (window index << 7) + (its lane's copy << 5): the counter's
     // byte offset << kCntShift, so one shift gives the address.  Exponents below the window wrap past
@@ -1503,13 +1535,31 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
     };
 
     uint32_t prev = 0;  // exponent ln's count before the row
+    WeightedSum cs;     // COLD: the checksum sum
+    const bool odd = td.hist_in == nullptr;  // COLD: the histogram pass summed the even rows
+    // COLD: z = (index + 1) * golden of this lane's low element in the current row (its high element: + 64)
+    uint64_t z = COLD ? (uint64_t)(2 * (int64_t)sl.first - (int64_t)td.lead + ln + 1) * kGolden : 0;
     stream_halves<kSelectRows, kStreamNT>(sl, slab_rsrc(td.frame, sl), [&](uint32_t r, uint32_t o) {
         // both elements' keys; outside the window or the slab: the spare's
         u16x2 c = __builtin_elementwise_min(as16(o & 0x7F807F80u) - as16(kb), as16(sp));
         const uint32_t f = r * kRow + ln;  // the low element's offset; the high one's is f + 64
+        uint32_t v = o;                    // COLD: the slab's own elements (zero outside it)
         if (!row_full(sl, r)) {
-            if (f < sl.f_lo || f >= sl.f_hi) c.x = as16(sp).x;
-            if (f + 64 < sl.f_lo || f + 64 >= sl.f_hi) c.y = as16(sp).y;
+            if (f < sl.f_lo || f >= sl.f_hi) {
+                c.x = as16(sp).x;
+                v &= 0xFFFF0000u;
+            }
+            if (f + 64 < sl.f_lo || f + 64 >= sl.f_hi) {
+                c.y = as16(sp).y;
+                v &= 0xFFFFu;
+            }
+        }
+        if (COLD) {  // the odd rows, or all of them when the histogram pass did not stream the slab
+            if (!odd || (r & 1u)) {
+                cs.add(v & 0xFFFF, mix_weight(z));
+                cs.add(v >> 16, mix_weight(z + 64 * kGolden));
+            }
+            z += (uint64_t)kRow * kGolden;
         }
         const uint32_t key = __builtin_bit_cast(uint32_t, c);
         atomicAdd(reinterpret_cast<uint32_t *>(cnt + ((key & 0xFFFFu) >> kCntShift)), 1u);
@@ -1584,6 +1634,7 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
     // every target of this window's exponents is found once its rank is passed: one still pending
     // lies past the slab's elements of its exponent (never so when the local indices were in range)
     if (ci < cend) atomicOr(a.bad, kBadUnplaced);
+    if (COLD) fsum = wave_sum(cs.total());
     return j;  // past the window's last record
 }
 
@@ -1647,8 +1698,9 @@ __device__ void write_through(const SelectArgs &a, const TensorDesc &td, uint32_
 
 // One window of one slab: exponents [kfirst, kfirst + kWin), or from the slab's lowest exponent with
 // targets when kfirst is 256.  The slab's targets are the group changes [lb(slab), lb(next slab)) of
-// each exponent (to the group's end for a tensor's last slab).
-template <uint32_t CAP>
+// each exponent (to the group's end for a tensor's last slab).  ANYCOLD: some tensor of the update has
+// no cached checksum (otherwise the checksum summing is left out of the kernel's code).
+template <uint32_t CAP, bool ANYCOLD>
 __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau, uint32_t kfirst, SelectLds<CAP> &S) {
     const uint32_t ln = lane();
     const uint32_t t = a.tile_tensor[tau];
@@ -1682,7 +1734,14 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
     for (int o = 32; o > 0; o >>= 1) klo = min(klo, (uint32_t)__shfl_xor(klo, o, 64));
     const uint32_t kbase = kfirst < 256 ? kfirst : klo;
     if (kbase >= 256) {  // no targets in this slab: nothing to write, a checksum delta of zero
-        if (kfirst == 256 && ln == 0) a.sdelta[tau] = 0;
+        if (kfirst == 256) {
+            const bool cold = ANYCOLD && td.cold;
+            const uint64_t f = cold ? cold_sum(td, slab_of(td, local_tile, a.slab), !td.hist_in) : 0;
+            if (ln == 0) {
+                a.sdelta[tau] = 0;
+                a.full[tau] = f + (cold && !td.hist_in ? a.full[tau] : 0);
+            }
+        }
         return;
     }
     // the window's records follow the slab's records of lower exponents (other windows)
@@ -1775,26 +1834,44 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
         wave_fence();
         const uint32_t c_first = inf.x + inf.z, c_end = inf.y + inf.z;  // change indices
         const uint32_t j = __builtin_amdgcn_readfirstlane(jbase);  // uniform: kept in a scalar register
-        const uint32_t jend = in_lds ? select_slab<CAP, true>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j)
-                                     : select_slab<CAP, false>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j);
+        // a slab's first window sums its weights for a cold tensor's checksum
+        const bool cold = ANYCOLD && kfirst == 256 && td.cold;
+        uint64_t fsum = 0;
+        uint32_t jend;
+        if (in_lds)
+            jend = cold ? select_slab<CAP, true, ANYCOLD>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j, fsum)
+                        : select_slab<CAP, true, false>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j, fsum);
+        else
+            jend = cold ? select_slab<CAP, false, ANYCOLD>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j, fsum)
+                        : select_slab<CAP, false, false>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j, fsum);
+        if (kfirst == 256 && ln == 0) a.full[tau] = fsum + (cold && !td.hist_in ? a.full[tau] : 0);
         // a slab streamed once (its first window is its only one) is written now
         if (kfirst == 256 && !a.multi[tau]) write_through(a, td, tau, local_tile, j, jend);
     }
 }
 
 // Blocks [0, n_front): the first n_front windows k_locate listed (started first, so they overlap
-// the rest); then one block per slab for its first window.
-template <uint32_t CAP>
+// the rest); then one block per slab for its first window.  ANYCOLD as for select_window.
+template <uint32_t CAP, bool ANYCOLD>
 __global__ __launch_bounds__(64) void k_select(SelectArgs a) {
     __shared__ __attribute__((aligned(16))) SelectLds<CAP> S;
-    if (*a.bad) return;
     const uint32_t b = blockIdx.x;
+    if (*a.bad) {  // positions will not be used; a cold slab's checksum still feeds the verdict
+        if (b >= a.n_front) {
+            const uint32_t tau = b - a.n_front;
+            const TensorDesc td = a.descs[a.tile_tensor[tau]];
+            const bool cold = ANYCOLD && td.cold;
+            const uint64_t f = cold ? cold_sum(td, slab_of(td, tau - td.tile_begin, a.slab), !td.hist_in) : 0;
+            if (lane() == 0) a.full[tau] = f + (cold && !td.hist_in ? a.full[tau] : 0);
+        }
+        return;
+    }
     if (b < a.n_front) {
         if (b >= *a.n_more) return;
         const uint2 m = a.more[b];
-        select_window(a, m.x, m.y, S);
+        select_window<CAP, ANYCOLD>(a, m.x, m.y, S);
     } else {
-        select_window(a, b - a.n_front, 256u, S);
+        select_window<CAP, ANYCOLD>(a, b - a.n_front, 256u, S);
     }
 }
 
@@ -1806,7 +1883,7 @@ __global__ __launch_bounds__(64) void k_select_more(SelectArgs a) {
     const uint32_t n = *a.n_more;
     for (uint32_t i = a.n_front + blockIdx.x; i < n; i += gridDim.x) {
         const uint2 m = a.more[i];
-        select_window(a, m.x, m.y, S);
+        select_window<CAP, false>(a, m.x, m.y, S);  // windows after a slab's first: no checksum
         wave_fence();
     }
 }
@@ -2031,12 +2108,14 @@ void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s) {
     CRX_LAUNCH("locate", k_locate, grid1(tiles, kLocTiles), 64, s, a, tiles);
 }
 
-void launch_select(const SelectArgs &a, uint32_t tiles, bool dense, hipStream_t s) {
+void launch_select(const SelectArgs &a, uint32_t tiles, bool dense, bool any_cold, hipStream_t s) {
     if (dense) {
-        CRX_LAUNCH("select", k_select<kTgtCapDense>, a.n_front + tiles, 64, s, a);
+        if (any_cold) CRX_LAUNCH("select", (k_select<kTgtCapDense, true>), a.n_front + tiles, 64, s, a);
+        else CRX_LAUNCH("select", (k_select<kTgtCapDense, false>), a.n_front + tiles, 64, s, a);
         CRX_LAUNCH("select_more", k_select_more<kTgtCapDense>, 256, 64, s, a);
     } else {
-        CRX_LAUNCH("select", k_select<kTgtCapSparse>, a.n_front + tiles, 64, s, a);
+        if (any_cold) CRX_LAUNCH("select", (k_select<kTgtCapSparse, true>), a.n_front + tiles, 64, s, a);
+        else CRX_LAUNCH("select", (k_select<kTgtCapSparse, false>), a.n_front + tiles, 64, s, a);
         CRX_LAUNCH("select_more", k_select_more<kTgtCapSparse>, 256, 64, s, a);
     }
 }
