@@ -986,15 +986,8 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     unsigned long long *blk_sum = ar.get<unsigned long long>(B), *blk_prefix = ar.get<unsigned long long>(B + 1);
     hc.mark("apply_upload");
     Fork fork(s);
-    // payload words of the decoder's widest wavefront (64 consecutive blocks): its LDS is sized to them
-    uint64_t widest = 2, bit = 0;
-    for (uint64_t g0 = 0; g0 < B; g0 += 64) {
-        const uint64_t start = bit, n = std::min<uint64_t>(64, B - g0);
-        for (uint64_t k = 0; k < n; ++k) bit += u.block_bits(g0 + k);
-        widest = std::max(widest, ((bit + 63) >> 6) + 2 - (start >> 6));
-    }
     DecodeArgs da{d_descs, pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, bmap, d_lim, d_off, d_syms,
-                  (uint32_t)syms.size(), dz, blk_sum, bad, (uint32_t)std::min<uint64_t>(widest, kDecPayWords)};
+                  (uint32_t)syms.size(), dz, blk_sum, bad};
     launch_decode(da, fork.aux);
     launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), fork.aux);
 

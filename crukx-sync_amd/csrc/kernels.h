@@ -136,7 +136,6 @@ struct DecodeArgs {
     unsigned long long *dz;         // [changes] zz | (block-relative local index << 32)
     unsigned long long *blk_sum;    // [blocks] sum of (gap + 1) per block
     unsigned int *bad;
-    uint32_t lds_pay_words;         // payload words a wavefront stages in LDS (>= 2); wider ones read HBM
 };
 
 struct SelectArgs {
@@ -236,11 +235,8 @@ void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint6
                         hipStream_t s);
 void launch_decode(const DecodeArgs &a, hipStream_t s);
 constexpr uint32_t kDecSyms = 2048;  // decoding symbols staged in LDS when they fit
-constexpr uint32_t kDecPayWords = 3584;  // at most 28 KiB of payload per wavefront in LDS
-// Dynamic LDS of the decoder for `pay_words` staged payload words and n_syms symbols.
-inline uint32_t decode_lds_bytes(uint32_t pay_words, uint32_t n_syms) {
-    return pay_words * 8u + (n_syms <= kDecSyms ? n_syms * 4u : 0u);
-}
+// Dynamic LDS of the decoder for n_syms symbols.
+inline uint32_t decode_lds_bytes(uint32_t n_syms) { return n_syms <= kDecSyms ? n_syms * 4u : 0u; }
 void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
 void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s);
 // tile_tensor[tile] = tensor of every slab of the layout

@@ -1089,46 +1089,62 @@ __global__ __launch_bounds__(256) void k_sum_parts(const unsigned long long *par
 }
 
 // ================================================================== apply: block decode
-// One lane per 256-change block (codec.py:504-575), 64 consecutive blocks per wavefront.  The
-// wavefront's payload bits (contiguous: blocks are stored in order) are staged in LDS as
-// host-order 64-bit words, and so are the decoding symbols when they fit.  A change normally costs
-// one 64-bit window of the stream (unary run, remainder and Huffman peek together) and one LDS read
-// of its symbol; code lengths come from comparisons of the 17-bit peek with the canonical limits
+// One lane per 256-change block (codec.py:504-575), 64 consecutive blocks per wavefront.  Each lane
+// reads its block's payload bits from HBM (BitReader below); the decoding symbols are staged in LDS
+// when they fit.  A change normally costs one 64-bit window of the stream (unary run, remainder and
+// Huffman peek together) and one LDS read of its symbol; code lengths come from comparisons of the 17-bit peek with the canonical limits
 // held in registers.  The decoder does not read the receiver's weights or counts (positions are
 // checked against those by k_local_fix), so it can run beside the exponent-count pass.  Each lane
 // keeps kDecBuf decoded changes in registers and stores them together: storing one change at a time
 // left each lane's output lines half-written in L2, and they reached HBM several times over.
 constexpr uint32_t kDecBuf = 8;          // changes decoded per lane between stores
 
-// The decoder's LDS, sized per launch (decode_lds_bytes): the wavefront's payload words, then the
-// symbols.  Sizing it to the update's widest wavefront rather than the largest allowed lets more
-// wavefronts share a CU (1% updates: 23 instead of 36 KiB, 6 instead of 4 per CU).
-struct DecodeLds {
-    uint64_t *pay;
-    uint32_t *syms;
-    uint32_t pay_words;
+// A lane's reader of its block's bits: the two 64-bit words around the read position in registers
+// (hi, lo) and the next one already loading (nx), so each word's load has the decoding of the 64 bits
+// before it (about six changes) to arrive.  Staging a wavefront's payload in LDS instead took up to
+// 28 KiB per wavefront: a quarter of the wavefronts fit, each alone on its SIMD with nothing to hide
+// its dependent chain.  Read positions only move forward.  The words are kept as loaded (byte-swapped
+// only when read), so nothing consumes a load before the read that needs it: swapping or testing it at
+// the load made every load wait at once.  Past the stream's last word the last word is read again:
+// bits past a block's end never decide a valid change (a canonical code's length does not depend on
+// the bits after it, and unary runs stop at the block's end).
+struct BitReader {
+    const uint64_t *p;
+    uint64_t n, w;  // words in the stream; index of hi
+    uint64_t hi, lo, nx;
+    __device__ __forceinline__ uint64_t word(uint64_t i) const { return p[min64(i, n - 1)]; }
+    __device__ __forceinline__ void start(const uint64_t *payload, uint64_t n_words, uint64_t pos) {
+        p = payload;
+        n = n_words;
+        w = pos >> 6;
+        hi = word(w);
+        lo = word(w + 1);
+        nx = word(w + 2);
+    }
+    // the 64 bits from bit pos, which is at or past the previous read's
+    __device__ __forceinline__ uint64_t bits(uint64_t pos) {
+        const uint64_t t = pos >> 6;
+        if (t >= w + 3) {  // a long jump (a long unary run): start over there
+            w = t;
+            hi = word(t);
+            lo = word(t + 1);
+            nx = word(t + 2);
+        } else {
+            while (w < t) {
+                hi = lo;
+                lo = nx;
+                nx = word(w + 3);
+                ++w;
+            }
+        }
+        const uint32_t s = (uint32_t)(pos & 63);
+        const uint64_t h = __builtin_bswap64(hi), l = __builtin_bswap64(lo);
+        return s ? (h << s) | (l >> (64 - s)) : h;
+    }
 };
 
-// 64 bits of the stream from bit `pos`: LDS words [w0, ...) when staged, else HBM.
-template <bool LDS>
-__device__ __forceinline__ uint64_t bits64(const DecodeArgs &a, const DecodeLds &S, uint64_t w0, uint64_t pos) {
-    const uint32_t s = (uint32_t)(pos & 63);
-    uint64_t hi, lo;
-    if (LDS) {
-        const uint64_t *W = S.pay;
-        const uint32_t w = (uint32_t)min64((pos >> 6) - w0, S.pay_words - 2);
-        hi = W[w];
-        lo = W[w + 1];
-    } else {
-        const uint64_t w = pos >> 6;
-        hi = w < a.n_words ? __builtin_bswap64(a.payload[w]) : 0ULL;
-        lo = w + 1 < a.n_words ? __builtin_bswap64(a.payload[w + 1]) : 0ULL;
-    }
-    return s ? (hi << s) | (lo >> (64 - s)) : hi;
-}
-
-template <bool LDS_PAY, bool LDS_SYMS>
-__device__ void decode_blocks(const DecodeArgs &a, const DecodeLds &S, uint64_t w0) {
+template <bool LDS_SYMS>
+__device__ void decode_blocks(const DecodeArgs &a, const uint32_t *S_syms) {
     const uint32_t ln = lane();
     const uint64_t b = (uint64_t)blockIdx.x * 64 + ln;
     if (b >= a.n_blocks) return;
@@ -1146,6 +1162,8 @@ __device__ void decode_blocks(const DecodeArgs &a, const DecodeLds &S, uint64_t 
     uint64_t cur = a.block_off[b];
     const uint64_t end = cur + a.block_bits[b];
     bool bad = false;
+    BitReader R;
+    R.start(a.payload, a.n_words, cur);
 #pragma unroll
     for (int l = 0; l < 17; ++l) {
         lim[l] = a.lim[(uint64_t)gr.table * 17 + l];
@@ -1154,7 +1172,7 @@ __device__ void decode_blocks(const DecodeArgs &a, const DecodeLds &S, uint64_t 
     uint64_t rel = 0;  // sum of (gap + 1) so far in this block
     // decodes change s of the block into out: zz | (block-relative local << 32); false once bad
     auto step = [&](uint32_t s, unsigned long long &out) {
-        uint64_t x = bits64<LDS_PAY>(a, S, w0, cur);
+        uint64_t x = R.bits(cur);
         uint64_t q;
         if (~x) {  // the unary run ends inside this window
             q = (uint64_t)__builtin_clzll(~x);
@@ -1162,7 +1180,7 @@ __device__ void decode_blocks(const DecodeArgs &a, const DecodeLds &S, uint64_t 
             q = 64;
             for (;;) {
                 if (q > qmax || cur + q >= end) break;
-                const uint64_t y = ~bits64<LDS_PAY>(a, S, w0, cur + q);
+                const uint64_t y = ~R.bits(cur + q);
                 if (y) {
                     q += (uint64_t)__builtin_clzll(y);
                     break;
@@ -1173,7 +1191,7 @@ __device__ void decode_blocks(const DecodeArgs &a, const DecodeLds &S, uint64_t 
         const uint64_t c = cur + q + 1;
         // remainder and Huffman peek: from the same window when they fit in it, else a new read
         if (q + 1 + rice + 17 <= 64) x <<= (q + 1);
-        else x = bits64<LDS_PAY>(a, S, w0, c);
+        else x = R.bits(c);
         const uint64_t rem = rice ? x >> (64 - rice) : 0ULL;
         const uint32_t peek = (uint32_t)((x << rice) >> (64 - 17));
         // code length: 1 + #{l : lim[l] <= peek} (lim is non-decreasing), summed as a tree; then the
@@ -1200,7 +1218,7 @@ __device__ void decode_blocks(const DecodeArgs &a, const DecodeLds &S, uint64_t 
         } else {
             rel += gap + 1;
             const uint32_t si = min(idx, a.n_syms - 1);
-            const uint32_t zz = LDS_SYMS ? S.syms[si] : a.syms[si];
+            const uint32_t zz = LDS_SYMS ? S_syms[si] : a.syms[si];
             out = (unsigned long long)zz | ((unsigned long long)min64(rel - 1, 0xFFFFFFFFULL) << 32);
             cur = c + rice + L;
         }
@@ -1230,22 +1248,12 @@ __device__ void decode_blocks(const DecodeArgs &a, const DecodeLds &S, uint64_t 
 
 template <bool LDS_SYMS>
 __global__ __launch_bounds__(64) void k_decode(DecodeArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint64_t dyn_lds[];
-    const DecodeLds S{dyn_lds, reinterpret_cast<uint32_t *>(dyn_lds + a.lds_pay_words), a.lds_pay_words};
+    extern __shared__ __attribute__((aligned(16))) uint32_t dyn_lds[];  // the symbols, when they fit
     const uint32_t ln = lane();
-    const uint64_t b0 = (uint64_t)blockIdx.x * 64;
-    const uint64_t nb = min64(64, a.n_blocks - b0);
-    // this wavefront's bits [block_off[b0], block_off[b0 + nb]) lie in words [w0, wend)
-    const uint64_t w0 = a.block_off[b0] >> 6;
-    const uint64_t wend = min64(a.n_words, ((a.block_off[b0 + nb] + 63) >> 6) + 2);
-    const bool lds_pay = wend > w0 && wend - w0 <= a.lds_pay_words;
-    if (lds_pay)
-        for (uint64_t w = w0 + ln; w < wend; w += 64) S.pay[w - w0] = __builtin_bswap64(a.payload[w]);
     if (LDS_SYMS)
-        for (uint32_t i = ln; i < a.n_syms; i += 64) S.syms[i] = a.syms[i];
+        for (uint32_t i = ln; i < a.n_syms; i += 64) dyn_lds[i] = a.syms[i];
     wave_fence();
-    if (lds_pay) decode_blocks<true, LDS_SYMS>(a, S, w0);
-    else decode_blocks<false, LDS_SYMS>(a, S, w0);
+    decode_blocks<LDS_SYMS>(a, dyn_lds);
 }
 
 // Change blocks handled by one workgroup of the per-block kernels (fewer, longer workgroups; their
@@ -2092,7 +2100,7 @@ void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint6
 }
 
 void launch_decode(const DecodeArgs &a, hipStream_t s) {
-    const uint32_t grid = grid1(a.n_blocks, 64), lds = decode_lds_bytes(a.lds_pay_words, a.n_syms);
+    const uint32_t grid = grid1(a.n_blocks, 64), lds = decode_lds_bytes(a.n_syms);
     if (!grid) return;
     timing_begin("decode", s);
     if (a.n_syms <= kDecSyms) hipLaunchKernelGGL(k_decode<true>, dim3(grid), dim3(64), lds, s, a);
