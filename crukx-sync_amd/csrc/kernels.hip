@@ -158,9 +158,10 @@ __device__ __forceinline__ Rsrc slab_rsrc(const uint32_t *frame, const Slab &s) 
 }
 
 // Streams the slab's rows through `body(row, word of stream 0, word of stream S-1)`, U rows per batch
-// with the next batch already in flight (double buffering keeps U..2U rows of loads outstanding
-// per wavefront while a batch is processed).  Every batch is whole: rows at or past nrows read as
-// zero and lie outside [f_lo, f_hi), so the body treats them as partial rows with no valid lane.
+// with the next batch already in flight (U..2U rows of loads outstanding per wavefront while a batch
+// is processed).  The two batches' registers alternate (the loop body holds two batches), so no
+// registers are copied between batches.  Every batch is whole: rows at or past nrows read as zero
+// and lie outside [f_lo, f_hi), so the body treats them as partial rows with no valid lane.
 // CPOL is the cache policy of the loads of the first stream, CPOL_LAST that of the last stream
 // (kStreamNT: non-temporal).  Measured: the select pass with non-temporal loads 5.08 -> 4.93 ms; the
 // rank pass 6.50 -> 6.18 ms with them on one of its two streams, 6.71 ms with them on both.
@@ -169,23 +170,25 @@ template <int U, int S, int CPOL = 0, int CPOL_LAST = CPOL, typename Body>
 __device__ __forceinline__ void stream_rows(const Slab &sl, const Rsrc (&src)[S], Body &&body) {
     static_assert(S == 1 || S == 2, "one or two streams");
     const uint32_t lb = lane() * 4u;
-    uint32_t cur[S][U], nxt[S][U];
-    auto load = [&](uint32_t(&dst)[S][U], uint32_t base) {
+    uint32_t a[S][U], b[S][U];
+    auto load = [&](uint32_t(&dst)[S][U], uint32_t r) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            dst[0][u] = __builtin_amdgcn_raw_buffer_load_b32(src[0], base + u * 256u, 0, S == 1 ? CPOL_LAST : CPOL);
-            if (S == 2) dst[S - 1][u] = __builtin_amdgcn_raw_buffer_load_b32(src[S - 1], base + u * 256u, 0, CPOL_LAST);
+            dst[0][u] = __builtin_amdgcn_raw_buffer_load_b32(src[0], (r + u) * 256u + lb, 0, S == 1 ? CPOL_LAST : CPOL);
+            if (S == 2) dst[S - 1][u] = __builtin_amdgcn_raw_buffer_load_b32(src[S - 1], (r + u) * 256u + lb, 0, CPOL_LAST);
         }
     };
-    load(cur, lb);
-    for (uint32_t r0 = 0; r0 < sl.nrows; r0 += U) {
-        load(nxt, (r0 + U) * 256u + lb);
+    if (sl.nrows == 0) return;
+    load(a, 0);
+    for (uint32_t r0 = 0;; r0 += 2 * U) {  // r0 < nrows here
+        load(b, r0 + U);
 #pragma unroll
-        for (int u = 0; u < U; ++u) body(r0 + u, cur[0][u], cur[S - 1][u]);
+        for (int u = 0; u < U; ++u) body(r0 + u, a[0][u], a[S - 1][u]);
+        if (r0 + U >= sl.nrows) break;
+        load(a, r0 + 2 * U);
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int q = 0; q < S; ++q) cur[q][u] = nxt[q][u];
+        for (int u = 0; u < U; ++u) body(r0 + U + u, b[0][u], b[S - 1][u]);
+        if (r0 + 2 * U >= sl.nrows) break;
     }
 }
 
@@ -369,13 +372,15 @@ constexpr uint32_t kHistCopies = 8;
 // The weighted sum of a cold slab's weights for its tensor's checksum (codec.py:61-68), over its odd
 // rows (odd) or all of them: one stream of the slab, for slabs the select pass does not stream (no
 // targets, or an update already rejected).
-__device__ uint64_t cold_sum(const TensorDesc &td, const Slab &sl, bool odd) {
+__device__ __forceinline__ uint64_t cold_sum(const TensorDesc &td, const Slab &sl, bool odd) {
     const uint32_t ln = lane();
     const Rsrc src[1] = {slab_rsrc(td.frame, sl)};
     WeightedSum acc;
     // z = (index + 1) * golden of this lane's first element in the current row
     uint64_t z = (uint64_t)(2 * (int64_t)sl.first - (int64_t)td.lead + 2 * ln + 1) * kGolden;
-    stream_rows<kScanRows>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
+    // half the histogram pass's batch: this runs for few slabs, inside kernels whose occupancy its
+    // registers would otherwise set
+    stream_rows<kScanRows / 2>(sl, src, [&](uint32_t r, uint32_t o, uint32_t) {
         uint32_t v = o;
         if (!row_full(sl, r)) {
             const uint32_t f = r * kRow + 2 * ln;
