@@ -651,6 +651,9 @@ std::string py_repr(const std::string &s) {
 
 // ------------------------------------------------------------------ encode
 // codec.encode (codec.py:278-420) on the device.
+// rare symbols downloaded with the symbol counts, before their number is known
+constexpr uint64_t kRareFirst = 16384;
+
 void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news, const uint64_t *numels,
             const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab_req, hipStream_t s, Arena &ar,
             crx_encoded &E) {
@@ -759,41 +762,43 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     d2h(hdelta.data(), t_delta, T, s);
     d2h(hfull.data(), t_full, T, s);
     d2h(hs, scnt, 2, s);
+    // the first rare symbols in the same wait (an update has few); the rest, if any, after it
+    const uint64_t rare_first = std::min<uint64_t>(C, kRareFirst);
+    std::vector<uint32_t> hrare(rare_first);
+    d2h(hrare.data(), rare, rare_first, s);
     sync(s);
     hc.mark("enc_wait_stats");
     if (hs[1]) throw DeviceError("rare symbol list overflowed");
-    std::vector<uint32_t> hrare(hs[0]);
-    d2h(hrare.data(), rare, hs[0], s);
-    sync(s);
+    hrare.resize(hs[0]);
+    if (hs[0] > rare_first) {
+        d2h(hrare.data() + rare_first, rare + rare_first, hs[0] - rare_first, s);
+        sync(s);
+    }
     hc.mark("enc_wait_rare");
     std::sort(hrare.begin(), hrare.end());
 
-    // checksums (codec.py:344-352) and groups / Rice parameters (codec.py:354-360)
-    for (uint32_t d = 0; d < T; ++d) {
-        const int32_t t = L.call_index[d];
-        E.checksum[t] = (has_cache && has_cache[t]) ? cache_vals[t] + hdelta[d] : hfull[d];
-    }
-    uint64_t blk = 0;
+    // What the code kernels need first: Rice parameters and first blocks of the groups (codec.py:354-360),
+    // and one canonical Huffman table per exponent, symbols ascending (codec.py:369-392).  The payload's
+    // length follows from them: a group's gap codes take its chosen cost, its symbols their code lengths.
+    uint64_t blk = 0, total_bits = 0;
     for (uint64_t g = 0; g < G; ++g) {
         GroupDev &gr = groups[g];
         const int c[3] = {(int)(gr.r0 ? gr.r0 - 1 : 0), (int)gr.r0, (int)std::min<uint32_t>(gr.r0 + 1, kMaxRice)};
         const uint64_t sh[3] = {hcost[g * 3], hcost[g * 3 + 1], hcost[g * 3 + 2]};
         gr.rice = (uint32_t)rice_choose(gr.count, c, sh);
+        const int k = gr.rice == (uint32_t)c[0] ? 0 : gr.rice == (uint32_t)c[1] ? 1 : 2;
+        total_bits += sh[k] + (uint64_t)gr.count * (1 + gr.rice);
         gr.blk_base = (uint32_t)blk;
         blk += n_blocks(gr.count);
-        const int32_t t = L.call_index[gr.tensor];
-        E.present[t] = 1;
-        E.groups[t].push_back(Group{(int)gr.exponent, gr.count, (int)gr.rice});
     }
     const uint64_t B = blk;
-    E.n_blocks = B;
-
-    // one canonical Huffman table per exponent, symbols ascending (codec.py:369-392)
     std::vector<uint32_t> lut(256 * kDense, 0), rkeys, rvals;
+    std::vector<uint32_t> syms;
+    std::vector<uint64_t> counts;
     size_t ri = 0;
     for (int e = 0; e < 256; ++e) {
-        std::vector<uint32_t> syms;
-        std::vector<uint64_t> counts;
+        syms.clear();
+        counts.clear();
         for (int z = 0; z < kDense; ++z)
             if (hdense[e * kDense + z]) {
                 syms.push_back(z);
@@ -810,13 +815,15 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
             counts.push_back(c);
         }
         if (syms.empty()) continue;
-        std::vector<int> len = huffman_lengths(counts);
-        std::vector<uint32_t> code = canonical_codes(len);
+        const std::vector<int> len = huffman_lengths(counts);
+        const std::vector<uint32_t> code = canonical_codes(len);
         Table tb;
         tb.exponent = e;
         tb.symbols = syms;
+        tb.lengths.resize(syms.size());
         for (size_t k = 0; k < syms.size(); ++k) {
-            tb.lengths.push_back((uint8_t)len[k]);
+            tb.lengths[k] = (uint8_t)len[k];
+            total_bits += counts[k] * (uint64_t)len[k];
             const uint32_t v = (code[k] << 5) | (uint32_t)len[k];
             if (syms[k] < (uint32_t)kDense) lut[e * kDense + syms[k]] = v;
             else {
@@ -826,8 +833,9 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
         }
         E.tables.push_back(std::move(tb));
     }
-
     hc.mark("enc_tables");
+
+    // the code lengths, their offsets and the bits, with no wait: the payload's size is known
     GroupDev *d_groups2 = ar.get<GroupDev>(G);
     uint32_t *d_lut = ar.get<uint32_t>(256 * kDense);
     uint32_t *d_rk = ar.get<uint32_t>(rkeys.size()), *d_rv = ar.get<uint32_t>(rvals.size());
@@ -836,31 +844,40 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     h2d(d_rk, rkeys.data(), rkeys.size(), s);
     h2d(d_rv, rvals.data(), rvals.size(), s);
     unsigned long long *tsum = ar.get<unsigned long long>(n_thr), *toff = ar.get<unsigned long long>(n_thr + 1);
-    CodeArgs ca{sorted, C, d_groups2, (uint32_t)G, d_lut, d_rk, d_rv, (uint32_t)rkeys.size(), cmap, tsum, toff,
-                nullptr, nullptr};
-    launch_code_lengths(ca, s);
-    launch_scan_u64(tsum, n_thr, toff, ar.get<unsigned long long>(scan_parts(n_thr)), s);
-    unsigned long long total_bits = 0;
-    d2h(&total_bits, toff + n_thr, 1, s);
-    sync(s);
-    hc.mark("enc_wait_lengths");
-
     const uint64_t n_words = (total_bits + 31) / 32 + 4;
     uint32_t *words = ar.get<uint32_t>(n_words);
     unsigned long long *bstart = ar.get<unsigned long long>(B + 1);
     uint32_t *bb = ar.get<uint32_t>(B);
     unsigned int *bovf = ar.get<unsigned int>(1);
+    CodeArgs ca{sorted, C, d_groups2, (uint32_t)G, d_lut, d_rk, d_rv, (uint32_t)rkeys.size(), cmap, tsum, toff,
+                words, bstart, n_words, bovf};
+    launch_code_lengths(ca, s);
+    launch_scan_u64(tsum, n_thr, toff, ar.get<unsigned long long>(scan_parts(n_thr)), s);
     zero(words, n_words, s);
     zero(bovf, 1, s);
     HIP_OK(hipMemcpyAsync(bstart + B, toff + n_thr, sizeof(unsigned long long), hipMemcpyDeviceToDevice, s));
-    ca.words = words;
-    ca.bstart = bstart;
     launch_pack(ca, s);
     launch_block_bits(bstart, B, bb, bovf, s);
     unsigned int hovf = 0;
+    unsigned long long dev_bits = 0;
     d2h(&hovf, bovf, 1, s);
+    d2h(&dev_bits, toff + n_thr, 1, s);
+
+    // the rest of the host's part while the device packs: checksums (codec.py:344-352), the groups
+    for (uint32_t d = 0; d < T; ++d) {
+        const int32_t t = L.call_index[d];
+        E.checksum[t] = (has_cache && has_cache[t]) ? cache_vals[t] + hdelta[d] : hfull[d];
+    }
+    for (uint64_t g = 0; g < G; ++g) {
+        const GroupDev &gr = groups[g];
+        const int32_t t = L.call_index[gr.tensor];
+        E.present[t] = 1;
+        E.groups[t].push_back(Group{(int)gr.exponent, gr.count, (int)gr.rice});
+    }
+    E.n_blocks = B;
     sync(s);
     hc.mark("enc_wait_pack");
+    if (hovf & 2u || dev_bits != total_bits) throw DeviceError("the packed payload's size differs from its codes' lengths");
     if (hovf) throw Invalid("a block exceeds 2^32 bits; the update cannot be represented");
     g_encode_hint.put(hint_key, ar.total);
     E.d_block_bits = bb;

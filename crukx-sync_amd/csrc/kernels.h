@@ -117,6 +117,8 @@ struct CodeArgs {
     const unsigned long long *toff; // [threads] exclusive bit offsets
     uint32_t *words;                // payload as big-endian bytes in 32-bit words
     unsigned long long *bstart;     // [blocks + 1] bit offset of each block
+    uint64_t n_words;               // words allocated: a workgroup whose bits end past them writes nothing
+    unsigned int *overflow;         // |= 2 when that happens
 };
 
 struct DecodeArgs {

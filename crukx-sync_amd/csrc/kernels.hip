@@ -961,6 +961,10 @@ __global__ __launch_bounds__(256) void k_pack(CodeArgs a) {
     const unsigned long long b_lo = a.toff[t0], b_hi = a.toff[min64(t0 + 256, n_thr)];
     const uint64_t w0 = b_lo >> 5, nw = ((b_hi + 31) >> 5) - w0;
     const unsigned long long off = tc.n ? a.toff[t0 + threadIdx.x] : 0ULL;
+    if (w0 + nw > a.n_words) {  // uniform: the payload was sized from other lengths than these
+        if (threadIdx.x == 0) atomicOr(a.overflow, 2u);
+        return;
+    }
     if (nw > kPackLdsWords) {  // uniform across the workgroup
         if (tc.n) pack_thread<false>(a, tc, a.words, 0, off);
         return;

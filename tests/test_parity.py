@@ -299,6 +299,28 @@ def test_change_densities_across_target_list_sizes(rho):
     assert torch.equal(got["w"].cpu().view(torch.int16), b.view(torch.int16))
 
 
+@pytest.mark.parametrize("n_large", [16_000, 60_000])
+def test_many_large_residuals_bytes_equal_oracle(n_large):
+    """Residuals of 16 ULP or more (zigzag symbols past the dense per-exponent table, counted in the
+    rare list): fewer than the 16384 the encoder downloads with the symbol counts, and more, which
+    take a second download.  Bytes equal the oracle's; the update applies exactly."""
+    g = torch.Generator().manual_seed(n_large)
+    n = 1 << 20
+    a = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    bits = a.view(torch.int16).clone()
+    idx = torch.randperm(n, generator=g)[:n_large]
+    step = torch.randint(16, 2000, (n_large,), generator=g, dtype=torch.int16)
+    step = torch.where(torch.rand(n_large, generator=g) < 0.5, -step, step)
+    bits[idx] = bits[idx] + step  # magnitudes near 0.02: sign and exponent range stay finite
+    b = bits.view(torch.bfloat16)
+    assert torch.isfinite(b.float()).all()
+    upd = crukx_sync.encode_update({"w": a.cuda()}, {"w": b.cuda()})
+    assert upd == oracle.encode_update({"w": a}, {"w": b})
+    got = {"w": a.cuda()}
+    crukx_sync.apply_update(got, upd)
+    assert torch.equal(got["w"].cpu().view(torch.int16), b.view(torch.int16))
+
+
 def test_exponent_counts_are_not_reused_across_slab_sizes(monkeypatch):
     """Counts recorded with one slab size are recomputed, not reused, when the slab size changes
     between updates of the same receiver tensors (their layout differs)."""
