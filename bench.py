@@ -11,7 +11,8 @@ Prints one JSON line.
   (`roofline` divides its algorithmic bytes by its average duration over those same steps).
 - `detail.kernels_ms_per_step`: every kernel and host phase, from a separate instrumented pass.
 - `detail.cold_*`: the process's first update (first allocations included); `detail.cold2_*`: an
-  update with both checksum caches dropped and the allocator warm, i.e. full checksums on both sides.
+  update with both checksum caches dropped and the allocator warm, i.e. full checksums on both sides
+  (the median of three such steps, each after a warm step).
 - `detail.configs`: the same measurement at other sizes and densities.
 - `cpu_baseline`: a torch-CPU restatement of the reference's CPU path (oracle/torch_cpu.py, bytes
   checked against the reference's golden vectors by the tests) on the host cores, over a sample of
@@ -207,8 +208,17 @@ class Run:
         for _ in range(warmup):
             self.step()
         self.exact()
-        # caches dropped, allocator warm: once plain, once instrumented; then warm again
-        (e, a, _, _), _ = self.cold_step(False)
+        # caches dropped, allocator warm: three plain steps, each after a warm step (the median is
+        # reported: single such steps varied by up to 1 ms), then one instrumented; then warm again
+        e2, a2 = [], []
+        for _ in range(3):
+            self.step()
+            (e, a, _, _), _ = self.cold_step(False)
+            e2.append(e)
+            a2.append(a)
+        log("[bench] caches dropped, three steps: encode " + " ".join(f"{x * 1e3:.2f}" for x in e2) +
+            " ms, apply " + " ".join(f"{x * 1e3:.2f}" for x in a2) + " ms")
+        e, a = sorted(e2)[1], sorted(a2)[1]
         out["cold2_encode_ms"], out["cold2_apply_ms"] = round(e * 1e3, 3), round(a * 1e3, 3)
         _, out["cold2_breakdown"] = self.cold_step(True)
         for _ in range(max(warmup, 1)):
