@@ -189,6 +189,49 @@ def test_corruptions_match_oracle_verdicts():
         assert torch.equal(w_hip["w"].cpu().view(torch.int16), w_ref["w"].view(torch.int16))
 
 
+def test_many_small_slabs_with_corruptions_in_the_last_tensor(monkeypatch):
+    """Six tensors in 128-element slabs (over 7000 slabs).  Clean: the oracle's bytes, applied exactly.
+    Corrupted in the payload of the last tensor: rejected, as by the oracle, with one of the
+    reference's messages, and the weights as they were."""
+    monkeypatch.setattr(codec, "_SLAB", 128)
+    g = torch.Generator().manual_seed(5)
+    names = [f"t{i}" for i in range(6)]
+    old, new = {}, {}
+    for i, n in enumerate(names):
+        a, b = scenarios.rl_pair(150_000 + 37 * i, lr=3e-6, seed=40 + i)
+        old[n], new[n] = a, b
+    upd = crukx_sync.encode_update(_cuda(old), _cuda(new))
+    assert upd == oracle.encode_update(old, new)
+    w = _cuda({k: v.clone() for k, v in old.items()})
+    crukx_sync.apply_update(w, upd)
+    for k in names:
+        assert torch.equal(w[k].cpu().view(torch.int16), new[k].view(torch.int16)), k
+    tail = len(upd) // 6  # about the last tensor's share of the payload
+    outcomes = set()
+    for _ in range(60):
+        bad = bytearray(upd)
+        for i in torch.randint(len(upd) - tail, len(upd), (2,), generator=g).tolist():
+            bad[i] ^= int(torch.randint(1, 256, (1,), generator=g))
+        bad = bytes(bad)
+        w_hip, w_ref = _cuda({k: v.clone() for k, v in old.items()}), {k: v.clone() for k, v in old.items()}
+        hip = ref = None
+        try:
+            crukx_sync.apply_update(w_hip, bad)
+        except ValueError as e:
+            hip = str(e)
+        try:
+            oracle.apply_update(w_ref, bad)
+        except ValueError as e:
+            ref = str(e)
+        assert (hip is None) == (ref is None)
+        outcomes.add(hip)
+        for k in names:
+            assert torch.equal(w_hip[k].cpu().view(torch.int16), w_ref[k].view(torch.int16)), k
+    assert None not in outcomes  # every corruption here is rejected
+    assert all(m.startswith("update does not verify (checksum mismatch: [") or
+               m == "payload positions outside their exponent groups" for m in outcomes), outcomes
+
+
 def test_qwen_layer_sized_round_trip_properties():
     """One 7B-shaped decoder layer plus the final norm (233M weights), three chained steps with
     caches: exact round trips, sender cache == receiver cache == full checksums of the result."""
