@@ -382,6 +382,7 @@ def cpu_baseline(args, shapes, A, B, N):
     log(f"[bench] torch-cpu restatement on {n_sample:,} weights ({threads} threads): encode {t1 - t0:.2f}s "
         f"apply {t2 - t1:.2f}s -> {ms / 1e3:.1f}s per full update; C oracle (1 thread) encode {t4 - t3:.2f}s "
         f"apply {t5 - t4:.2f}s; {len(data):,} bytes identical on GPU, restatement and oracle")
+    small4 = small4_chain(threads)
     return {"value": round(ms, 1), "unit": "ms", "cores": threads, "kind": "port",
             "impl": "torch-CPU restatement of the reference's CPU path (oracle/torch_cpu.py): slab-wise stable "
                     "argsort ranking, 256-step vectorised block decode, index_put_ scatter",
@@ -391,7 +392,54 @@ def cpu_baseline(args, shapes, A, B, N):
             "sample_encode_s": round(t1 - t0, 3), "sample_apply_s": round(t2 - t1, 3),
             "sample_bytes_identical": True,
             "c_oracle_1_thread": {"sample_encode_s": round(t4 - t3, 3), "sample_apply_s": round(t5 - t4, 3),
-                                  "value_ms": round((t5 - t3) * scale * 1e3, 1)}}
+                                  "value_ms": round((t5 - t3) * scale * 1e3, 1)},
+            "small4_chain": small4}
+
+
+def small4_chain(threads):
+    """The reference's CPU plumbing case in full: four tensors (26,611,713 weights), three chained
+    steps with both checksum caches, through the torch-CPU restatement on the host threads and through
+    the GPU (bytes API); every step's bytes must be identical, and both receivers end equal to the
+    last state."""
+    import torch
+
+    import crukx_sync
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import torch_cpu
+    from crukx_sync import workloads
+
+    states = [workloads.make_weights(workloads.small4_shapes(), seed=0, device="cuda")]
+    for k in range(1, 4):
+        states.append(workloads.make_step(states[-1], k, rho=0.01, p_one=0.87, seed=0))
+    host = [{n: v.cpu() for n, v in st.items()} for st in states]
+    send_g, recv_g, send_c, recv_c = {}, {}, {}, {}
+    w_gpu = {n: v.clone() for n, v in states[0].items()}
+    w_cpu = {n: v.clone() for n, v in host[0].items()}
+    cpu_enc, cpu_app, gpu_step = [], [], []
+    for k in range(1, 4):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        data = crukx_sync.encode_update(states[k - 1], states[k], send_g)
+        crukx_sync.apply_update(w_gpu, data, recv_g)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        ref = torch_cpu.encode_update(host[k - 1], host[k], send_c)
+        t2 = time.perf_counter()
+        torch_cpu.apply_update(w_cpu, ref, recv_c)
+        t3 = time.perf_counter()
+        assert ref == data, f"small4 step {k}: the restatement's bytes differ from the GPU's"
+        gpu_step.append(t1 - t0)
+        cpu_enc.append(t2 - t1)
+        cpu_app.append(t3 - t2)
+    for n in w_cpu:
+        assert torch.equal(w_cpu[n].view(torch.int16), host[3][n].view(torch.int16)), n
+        assert torch.equal(w_gpu[n].view(torch.int16), states[3][n].view(torch.int16)), n
+    log(f"[bench] small4 chain (26,611,713 weights, 3 steps): torch-cpu restatement encode "
+        + " ".join(f"{x:.3f}" for x in cpu_enc) + " s, apply " + " ".join(f"{x:.3f}" for x in cpu_app)
+        + " s; GPU (bytes API) " + " ".join(f"{x * 1e3:.2f}" for x in gpu_step) + " ms per step; bytes identical")
+    return {"weights": 26611713, "steps": 3, "threads": threads, "cpu_encode_s": [round(x, 4) for x in cpu_enc],
+            "cpu_apply_s": [round(x, 4) for x in cpu_app], "gpu_bytes_api_step_ms": [round(x * 1e3, 3) for x in gpu_step],
+            "bytes_identical": True}
 
 
 if __name__ == "__main__":
