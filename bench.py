@@ -70,8 +70,8 @@ def main():
         return
 
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only: the update codec has no multi-GPU path "
-                                   "here (sharding is described in DESIGN.md); run with --gpus 1"}))
+        print(json.dumps({"error": "bench.py measures one GPU: the update codec here has no multi-GPU path "
+                                   "(it would shard by whole tensors); run with --gpus 1"}))
         sys.exit(2)
 
     import torch

@@ -5,7 +5,7 @@
  * The reference (Crukx-dev/crukx-sync v0.2.0) is pure Python/torch and has no FFI; these entry
  * points replace the functions of its hot path, named per declaration below (paths relative to
  * the reference repository).  The Python package crukx_sync in crukx-sync_amd/ binds them with
- * ctypes (INTEGRATION.md shows the binding) and keeps the reference's public API unchanged.
+ * ctypes (crukx_sync/_native.py) and keeps the reference's public API unchanged.
  *
  * Conventions
  *   - Status codes: CRX_OK, CRX_CORRUPT (-> crukx_sync.CorruptUpdate), CRX_INVALID (-> ValueError),
