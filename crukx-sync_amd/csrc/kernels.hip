@@ -255,7 +255,7 @@ __device__ __forceinline__ uint32_t rank_count(const uint32_t *hall, uint32_t k)
 }
 
 template <bool COLD>
-__device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32_t tau, const Slab &sl,
+__device__ __forceinline__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32_t tau, const Slab &sl,
                               uint32_t *hall, uint32_t *hchg, uint32_t *meta, uint32_t *vals) {
     const uint32_t ln = lane(), rep = ln & (kRankCopies - 1);
     const Rsrc src[2] = {slab_rsrc(td.frame, sl), slab_rsrc(td.frame_new, sl)};
@@ -286,7 +286,23 @@ __device__ void enc_rank_slab(const EncRankArgs &a, const TensorDesc &td, uint32
         }
         const bool c0 = (x & 0xFFFF) != 0, c1 = x > 0xFFFF;
         const uint64_t C0 = ballot(c0), C1 = ballot(c1);
-        if (C0 | C1) {
+        if ((C0 | C1) && __popcll(C0) + __popcll(C1) == 1) {
+            // one change in the row (about half the rows with changes at 1%): its rank and buffer
+            // entry from scalar ballot arithmetic, written by its own lane
+            const bool hi = C0 == 0;  // the change is the high element of its lane
+            const uint32_t l = (uint32_t)__builtin_ctzll(hi ? C1 : C0);
+            const uint32_t k = hi ? rdlane(k1, l) : rdlane(k0, l);
+            const uint64_t M0 = ballot(k0 == k), M1 = ballot(k1 == k), lt = (1ULL << l) - 1;
+            const uint32_t in_row = (uint32_t)(__popcll(M0 & lt) + __popcll(M1 & lt)) + (hi ? (uint32_t)(M0 >> l) & 1u : 0u);
+            const uint32_t rk = rank_count(hall, k) + in_row;
+            if (ln == l) {
+                const uint32_t fr = (r * kRow + 2 * ln + (hi ? 1u : 0u) - sl.f_lo) << 16;
+                meta[cnt] = rk | fr;
+                vals[cnt] = hi ? (o >> 16) | (n & 0xFFFF0000u) : (o & 0xFFFF) | (n << 16);
+            }
+            cnt += 1;
+            wave_fence();
+        } else if (C0 | C1) {
             uint32_t rk0 = 0, rk1 = 0;  // meaningful for changed elements only
             uint64_t P0 = C0, P1 = C1;
             do {  // once per distinct exponent among this row's changes
