@@ -315,8 +315,7 @@ def _encode_inputs(names, old, new, checksums):
     A = list(old.values()) if type(old) is dict else [old[n] for n in names]
     B = list(new.values()) if type(new) is dict and list(new) == names else [new[n] for n in names]
     try:
-        ma, mb = M.meta(A), M.meta(B)
-        same = M.same_shapes(A, B)
+        ma, mb, same = M.meta_pair(A, B)
     except (TypeError, RuntimeError):  # not all tensors
         return None
     n = len(names)

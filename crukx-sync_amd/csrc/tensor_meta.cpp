@@ -40,6 +40,12 @@ bool same_shapes(const std::vector<at::Tensor> &a, const std::vector<at::Tensor>
     return true;
 }
 
+// The encoder's inputs in one call: meta() of both lists and whether their shapes agree pairwise (each
+// list is converted from Python once instead of twice).
+py::tuple meta_pair(const std::vector<at::Tensor> &a, const std::vector<at::Tensor> &b) {
+    return py::make_tuple(meta(a), meta(b), same_shapes(a, b));
+}
+
 // Version counters only (after an in-place write), as packed u64.
 py::bytes versions(const std::vector<at::Tensor> &ts) {
     std::vector<uint64_t> ver(ts.size());
@@ -52,5 +58,6 @@ py::bytes versions(const std::vector<at::Tensor> &ts) {
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("meta", &meta, "address, numel, device, flags, version of every tensor of a list");
     m.def("same_shapes", &same_shapes, "whether two lists of tensors agree in shape pairwise");
+    m.def("meta_pair", &meta_pair, "meta of two lists and whether their shapes agree pairwise");
     m.def("versions", &versions, "version counters of a list of tensors");
 }

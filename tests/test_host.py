@@ -212,5 +212,10 @@ def test_tensor_metadata_helper_agrees_with_the_tensors():
         assert flags[i] == (1 if t.dtype in (torch.bfloat16, torch.int16) else 0) | (2 if t.is_contiguous() else 0)
     assert array("Q", M.versions(ts)) == ver
     assert M.same_shapes(ts, [t.clone() for t in ts]) and not M.same_shapes(ts[:2], ts[1:3])
+    ma, mb, same = M.meta_pair(ts, [t.clone() for t in ts])  # the encoder's combined call
+    assert ma == M.meta(ts) and array("Q", mb[1]) == numel and same
+    assert M.meta_pair(ts[:2], ts[1:3])[2] is False
     with pytest.raises(TypeError):
         M.meta([ts[0], None])
+    with pytest.raises(TypeError):
+        M.meta_pair([ts[0]], [None])
