@@ -308,6 +308,10 @@ void copy_from_host(uint8_t *dst, const uint8_t *src, uint64_t n, hipStream_t s)
 // a reserved block (reserve) still has room for them.
 constexpr uint64_t kArenaChunk = 8ULL << 20;
 
+// Every buffer an allocation of its own, of exactly the size asked for (no chunks, no reserved
+// block): set by the CPU model of the library, so that a memory checker sees each buffer's bounds.
+bool g_arena_unpooled = false;
+
 struct Arena {
     crx_alloc_fn fn;
     void *ctx;
@@ -322,6 +326,7 @@ struct Arena {
     }
     // one block of `bytes` for the buffers that follow
     void reserve(uint64_t bytes) {
+        if (g_arena_unpooled) return;
         bytes = (bytes + 255) & ~uint64_t(255);
         if (bytes <= size - used) return;
         chunk = static_cast<uint8_t *>(raw(bytes));
@@ -330,6 +335,10 @@ struct Arena {
     }
     template <typename T>
     T *get(uint64_t count) {
+        if (g_arena_unpooled) {
+            total += count * sizeof(T);
+            return static_cast<T *>(raw(std::max<uint64_t>(count * sizeof(T), 1)));
+        }
         uint64_t bytes = std::max<uint64_t>(count * sizeof(T), 16);
         bytes = (bytes + 255) & ~uint64_t(255);
         total += bytes;

@@ -8,6 +8,8 @@
 // histograms are scanned per tensor afterwards, so a slab's ranks become tensor-wide ranks.
 #include "kernels.h"
 
+#include <crx_wave.h>
+
 #include <algorithm>
 #include <mutex>
 
@@ -50,10 +52,6 @@ struct WeightedSum {
 __device__ __forceinline__ uint32_t lane() { return __lane_id(); }
 // 64-bit integer min (the generic min template of the HIP headers goes through double precision)
 __device__ __forceinline__ uint64_t min64(uint64_t a, uint64_t b) { return a < b ? a : b; }
-// Orders this wavefront's LDS accesses in the compiler's view without waiting on outstanding memory
-// operations (LDS instructions of one wavefront execute in order).  The streaming kernels run one
-// wavefront per workgroup, so a workgroup barrier would only drain the rows loaded ahead.
-__device__ __forceinline__ void wave_fence() { asm volatile("" ::: "memory"); }
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 // number of set bits of m below this lane
 __device__ __forceinline__ uint32_t mbcnt(uint64_t m) {
@@ -1088,11 +1086,14 @@ __global__ __launch_bounds__(256) void k_checksum(const uint32_t *frame, uint32_
     const uint64_t words = (n + lead + 1) >> 1;
     const uint64_t per = (words + n_parts - 1) / n_parts;
     const uint64_t wb = (uint64_t)blockIdx.x * per, we = min(wb + per, words);
+    // the range's words (at most 2^31 bytes: per <= max(65536, words / 2048) words)
+    const Rsrc src = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(frame + min64(wb, words)), (short)0,
+                                                       (int)(we > wb ? (we - wb) * 4u : 0u), 0x00020000);
     WeightedSum acc;
     // z = (index + 1) * golden of the thread's first element of word d, stepped with d
     uint64_t z = (uint64_t)(2 * (int64_t)(wb + threadIdx.x) - (int64_t)lead + 1) * kGolden;
     for (uint64_t d = wb + threadIdx.x; d < we; d += 256, z += 512 * kGolden) {
-        const uint32_t o = frame[d];
+        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b32(src, (uint32_t)(d - wb) * 4u, 0, 0);
         const int64_t i0 = (int64_t)(2 * d) - (int64_t)lead;
         const uint32_t u0 = i0 >= 0 ? o & 0xFFFF : 0u, u1 = i0 + 1 < (int64_t)n ? o >> 16 : 0u;
         acc.add(u0, mix_weight(z));
@@ -1273,7 +1274,7 @@ __device__ void decode_blocks(const DecodeArgs &a, const uint32_t *S_syms) {
 
 template <bool LDS_SYMS>
 __global__ __launch_bounds__(64) void k_decode(DecodeArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint32_t dyn_lds[];  // the symbols, when they fit
+    CRX_DYNAMIC_LDS(uint32_t, dyn_lds);  // the symbols, when they fit
     const uint32_t ln = lane();
     if (LDS_SYMS)
         for (uint32_t i = ln; i < a.n_syms; i += 64) dyn_lds[i] = a.syms[i];
@@ -1470,24 +1471,6 @@ static_assert(kTgtCapSparse % 1024 == 0 && kTgtCapDense % 1024 == 0, "target lis
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u16x2 as16(uint32_t v) { return __builtin_bit_cast(u16x2, v); }
 
-// m with bit k (uniform) cleared, in one scalar instruction
-__device__ __forceinline__ void clear_bit(uint64_t &m, uint32_t k) { asm("s_bitset0_b64 %0, %1" : "+s"(m) : "s"(k)); }
-
-// (a & m) | b in one instruction (the mask from a scalar register)
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t b) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(b));
-    return r;
-}
-
-// v + this lane's bit of m, in one instruction (the mask as carry-in)
-__device__ __forceinline__ uint32_t add_bit(uint32_t v, uint64_t m) {
-    uint32_t r;
-    uint64_t carry;
-    asm("v_addc_co_u32_e64 %0, %1, 0, %2, %3" : "=v"(r), "=s"(carry) : "v"(v), "s"(m));
-    return r;
-}
-
 // sum of the copies of count c
 __device__ __forceinline__ uint32_t sel_count(const uint32_t *cnt, uint32_t c) {
     uint32_t s = 0;
@@ -1597,6 +1580,7 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
         const uint32_t key = __builtin_bit_cast(uint32_t, c);
         atomicAdd(reinterpret_cast<uint32_t *>(cnt + ((key & 0xFFFFu) >> kCntShift)), 1u);
         atomicAdd(reinterpret_cast<uint32_t *>(cnt + (key >> (16 + kCntShift))), 1u);
+        wave_fence();  // the counts every lane added
         const uint32_t s = sel_count(S.cnt, ln);  // exponent ln's count up to the row's end
         const uint32_t seen = prev;
         prev = s;
@@ -1619,7 +1603,8 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
                 if (m0 && mbcnt(M0) == qk) a.rec[j] = record(ck, w0);
             } else {        // a high element: rank qk - n0 among the high ones
                 const bool m1 = c1 == kk;
-                if (m1 && mbcnt(ballot(m1)) == qk - n0) a.rec[j] = record(ck, w1);
+                const uint64_t M1 = ballot(m1);  // by every lane: a wave-wide vote
+                if (m1 && mbcnt(M1) == qk - n0) a.rec[j] = record(ck, w1);
             }
             ++j;
             clear_bit(H, k);

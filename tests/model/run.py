@@ -1,0 +1,197 @@
+"""Runs crukx_sync's Python layer on the CPU model of the library (tests/model/, libcrukx_model.so):
+the library's own kernels and host code, built for the CPU under AddressSanitizer and UBSan, with
+every kernel run by the wave64 emulator of simt.cpp.  Test infrastructure only.
+
+The process must start with the sanitizer runtime preloaded (`env()` gives the environment); it then
+binds crukx_sync to the model library and routes the few device-only pieces of the Python layer to
+the CPU: tensors live in host memory, the "device" is the CPU, every stream is the null stream.  The
+rest of the Python layer (argument checks, caches, the receiver's exponent counts and their
+lifecycle) runs unchanged.
+
+    python tests/model/run.py <scenario> [args]   (scenarios below)
+"""
+
+from __future__ import annotations
+
+import contextlib
+import ctypes
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+LIB = os.path.join(HERE, "_build", "libcrukx_model.so")
+CLANG = "/opt/rocm/llvm/bin/clang++"
+
+
+def build() -> str:
+    """Builds the model library (make in tests/model); returns its path."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB
+
+
+def asan_runtime() -> str:
+    out = subprocess.run([CLANG, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    path = out.stdout.strip()
+    if not os.path.isabs(path):  # this clang keeps it under its resource directory
+        res = subprocess.run([CLANG, "-print-resource-dir"], capture_output=True, text=True).stdout.strip()
+        path = os.path.join(res, "lib", "linux", "libclang_rt.asan-x86_64.so")
+    return path
+
+
+def env(lib: str | None = None) -> dict:
+    """The environment of a model process: the sanitizer runtime first, leaks not reported (the
+    interpreter keeps its own until exit), a sanitizer report ends the process with status 86."""
+    e = dict(os.environ)
+    e["LD_PRELOAD"] = asan_runtime()
+    # every allocation filled with 0xBE: a read of device memory no kernel wrote shows in the results
+    e["ASAN_OPTIONS"] = ("detect_leaks=0:detect_stack_use_after_return=0:exitcode=86:abort_on_error=0:"
+                         "malloc_fill_byte=190:max_malloc_fill_size=1099511627776")
+    e["UBSAN_OPTIONS"] = "print_stacktrace=1:halt_on_error=1:exitcode=86"
+    e["CRX_LIBRARY"] = lib or LIB
+    e["OMP_NUM_THREADS"] = "1"
+    return e
+
+
+def install():
+    """Binds crukx_sync to the model library (CRX_LIBRARY) and routes its device plumbing to the CPU."""
+    for p in (os.path.join(ROOT, "crukx-sync_amd"), os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")):
+        if p not in sys.path:
+            sys.path.insert(0, p)
+    assert os.environ.get("CRX_LIBRARY"), "start the process with run.env()"
+    import torch
+
+    import crukx_sync  # noqa: F401
+    from crukx_sync import _native, codec, wire
+
+    assert os.path.samefile(_native.LIB_PATH, os.environ["CRX_LIBRARY"])
+    codec._hip_device = lambda dev: dev          # the model's device is the CPU
+    _native.stream_of = lambda dev: 0            # the null stream
+    torch.cuda.device = lambda d: contextlib.nullcontext()
+
+    def parse_tensor(t, L, err):
+        """wire._parse_tensor's device branch for a host tensor: the header and block table are parsed
+        from a copy of the leading bytes, and apply reads the block table and payload from `t` itself."""
+        if t.dtype != torch.uint8 or t.dim() != 1 or not t.is_contiguous():
+            raise TypeError("an update tensor must be a contiguous 1-D uint8 tensor")
+        total = t.numel()
+        if total == 0:
+            return wire.parse(b"")
+        have = min(total, 1 << 16)
+        while True:
+            host = torch.empty(have + 1, dtype=torch.uint8)
+            host[:have].copy_(t[:have])
+            host[have:].copy_(t[total - 1:])
+            h, need = ctypes.c_void_p(), ctypes.c_uint64()
+            rc = L.crx_parse_prefix(ctypes.c_void_p(host.data_ptr()), have, total, int(host[have]), ctypes.byref(h),
+                                    ctypes.byref(need), err, 512)
+            if rc == _native.INVALID and need.value > have:
+                have = min(total, max(need.value + 64, 2 * have))
+                continue
+            _native.raise_for(rc, err)
+            return wire.ParsedUpdate(h.value, host, dev_bytes=t)
+
+    wire._parse_tensor = parse_tensor
+
+
+# ------------------------------------------------------------------ scenarios
+
+def scenario_parity() -> None:
+    """Encode (bytes and the device-resident form) and apply of the small scenarios against the oracle."""
+    import torch
+
+    import crukx_sync
+    import oracle
+    import scenarios
+    sc = scenarios.single_scenarios()
+    names = sorted(sc)
+    for name in names:
+        old, new = sc[name]
+        upd = crukx_sync.encode_update(old, new)
+        ref = oracle.encode_update(old, new)
+        assert upd == ref, f"{name}: model bytes differ from the oracle ({len(upd)} vs {len(ref)})"
+        dev = crukx_sync.encode_update_device(old, new)
+        assert bytes(dev.numpy()) == ref, name
+        for u in (upd, dev):
+            w = {k: v.clone() for k, v in old.items()}
+            crukx_sync.apply_update(w, u)
+            for k in new:
+                assert torch.equal(w[k].view(torch.int16), new[k].view(torch.int16)), (name, k)
+        print(f"parity {name}: {len(upd)} bytes", flush=True)
+
+
+def scenario_small4_flips(first: int = 0, count: int = -1, every: int = 1) -> None:
+    """The four-tensor exhaustive corruption sequence of tests/test_full_sizes.py, on the model: the
+    same weights (seed 7), steps, caches, device-resident update and flips in the same order.  Flips
+    [first, first + count) of the list are applied (every `every`-th), starting from the warm state."""
+    import random
+
+    import torch
+
+    import crukx_sync
+    from crukx_sync import CorruptUpdate, _native, wire, workloads
+
+    def equal(x, y):
+        return all(torch.equal(x[k].view(torch.int16), y[k].view(torch.int16)) for k in x)
+
+    def varint_len(v):
+        n = 1
+        while v >= 0x80:
+            v >>= 7
+            n += 1
+        return n
+
+    shapes = workloads.small4_shapes()
+    p0 = workloads.make_weights(shapes, seed=7, device="cpu")
+    p1 = workloads.make_step(p0, 1, rho=0.01, seed=7)
+    p2 = workloads.make_step(p1, 2, rho=0.01, seed=7)
+    send, rc = {}, {}
+    recv = {k: v.clone() for k, v in p0.items()}
+    crukx_sync.apply_update(recv, crukx_sync.encode_update_device(p0, p1, send), rc)
+    assert equal(recv, p1)
+    chk1 = {k: v[0] for k, v in rc.items()}
+    buf = crukx_sync.encode_update_device(p1, p2, send)
+    u, L = wire.parse(buf), _native.lib()
+    n_blocks = L.crx_update_n_blocks(u.handle)
+    pay, pay_len = L.crx_update_payload_offset(u.handle), L.crx_update_payload_len(u.handle)
+    bt = pay - varint_len(pay_len) - 4 * n_blocks
+    del u
+    rnd = random.Random(11)
+    offsets = list(range(bt))
+    for b in range(n_blocks):
+        offsets += [bt + 4 * b, bt + 4 * b + 3]
+    offsets += list(range(bt + 4 * n_blocks, pay))
+    offsets += [pay, pay + pay_len - 1] + rnd.sample(range(pay + 1, pay + pay_len - 1), 10_000)
+    print(f"small4: {len(offsets)} flips ({bt} header bytes, {n_blocks} blocks, {pay_len} payload bytes)", flush=True)
+    end = len(offsets) if count < 0 else min(len(offsets), first + count)
+    rejected = applied = 0
+    for j in range(first, end, every):
+        i = offsets[j]
+        x = (0x01, 0x80, 0xFF)[j % 3]
+        buf[i:i + 1].bitwise_xor_(x)
+        try:
+            crukx_sync.apply_update(recv, buf, rc)
+        except (CorruptUpdate, ValueError):
+            rejected += 1
+        else:
+            applied += 1
+            assert equal(recv, p2), (i, x)
+            for k in recv:
+                recv[k].copy_(p1[k])
+            rc.update({k: (chk1[k], recv[k]._version) for k in recv})
+        buf[i:i + 1].bitwise_xor_(x)
+        assert equal(recv, p1), f"a write after the flip of byte {i} by {x:#x} (flip {j})"
+        if (j - first) % (50 * every) == 0 or j + every >= end:
+            print(f"small4: flip {j} (byte {i} ^ {x:#x}): {rejected} rejected, {applied} applied", flush=True)
+    crukx_sync.apply_update(recv, buf, rc)
+    assert equal(recv, p2)
+    assert send == {k: v[0] for k, v in rc.items()}
+    print(f"small4 done: flips {first}..{end}: {rejected} rejected, {applied} applied", flush=True)
+
+
+SCENARIOS = {"parity": scenario_parity, "small4_flips": scenario_small4_flips}
+
+if __name__ == "__main__":
+    install()
+    SCENARIOS[sys.argv[1]](*[int(a) for a in sys.argv[2:]])
