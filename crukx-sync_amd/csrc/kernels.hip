@@ -1350,7 +1350,11 @@ __global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
         a.done[blockIdx.x * kLocTiles + ln] = 0;
         a.multi[blockIdx.x * kLocTiles + ln] = 0;
     }
-    if (*a.bad) return;
+    if (*a.bad) {  // an update already rejected: no records; rstart defined all the same
+        if (ln < kLocTiles && blockIdx.x * kLocTiles + ln < tiles) a.rstart[blockIdx.x * kLocTiles + ln] = 0;
+        if (ln == 0 && blockIdx.x == 0) a.rstart[tiles] = 0;
+        return;
+    }
     if (ln < kLocTiles) before[ln] = 0;
     // slab u of the wavefront, exponents ln + 64 q: those with a group are packed into consecutive
     // entries, so that the lower-bound searches (one per lane) take as few load instructions as the
@@ -1985,19 +1989,26 @@ __global__ __launch_bounds__(256) void k_commit(SlabArgs a, uint32_t tiles) {
     for (uint32_t tau = blockIdx.x; tau < tiles; tau += gridDim.x) {
         const bool multi = a.multi[tau] != 0;
         if (multi != ok) continue;  // verified and written through, or not verified and never written
-        const uint32_t r0 = a.rstart[tau], r1 = multi ? a.rstart[tau + 1] : r0 + a.done[tau];
+        // done is zero unless the select pass wrote the slab (k_locate clears it first): nothing to undo,
+        // and rstart is not read (k_locate does not locate the records of an update already rejected)
+        const uint32_t done = multi ? 1u : a.done[tau];
+        if (!done) continue;
+        // the records [r0, r0 + n), within the record buffer whatever rstart holds; counted from 0 so
+        // that no index wraps
+        const uint32_t r0 = min(a.rstart[tau], a.n_changes);
+        const uint32_t n = min(multi ? a.rstart[tau + 1] - r0 : done, a.n_changes - r0);
         const TensorDesc td = a.descs[a.tile_tensor[tau]];
         const uint64_t first = (uint64_t)(tau - td.tile_begin) * a.slab;
         const uint32_t extent = (uint32_t)min64(a.slab, td.numel - first);  // offsets of found targets lie below
         uint16_t *const base = td.base + first;
         if (multi) {
-            for (uint32_t i = r0 + threadIdx.x; i < r1; i += 256) {
-                const uint32_t v = a.pn[i];
+            for (uint32_t k = threadIdx.x; k < n; k += 256) {
+                const uint32_t v = a.pn[r0 + k];
                 if ((v & 0xFFFFu) < extent) base[v & 0xFFFFu] = (uint16_t)(v >> 16);
             }
-        } else {  // done is zero unless the select pass wrote the slab (k_locate clears it): an empty loop then
-            for (uint32_t i = r0 + threadIdx.x; i < r1; i += 256) {
-                const unsigned long long rc = a.rec[i];
+        } else {
+            for (uint32_t k = threadIdx.x; k < n; k += 256) {
+                const unsigned long long rc = a.rec[r0 + k];
                 const uint32_t off = (uint32_t)(rc >> 32) & 0xFFFFu;
                 if (off < extent) base[off] = (uint16_t)(rc >> 48);
             }

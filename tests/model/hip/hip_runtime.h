@@ -20,7 +20,9 @@
 #define __global__
 #define __device__
 #define __host__
-#define __shared__ static
+// LDS variables live in one section, so that the emulator can refill them at every workgroup's start
+// (LDS holds no values from earlier workgroups on the GPU either)
+#define __shared__ static __attribute__((section("simt_lds")))
 #define __constant__ static
 #define __launch_bounds__(...)
 #define __forceinline__ inline __attribute__((always_inline))

@@ -45,9 +45,10 @@ def env(lib: str | None = None) -> dict:
     interpreter keeps its own until exit), a sanitizer report ends the process with status 86."""
     e = dict(os.environ)
     e["LD_PRELOAD"] = asan_runtime()
-    # every allocation filled with 0xBE: a read of device memory no kernel wrote shows in the results
+    # every allocation filled with 0xFF: device memory that no kernel wrote reads as all ones (the
+    # kernels' "none" value, and the value closest to wrapping in index arithmetic)
     e["ASAN_OPTIONS"] = ("detect_leaks=0:detect_stack_use_after_return=0:exitcode=86:abort_on_error=0:"
-                         "malloc_fill_byte=190:max_malloc_fill_size=1099511627776")
+                         "malloc_fill_byte=255:max_malloc_fill_size=4294967295")
     e["UBSAN_OPTIONS"] = "print_stacktrace=1:halt_on_error=1:exitcode=86"
     e["CRX_LIBRARY"] = lib or LIB
     e["OMP_NUM_THREADS"] = "1"
@@ -165,15 +166,24 @@ def scenario_small4_flips(first: int = 0, count: int = -1, every: int = 1) -> No
     offsets += [pay, pay + pay_len - 1] + rnd.sample(range(pay + 1, pay + pay_len - 1), 10_000)
     print(f"small4: {len(offsets)} flips ({bt} header bytes, {n_blocks} blocks, {pay_len} payload bytes)", flush=True)
     end = len(offsets) if count < 0 else min(len(offsets), first + count)
+    verbose = bool(os.environ.get("SMALL4_VERBOSE"))
     rejected = applied = 0
-    for j in range(first, end, every):
+    order = range(first, end, every)
+    if os.environ.get("SMALL4_LIST"):  # an explicit list of flip indices
+        order = [int(v) for v in os.environ["SMALL4_LIST"].split(",")]
+        end = max(order) + 1
+    for j in order:
         i = offsets[j]
         x = (0x01, 0x80, 0xFF)[j % 3]
+        if verbose:
+            print(f"small4: flip {j}: byte {i} ^ {x:#x}", flush=True)
         buf[i:i + 1].bitwise_xor_(x)
         try:
             crukx_sync.apply_update(recv, buf, rc)
-        except (CorruptUpdate, ValueError):
+        except (CorruptUpdate, ValueError) as e:
             rejected += 1
+            if verbose:
+                print(f"small4:   {type(e).__name__}: {e}", flush=True)
         else:
             applied += 1
             assert equal(recv, p2), (i, x)
@@ -182,7 +192,10 @@ def scenario_small4_flips(first: int = 0, count: int = -1, every: int = 1) -> No
             rc.update({k: (chk1[k], recv[k]._version) for k in recv})
         buf[i:i + 1].bitwise_xor_(x)
         assert equal(recv, p1), f"a write after the flip of byte {i} by {x:#x} (flip {j})"
-        if (j - first) % (50 * every) == 0 or j + every >= end:
+        if verbose:
+            import hashlib
+            print(f"small4:   update bytes {hashlib.sha1(buf.numpy().tobytes()).hexdigest()[:12]}", flush=True)
+        if verbose or (j - first) % (50 * every) == 0 or j + every >= end:
             print(f"small4: flip {j} (byte {i} ^ {x:#x}): {rejected} rejected, {applied} applied", flush=True)
     crukx_sync.apply_update(recv, buf, rc)
     assert equal(recv, p2)
@@ -190,7 +203,61 @@ def scenario_small4_flips(first: int = 0, count: int = -1, every: int = 1) -> No
     print(f"small4 done: flips {first}..{end}: {rejected} rejected, {applied} applied", flush=True)
 
 
-SCENARIOS = {"parity": scenario_parity, "small4_flips": scenario_small4_flips}
+def scenario_rejected_early() -> None:
+    """Updates the decoder rejects, applied to multi-slab tensors (4096-element slabs) while device
+    memory starts as all ones: each raises CorruptUpdate and leaves the receiver as it was.  Two
+    neighbouring block-table entries are moved by one bit in opposite directions (the header and the
+    payload length still parse), so both blocks fail to decode and the update is rejected before its
+    changes are located; the receivers' caches are warm, as in a training run.  The undo pass once
+    took such an update's never-written record offsets (all ones) as a range to restore and walked
+    past the record buffer."""
+    import struct
+
+    import torch
+
+    import crukx_sync
+    import scenarios
+    from crukx_sync import CorruptUpdate, _native, codec, wire
+
+    codec._SLAB = 4096
+    old, new = {}, {}
+    for i, n in enumerate([300_000, 50_001, 4_097]):
+        a, b = scenarios.rl_pair(n, lr=4e-6, seed=80 + i)
+        old[f"t{i}"], new[f"t{i}"] = a, b
+    send, rc = {}, {}
+    recv = {k: v.clone() for k, v in old.items()}
+    crukx_sync.apply_update(recv, crukx_sync.encode_update(old, new, send), rc)  # caches warm
+    old, new = new, old  # the updates below take the receiver back
+    upd = bytearray(crukx_sync.encode_update(old, new, send))
+    u = wire.parse(bytes(upd))
+    L = _native.lib()
+    n_blocks, pay = L.crx_update_n_blocks(u.handle), L.crx_update_payload_offset(u.handle)
+    pay_len = L.crx_update_payload_len(u.handle)
+    n = 1
+    while pay_len >= 128 ** n:
+        n += 1
+    bt = pay - n - 4 * n_blocks
+    bits = list(struct.unpack_from(f"<{n_blocks}I", upd, bt))
+    rejected = 0
+    for b in range(0, n_blocks - 1, max(1, n_blocks // 12)):
+        bad = bytearray(upd)
+        struct.pack_into("<II", bad, bt + 4 * b, bits[b] + 1, bits[b + 1] - 1)
+        for form in (bytes(bad), torch.frombuffer(bytearray(bad), dtype=torch.uint8)):
+            try:
+                crukx_sync.apply_update(recv, form, rc)
+            except CorruptUpdate:
+                rejected += 1
+            else:
+                raise AssertionError(f"blocks {b}, {b + 1} moved by one bit: applied")
+            for k in old:
+                assert torch.equal(recv[k].view(torch.int16), old[k].view(torch.int16)), (b, k)
+    crukx_sync.apply_update(recv, bytes(upd), rc)
+    for k in new:
+        assert torch.equal(recv[k].view(torch.int16), new[k].view(torch.int16)), k
+    print(f"rejected early: {rejected} updates rejected, the receiver unchanged each time", flush=True)
+
+
+SCENARIOS = {"parity": scenario_parity, "small4_flips": scenario_small4_flips, "rejected_early": scenario_rejected_early}
 
 if __name__ == "__main__":
     install()

@@ -54,6 +54,9 @@ namespace crx {
 extern bool g_arena_unpooled;
 }
 
+// the LDS variables of the library's kernels (the section of the stand-in's __shared__)
+extern "C" uint8_t __start_simt_lds[], __stop_simt_lds[];
+
 namespace simt {
 namespace {
 
@@ -86,6 +89,9 @@ void *g_ctx = nullptr;
 uint8_t *g_dyn = nullptr;
 uint64_t g_launches = 0;
 uint64_t g_resolves = 0, g_switches = 0;
+const int g_stack_fill = std::getenv("SIMT_STACK_FILL") ? (int)std::strtol(std::getenv("SIMT_STACK_FILL"), nullptr, 0) : -1;
+constexpr size_t kStackFill = 32 << 10;
+const int g_lds_fill = std::getenv("SIMT_LDS_FILL") ? (int)std::strtol(std::getenv("SIMT_LDS_FILL"), nullptr, 0) : 0xA5;
 
 [[noreturn]] void fail(const char *what) {
     std::fprintf(stderr, "simt: %s (launch %llu, workgroup %u)\n", what, (unsigned long long)g_launches, g_block.x);
@@ -163,6 +169,9 @@ void prepare(Fiber &f, uint32_t tid) {
     }
     // (a work-item that returned left its stack as it found it: every frame it entered was left)
     uintptr_t top = ((uintptr_t)f.stack + f.size) & ~uintptr_t(15);
+    // private variables start as what the previous work-item left, as registers do on the GPU;
+    // SIMT_STACK_FILL fills the top of the stack with a byte instead
+    if (g_stack_fill >= 0) std::memset(reinterpret_cast<void *>(top - kStackFill), g_stack_fill, kStackFill);
     void **sp = reinterpret_cast<void **>(top);
     *--sp = nullptr;                                    // fiber_main's return address (never used)
     *--sp = reinterpret_cast<void *>(&fiber_main);      // where simt_switch's ret goes
@@ -323,6 +332,9 @@ void run(dim3 grid, dim3 block, size_t dyn_bytes, void (*body)(void *), void *ct
     const uint64_t r0 = g_resolves, s0 = g_switches;
     for (uint32_t b = 0; b < grid.x; ++b) {
         g_block = Idx{b, 0, 0};
+        // what a workgroup finds in LDS: not what an earlier one left (SIMT_LDS_FILL: the byte)
+        std::memset(__start_simt_lds, g_lds_fill, (size_t)(__stop_simt_lds - __start_simt_lds));
+        if (dyn_bytes) std::memset(g_dyn, g_lds_fill, dyn_bytes);
         for (uint32_t t = 0; t < g_n; ++t) prepare(g_pool[t], t);
         schedule();
     }
