@@ -76,9 +76,8 @@ def apply_update(weights: Mapping[str, torch.Tensor], update, checksums: dict | 
     """Write the update into `weights` in place; on any error the weights end as they were. `update`
     is the bytes from encode_update or the uint8 tensor from encode_update_device. Most changes are
     written while they are located, before the update's checksums are verified, and put back if the
-    update does not verify; the last writes (or that undoing) are ordered on the current stream, like
-    any in-place torch operation on the weights, so later work on that stream sees all of the update
-    or none of it."""
+    update does not verify; the call returns once the last writes (or that undoing) are done, so
+    later work on any stream sees all of the update or none of it."""
     u = parse(update)
     with torch.no_grad():
         changed = codec.apply(weights, u, checksums)

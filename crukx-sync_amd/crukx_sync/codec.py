@@ -21,14 +21,16 @@ import numpy as np
 import torch
 
 from . import _native
-from .wire import (BLOCK, MAX_CODE_LEN, MAX_RICE, MAX_SYMBOL, CorruptUpdate, Group, ParsedUpdate,  # noqa: F401
-                   Table, TensorHeader, Update, new_bytes, parse, serialize)
+from .wire import (BLOCK, MAX_CODE_LEN, MAX_RICE, MAX_SYMBOL, CorruptUpdate, Group, NativeUpdate,  # noqa: F401
+                   ParsedUpdate, Table, TensorHeader, Update, new_bytes, parse, serialize)
 
 _MASK64 = (1 << 64) - 1
-# Elements ranked by one wavefront (a multiple of 128, at most 2^17).  The reference's _SLAB bounds
-# the size of one stable sort (codec.py:30); here it cuts tensors into slabs whose exponent
-# histograms are scanned afterwards.  Either way it changes how work is split, never the bytes.
-_SLAB = 1 << 16
+# The reference's knob (codec.py:30), with its default: tensors of more than _SLAB elements get their
+# group sizes checked against the receiver's exponent counts before decoding ("group has more changes
+# than elements", codec.py:598-604).  The reference also sorts at most _SLAB elements at once; here one
+# wavefront ranks min(_SLAB, 65536) elements (rounded down to a multiple of 128), and the per-slab
+# exponent histograms are scanned afterwards.  It never changes the bytes.
+_SLAB = 1 << 24
 
 
 # ---------------------------------------------------------------- shared helpers
@@ -141,7 +143,7 @@ def _names_c(names: list[str]):
     return hit
 
 
-class EncodedUpdate(Update):
+class EncodedUpdate(NativeUpdate):
     """An update encoded on the device: header on the host, block table and payload in HBM."""
 
     def __init__(self, handle, names: list[str], device, workspace):
@@ -173,6 +175,8 @@ class EncodedUpdate(Update):
 
     def to_device(self) -> torch.Tensor:
         """The serialized update as a uint8 tensor on the encoding device."""
+        if self.edited:
+            return torch.frombuffer(bytearray(serialize(self)), dtype=torch.uint8).to(self._device)
         out = torch.empty(self.nbytes(), dtype=torch.uint8, device=self._device)
         self._write(out.data_ptr(), True)
         return out
@@ -185,8 +189,7 @@ class EncodedUpdate(Update):
                                                  _native.stream_of(self._device), err, 512)
         _native.raise_for(rc, err)
 
-    @property
-    def tensors(self) -> list[TensorHeader]:
+    def _read_tensors(self) -> list[TensorHeader]:
         if self._tensors is None:
             L = _native.lib()
             e, cnt, r = ctypes.c_int32(), ctypes.c_uint64(), ctypes.c_int32()
@@ -202,12 +205,7 @@ class EncodedUpdate(Update):
             self._tensors = out
         return self._tensors
 
-    @tensors.setter
-    def tensors(self, v):
-        self._tensors = v
-
-    @property
-    def tables(self) -> list[Table]:
+    def _read_tables(self) -> list[Table]:
         L = _native.lib()
         e, n = ctypes.c_int32(), ctypes.c_int64()
         out = []
@@ -218,12 +216,7 @@ class EncodedUpdate(Update):
             out.append(Table(e.value, list(syms), list(lens)))
         return out
 
-    @tables.setter
-    def tables(self, v):
-        pass
-
-    @property
-    def block_bits(self) -> list[int]:
+    def _read_block_bits(self) -> list[int]:
         L = _native.lib()
         n = L.crx_encoded_n_blocks(self._h)
         arr = (ctypes.c_uint32 * max(n, 1))()
@@ -231,22 +224,13 @@ class EncodedUpdate(Update):
             _native.raise_for(L.crx_encoded_block_bits(self._h, arr, _native.stream_of(self._device)), None)
         return list(arr[:n])
 
-    @block_bits.setter
-    def block_bits(self, v):
-        pass
-
-    @property
-    def payload(self) -> bytes:
+    def _read_payload(self) -> bytes:
         L = _native.lib()
         n = L.crx_encoded_payload_len(self._h)
         data, addr = new_bytes(n)
         with torch.cuda.device(self._device):
             _native.raise_for(L.crx_encoded_payload(self._h, addr, _native.stream_of(self._device)), None)
         return data
-
-    @payload.setter
-    def payload(self, v):
-        pass
 
 
 def _aligned(t: torch.Tensor) -> torch.Tensor:
@@ -443,7 +427,7 @@ def _device_of(ts: list, what: str) -> torch.device:
 def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None = None) -> int:
     """Verify `u` against `weights`, then write the new values in place. Returns elements changed
     (codec.py:578-717)."""
-    if not isinstance(u, ParsedUpdate):
+    if not isinstance(u, ParsedUpdate) or u.edited:
         u = parse(serialize(u))
     names, numels, header_chk = u.headers()
     if not names:

@@ -15,19 +15,20 @@ from dataclasses import dataclass, field
 
 MAGIC = b"CRXS"
 VERSION = 2
-MAX_CODE_LEN = 17   # residuals span +-65535, so <= 131071 zigzag symbols always fit in 17 bits
+MAX_CODE_LEN = 17   # a 16-bit difference has 131071 zigzag values: a code of 17 bits can name each
 MAX_SYMBOL = 131070
 MAX_RICE = 30
 BLOCK = 256
 
 
 class CorruptUpdate(ValueError):
-    """The update bytes are malformed, truncated, or do not reproduce the expected weights."""
+    """Raised for bytes that break the format, end early, or decode to weights whose checksum is not
+    the one the update carries."""
 
 
 @dataclass
 class Table:
-    """Canonical Huffman table for residual symbols of one old-weight exponent."""
+    """The code of one exponent's residuals: symbols and their canonical Huffman code lengths."""
     exponent: int
     symbols: list[int]
     lengths: list[int]
@@ -101,7 +102,7 @@ def _serialize_plain(u: Update) -> bytes:
 def serialize(u: Update) -> bytes:
     """Bytes of an update: natively for updates produced by encode, else from the plain fields."""
     native = getattr(u, "_serialize_native", None)
-    if native is not None:
+    if native is not None and not u.edited:
         return native()
     return _serialize_plain(u)
 
@@ -123,7 +124,42 @@ def new_bytes(n: int) -> tuple[bytes, int]:
     return b, _PyBytes_AsString(b)
 
 
-class ParsedUpdate(Update):
+class NativeUpdate(Update):
+    """An update whose fields live in the native library until read.  Assigning a field first reads all
+    four into plain Python data; from then on the object behaves as the reference's mutable Update
+    (wire.py:44-48): serialize() and apply use the edited fields."""
+
+    _FIELDS = ("tables", "tensors", "block_bits", "payload")
+
+    @property
+    def edited(self) -> bool:
+        return self.__dict__.get("_fields") is not None
+
+    def _materialise(self) -> dict:
+        f = self.__dict__.get("_fields")
+        if f is None:
+            f = {name: getattr(self, "_read_" + name)() for name in self._FIELDS}
+            self.__dict__["_fields"] = f
+        return f
+
+
+def _field(name):
+    def fget(self):
+        f = self.__dict__.get("_fields")
+        return f[name] if f is not None else getattr(self, "_read_" + name)()
+
+    def fset(self, v):
+        self._materialise()[name] = v
+
+    return property(fget, fset)
+
+
+for _n in NativeUpdate._FIELDS:
+    setattr(NativeUpdate, _n, _field(_n))
+del _n
+
+
+class ParsedUpdate(NativeUpdate):
     """An update parsed by the native library; fields are materialised on first access."""
 
     def __init__(self, handle, source, dev_bytes=None):
@@ -166,8 +202,7 @@ class ParsedUpdate(Update):
             self._headers = (out, list(numels[:n]), list(chks[:n]))
         return self._headers
 
-    @property
-    def tensors(self) -> list[TensorHeader]:
+    def _read_tensors(self) -> list[TensorHeader]:
         if self._tensors is None:
             from . import _native
             L = _native.lib()
@@ -187,12 +222,7 @@ class ParsedUpdate(Update):
             self._tensors = out
         return self._tensors
 
-    @tensors.setter
-    def tensors(self, v):
-        self._tensors = v
-
-    @property
-    def tables(self) -> list[Table]:
+    def _read_tables(self) -> list[Table]:
         if self._tables is None:
             from . import _native
             L = _native.lib()
@@ -207,12 +237,7 @@ class ParsedUpdate(Update):
             self._tables = out
         return self._tables
 
-    @tables.setter
-    def tables(self, v):
-        self._tables = v
-
-    @property
-    def block_bits(self) -> list[int]:
+    def _read_block_bits(self) -> list[int]:
         from . import _native
         L = _native.lib()
         n = L.crx_update_n_blocks(self._h)
@@ -220,22 +245,13 @@ class ParsedUpdate(Update):
         L.crx_update_block_bits(self._h, arr)
         return list(arr[:n])
 
-    @block_bits.setter
-    def block_bits(self, v):
-        pass
-
-    @property
-    def payload(self) -> bytes:
+    def _read_payload(self) -> bytes:
         from . import _native
         L = _native.lib()
         off, n = L.crx_update_payload_offset(self._h), L.crx_update_payload_len(self._h)
         if self._dev_bytes is not None:
             return self._dev_bytes[off:off + n].cpu().numpy().tobytes()
         return bytes(memoryview(self._source)[off:off + n])
-
-    @payload.setter
-    def payload(self, v):
-        pass
 
     @property
     def total_changes(self) -> int:

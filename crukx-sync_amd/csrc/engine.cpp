@@ -126,17 +126,23 @@ struct HostClock {
 };
 
 // ------------------------------------------------------------------ auxiliary stream
-// One extra stream per device and caller stream (default priority, created on first use, kept for
-// the process) for work of a call that can overlap the caller's stream: calls on different caller
-// streams never wait for each other through it.  A Fork makes it wait for everything enqueued on the
-// caller's stream so far; join() makes the caller's stream wait for what was enqueued on it.
+// Extra streams for work of a call that can overlap the caller's stream: a fixed pool of kAuxStreams
+// per device (default priority, created on first use, kept for the process), the caller's stream
+// choosing one by its address, so a caller that makes a new stream per step does not make the pool
+// grow.  Calls on different caller streams rarely share one (and then only queue behind each other's
+// auxiliary work).  A Fork makes it wait for everything enqueued on the caller's stream so far; join()
+// makes the caller's stream wait for what was enqueued on it.
+constexpr int kAuxStreams = 8, kAuxDevices = 64;
 hipStream_t aux_stream(hipStream_t caller) {
     static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, hipStream_t> streams;
+    static hipStream_t pool[kAuxDevices][kAuxStreams] = {};
     int dev = 0;
     HIP_OK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kAuxDevices) throw DeviceError("device index out of range");
+    const uintptr_t h = reinterpret_cast<uintptr_t>(caller);
+    const int k = (int)((h ^ (h >> 7) ^ (h >> 13)) % kAuxStreams);
     std::lock_guard<std::mutex> lk(mu);
-    hipStream_t &st = streams[{dev, caller}];
+    hipStream_t &st = pool[dev][k];
     if (!st) HIP_OK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
     return st;
 }
@@ -467,7 +473,12 @@ void sync(hipStream_t s) {
     t_stage.finish();
 }
 
-// Elements per slab: a multiple of kRow, at most 65536 (slab ranks and offsets are kept in 16 bits).
+// The caller's `slab` is the reference's _SLAB (codec.py:30): tensors of more elements get the exact
+// group-size check before decoding (codec.py:598-604); 0 or less means its default, 2^24.
+uint64_t group_check_numel(int32_t slab) { return slab > 0 ? (uint64_t)slab : (1ULL << 24); }
+
+// Elements per slab: the caller's `slab` as a multiple of kRow, at most 65536 (slab ranks and offsets
+// are kept in 16 bits).
 uint32_t slab_size(int32_t slab) {
     if (slab <= 0) return 65536;
     uint32_t s = (uint32_t)slab;
@@ -1054,7 +1065,8 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     fork.join();
     hc.mark("apply_pass_a");
 
-    BlockArgs ba{d_groups, (uint32_t)G, slab, binfo, d_descs, sizes, blk_prefix, local, dz, bad, B};
+    BlockArgs ba{d_groups, (uint32_t)G, slab, binfo, d_descs, sizes, blk_prefix, local, dz, bad, B,
+                 group_check_numel(slab_req)};
     launch_local_fix(ba, B, s);
     uint2 *more = ar.get<uint2>((uint64_t)kSelMoreWindows * tiles);  // windows after the first, per slab
     unsigned int *n_more = ar.get<unsigned int>(1);
@@ -1119,8 +1131,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     }
     if (hbad) throw Corrupt("payload positions outside their exponent groups");
     g_apply_hint.put(hint_key, ar.total);
-    // the verdict is final: the writes are left ordered on the stream, as an in-place torch op's
-    // would be (the reference's index_put_, codec.py:706, is not waited for either)
+    // the verdict is final, and the writes behind it are done (the downloads above followed them)
     *changed = C;
 }
 

@@ -20,9 +20,9 @@ constexpr unsigned int kBadDecode = 1;    // a block does not decode exactly to 
 constexpr unsigned int kBadLocal = 2;     // a change lies beyond its exponent group
 constexpr unsigned int kBadUnplaced = 4;  // a change was not found in the receiver's weights
 // a group has more changes than its tensor has elements of that exponent, in a tensor of more than
-// 2^24 elements (the reference raises this before decoding, codec.py:598-604)
+// `slab` elements (BlockArgs::group_check_numel; the reference raises this before decoding for tensors
+// larger than its _SLAB, codec.py:598-604)
 constexpr unsigned int kBadGroup = 8;
-constexpr uint64_t kGroupCheckNumel = 1ULL << 24;
 
 // One tensor of a call.  Elements are read as 32-bit words from `frame`, the 4-byte aligned address
 // at or below the first element: tensor element i is 16-bit frame element i + lead.
@@ -199,6 +199,7 @@ struct BlockArgs {                  // per-block kernels over the change list (o
     const unsigned long long *dz;   // [changes] decoder output: zz | (block-relative local << 32)
     unsigned int *bad;
     uint64_t n_blocks;
+    uint64_t group_check_numel;     // tensors of more elements report a group larger than its exponent's count as kBadGroup
 };
 
 void launch_enc_rank(const EncRankArgs &a, uint32_t tiles, hipStream_t s);

@@ -1321,7 +1321,7 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
         // a group with more changes than the receiver has elements of its exponent (checked even
         // after a failed decode: the reference checks it first)
         if (r[u].cnt && b == r[u].blk_base && r[u].count > size[u] && threadIdx.x == 0)
-            atomicOr(a.bad, a.descs[r[u].tensor].numel > kGroupCheckNumel ? kBadGroup : kBadLocal);
+            atomicOr(a.bad, a.descs[r[u].tensor].numel > a.group_check_numel ? kBadGroup : kBadLocal);
     }
     if (failed) return;
 #pragma unroll

@@ -21,15 +21,16 @@
  *     keeps until the process ends.  Copies of an update's bytes between device memory and
  *     pageable host memory go through 64 MiB of pinned buffers (allocated once per process) on up
  *     to four threads that the call starts and joins.  Work runs on `stream` (a hipStream_t).
- *     Results are final on return; crx_apply's last writes (or the undoing of its writes, as the
- *     device's verdict decides) and crx_encoded_write's device copies are left ordered on `stream`,
- *     so the buffers `alloc`
- *     handed out must stay usable by work already on `stream` after the call (a stream-ordered
- *     allocator such as torch's caching allocator does this).  Everything else is complete on
- *     return.
- *   - `slab` is the number of elements ranked by one wavefront (a multiple of 128, at most
- *     65536; 0 = default 65536).  It plays the role of codec._SLAB (codec.py:30): it changes
- *     how the work is cut, never the bytes.
+ *     Results are final on return.  crx_apply returns once its writes (or, for an update that does
+ *     not verify, the restoring of what it wrote) are done: the host waits for the verdict's data,
+ *     which the stream delivers after the last write.  crx_encoded_write's copies into device memory
+ *     are left ordered on `stream`, so the buffers `alloc` handed out must stay usable by work
+ *     already on `stream` after the call (a stream-ordered allocator such as torch's caching
+ *     allocator does this).  Everything else is complete on return.
+ *   - `slab` is the reference's codec._SLAB (codec.py:30; 0 = its default, 2^24).  As there, apply
+ *     checks the group sizes of tensors of more than `slab` elements before decoding (codec.py:598-604,
+ *     "group has more changes than elements").  It also bounds the elements ranked by one wavefront:
+ *     min(slab, 65536) rounded down to a multiple of 128 (at least 128).  It never changes the bytes.
  */
 #ifndef CRUKX_H
 #define CRUKX_H
@@ -176,10 +177,10 @@ void crx_encoded_free(crx_encoded *e);
 int32_t crx_checksum(const uint16_t *data, uint64_t n, void *stream, crx_alloc_fn alloc, void *alloc_ctx,
                      uint64_t *out, char *err, uint64_t errlen);
 /* crx_checksum without any allocation: no counterpart in the reference.  For callers that cannot
- * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the
- * per-workgroup partial sums live in a static device array of 2049 u64 (16 KiB per device, held
- * until the process ends) instead of memory from an allocator, and the result goes to *out (host
- * memory) through a plain copy; the call waits for `stream`.  n must be below 2^32 (as for
+ * allocate (tight serving loops, harnesses that forbid hipMalloc): the per-workgroup partial sums live
+ * in a static device array of 2049 u64 (16 KiB per device, held until the process ends) instead of
+ * memory from an allocator, and the result goes to *out (host memory) through a plain copy; the call
+ * waits for `stream`, so it cannot be used inside stream capture.  n must be below 2^32 (as for
  * crx_checksum; CRX_INVALID otherwise).  Calls that overlap on one device share that array and
  * race: serialize them. */
 int32_t crx_checksum_noalloc(const uint16_t *data, uint64_t n, void *stream, uint64_t *out, char *err,

@@ -257,7 +257,40 @@ def scenario_rejected_early() -> None:
     print(f"rejected early: {rejected} updates rejected, the receiver unchanged each time", flush=True)
 
 
-SCENARIOS = {"parity": scenario_parity, "small4_flips": scenario_small4_flips, "rejected_early": scenario_rejected_early}
+def scenario_group_message() -> None:
+    """The group-size check covers tensors of more than codec._SLAB elements (codec.py:598-604): a
+    20,000-element tensor whose group outnumbers the receiver's elements of its exponent is refused by
+    the verification with the default _SLAB, and with "group has more changes than elements" once
+    _SLAB is 4096; the receiver is unchanged either way."""
+    import torch
+
+    import crukx_sync
+    from crukx_sync import CorruptUpdate, codec
+
+    n = 20_000
+    base = torch.full((n,), 0x3F80, dtype=torch.int16)
+    sender = base.clone()
+    sender[100:105] = 0x3C00
+    target = sender.clone()
+    target[100:105] += 1
+    upd = crukx_sync.encode_update({"w": sender}, {"w": target})
+    short = base.clone()
+    short[100:103] = 0x3C00
+    msgs = []
+    for slab in (1 << 24, 4096):
+        codec._SLAB = slab
+        w = {"w": short.clone()}
+        try:
+            crukx_sync.apply_update(w, upd)
+        except CorruptUpdate as e:
+            msgs.append(str(e))
+        assert torch.equal(w["w"], short)
+    assert len(msgs) == 2 and msgs[0] != msgs[1] and msgs[1] == "group has more changes than elements", msgs
+    print(f"group message: {msgs}", flush=True)
+
+
+SCENARIOS = {"parity": scenario_parity, "small4_flips": scenario_small4_flips, "rejected_early": scenario_rejected_early,
+             "group_message": scenario_group_message}
 
 if __name__ == "__main__":
     install()

@@ -219,3 +219,25 @@ def test_tensor_metadata_helper_agrees_with_the_tensors():
         M.meta([ts[0], None])
     with pytest.raises(TypeError):
         M.meta_pair([ts[0]], [None])
+
+
+def test_parsed_update_fields_are_editable_like_the_reference_dataclass(golden):
+    """The reference's Update is a plain mutable dataclass (wire.py:44-48).  An update parsed by the
+    native library reads its fields lazily; assigning one turns it into plain data, so serialize()
+    writes what was assigned."""
+    rec = golden["updates"]["single"]["three_tensors"]["update"]
+    sc = __import__("scenarios").single_scenarios()["three_tensors"]
+    data = oracle.encode_update(*sc)
+    assert hashlib.sha256(data).hexdigest() == rec["sha256"]
+    u = wire.parse(data)
+    assert not u.edited and wire.serialize(u) == data
+    plain = wire.Update(u.tables, u.tensors, u.block_bits, u.payload)
+    assert wire.serialize(plain) == data
+    u.payload = u.payload[:-1] + bytes([u.payload[-1] ^ 0x80])
+    assert u.edited
+    edited = wire.serialize(u)
+    assert len(edited) == len(data) and edited[:-1] == data[:-1] and edited[-1] == data[-1] ^ 0x80
+    u.tables = u.tables[:1]
+    assert wire.serialize(u) == wire.serialize(wire.Update(u.tables, u.tensors, u.block_bits, u.payload))
+    with pytest.raises(crukx_sync.CorruptUpdate):  # the edited update, not the parsed one, is applied
+        codec.apply({k: v.clone() for k, v in sc[0].items()}, u)

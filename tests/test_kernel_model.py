@@ -11,7 +11,8 @@ with device memory in host memory that starts as all ones.  These tests need no 
 - updates that the decoder rejects, on multi-slab tensors with warm caches, raise and leave the receiver
   as it was, with no access outside any buffer.  Before the undo pass was fixed this faulted: it read
   the record offsets that the locate pass does not write for an update already rejected, and all-ones
-  offsets wrapped its 32-bit range start (the GPU fault of the four-tensor corruption test).
+  offsets wrapped its 32-bit range start (the GPU fault of the four-tensor corruption test);
+- the group-size check covers tensors of more than codec._SLAB elements, as in the reference.
 
 The whole four-tensor corruption sequence (`run.py small4_flips`, about 13,500 flips) takes hours on the
 model and is run outside the suite.
@@ -54,3 +55,8 @@ def test_model_bytes_and_applies_match_the_oracle(model):
 def test_updates_rejected_by_the_decoder_write_nothing(model):
     out = _run(model, "rejected_early")
     assert "updates rejected, the receiver unchanged each time" in out
+
+
+def test_group_size_check_follows_the_slab_knob(model):
+    out = _run(model, "group_message")
+    assert "group has more changes than elements" in out

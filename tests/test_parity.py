@@ -417,3 +417,28 @@ def test_verdict_messages_follow_the_reference():
     with pytest.raises(crukx_sync.CorruptUpdate) as e:
         crukx_sync.apply_update({"w": short.cuda()}, upd)
     assert str(e.value) == "group has more changes than elements"
+
+
+def test_group_size_check_follows_the_slab_knob(monkeypatch):
+    """The group-size check covers tensors of more than codec._SLAB elements, as in the reference
+    (codec.py:598-604): with _SLAB lowered to 4096 a 20,000-element tensor whose group outnumbers the
+    receiver's elements of that exponent raises "group has more changes than elements"; with the
+    default (2^24) the same update is refused by the verification instead."""
+    n = 20_000
+    base = torch.full((n,), 0x3F80, dtype=torch.int16)
+    sender = base.clone()
+    sender[100:105] = 0x3C00
+    target = sender.clone()
+    target[100:105] += 1
+    upd = crukx_sync.encode_update({"w": sender.cuda()}, {"w": target.cuda()})
+    short = base.clone()
+    short[100:103] = 0x3C00
+    with pytest.raises(crukx_sync.CorruptUpdate) as e:
+        crukx_sync.apply_update({"w": short.cuda()}, upd)
+    assert str(e.value) != "group has more changes than elements"
+    monkeypatch.setattr(codec, "_SLAB", 4096)
+    w = {"w": short.cuda()}
+    with pytest.raises(crukx_sync.CorruptUpdate) as e:
+        crukx_sync.apply_update(w, upd)
+    assert str(e.value) == "group has more changes than elements"
+    assert torch.equal(w["w"].cpu(), short)
