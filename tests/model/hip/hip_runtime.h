@@ -228,6 +228,16 @@ inline T simt_buffer_load(simt_rsrc r, uint32_t voff, uint32_t soff) {
     std::memcpy(&v, p, sizeof(T));
     return v;
 }
+// Raw buffer stores: the hardware range check drops a store that does not lie wholly below
+// num_records bytes.
+template <typename T>
+inline void simt_buffer_store(T v, simt_rsrc r, uint32_t voff, uint32_t soff) {
+    const uint64_t off = (uint64_t)voff + soff;
+    if (off + sizeof(T) > r.num_records) return;
+    std::memcpy(const_cast<uint8_t *>(r.base) + off, &v, sizeof(T));
+}
+#define __builtin_amdgcn_raw_buffer_store_b16(v, r, voff, soff, aux) simt_buffer_store<uint16_t>((uint16_t)(v), (r), (voff), (soff))
+#define __builtin_amdgcn_raw_buffer_store_b32(v, r, voff, soff, aux) simt_buffer_store<uint32_t>((uint32_t)(v), (r), (voff), (soff))
 #define __builtin_amdgcn_make_buffer_rsrc(p, stride, num, flags) simt_make_rsrc((p), (stride), (num), (flags))
 #define __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, aux) simt_buffer_load<uint32_t>((r), (voff), (soff))
 #define __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, aux) simt_buffer_load<uint16_t>((r), (voff), (soff))
