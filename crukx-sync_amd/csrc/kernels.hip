@@ -1489,9 +1489,7 @@ __device__ __forceinline__ uint32_t sel_count(const uint32_t *cnt, uint32_t c) {
 template <uint32_t CAP>
 struct SelectLds {
     uint32_t cnt[(kWin + kSpare) * kSelCopies];  // running counts, kSelCopies copies (by lane)
-    // the window's targets, per exponent in order: slab rank | min(zz, 0xFFFF) << 16 (0xFFFF: the
-    // residual is read from the decoder's output instead)
-    alignas(16) uint32_t list[CAP];
+    alignas(16) uint16_t list[CAP];                // slab ranks of the window's targets, per exponent in order
     union {
         uint32_t slot[2 * kRow];  // streaming: in-row rank -> record high word; [kRow, 2 kRow): per lane
         uint4 info[64];           // set-up, per lane (its window exponent; zero past kWin): {list begin, list end, change index - list
@@ -1504,16 +1502,10 @@ struct SelectLds {
 // lo | hi << 16).  Within a row the 64 low elements then come before the 64 high ones, each half in
 // lane order, so the rank of an element among the row's elements of one kind needs the ballot of its
 // own half only.
-// The body returns the row (the select pass merges new bits into it); epi(r0, rows) gets each batch's
-// rows as the body returned them, at the start of the next batch: after the wait for that batch's
-// loads and before the loads of the batch after it.  On this GPU one counter tracks both loads and
-// stores, and the wait for a batch's loads also waits for every store issued after them: stores made
-// at the end of a batch would be waited for at once, where stores made here have a whole batch to
-// complete.
-template <int U, int CPOL, typename Body, typename Epi>
-__device__ __forceinline__ void stream_halves(const Slab &sl, const Rsrc &src, Body &&body, Epi &&epi) {
+template <int U, int CPOL, typename Body>
+__device__ __forceinline__ void stream_halves(const Slab &sl, const Rsrc &src, Body &&body) {
     const uint32_t lb = lane() * 2u;
-    u16x2 cur[U], nxt[U], out[U];
+    u16x2 cur[U], nxt[U];
     auto load = [&](u16x2(&dst)[U], uint32_t base) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -1523,39 +1515,24 @@ __device__ __forceinline__ void stream_halves(const Slab &sl, const Rsrc &src, B
     };
     load(cur, lb);
     for (uint32_t r0 = 0; r0 < sl.nrows; r0 += U) {
-        if (r0) epi(r0 - U, out);
         load(nxt, (r0 + U) * 256u + lb);
 #pragma unroll
-        for (int u = 0; u < U; ++u) out[u] = __builtin_bit_cast(u16x2, body(r0 + u, __builtin_bit_cast(uint32_t, cur[u])));
+        for (int u = 0; u < U; ++u) body(r0 + u, __builtin_bit_cast(uint32_t, cur[u]));
 #pragma unroll
         for (int u = 0; u < U; ++u) cur[u] = nxt[u];
     }
-    if (sl.nrows) epi((sl.nrows - 1) / U * U, out);
-}
-
-// new = (old + unzigzag(zz)) mod 2^16 (codec.py:698-700); zz16 is the residual as the LDS list holds it
-// (0xFFFF: read it from the decoder's output for change c)
-__device__ __forceinline__ uint32_t new_bits(const SelectArgs &a, uint32_t old, uint32_t zz16, uint32_t c) {
-    const uint32_t zz = zz16 != 0xFFFFu ? zz16 : (uint32_t)a.dz[min(c, a.n_changes - 1)];
-    const int32_t delta = (int32_t)(zz >> 1) ^ -(int32_t)(zz & 1);
-    return (uint32_t)((int32_t)old + delta) & 0xFFFFu;
 }
 
 template <uint32_t CAP, bool LDS_LIST, bool COLD>
 __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase, SelectLds<CAP> &S,
-                            uint32_t nxt, uint32_t nz, uint32_t ci, const uint32_t cend, const uint32_t jofs,
-                            const uint32_t pre_k, uint32_t j, const bool write_in, uint64_t &fsum) {
-    const bool write = LDS_LIST && write_in;
-    // lane e, for window exponent e: nxt = slab rank of its next target (kFar: none left), nz = its
-    // residual as the LDS list holds it, ci = that target's change index, cend = the end of its changes,
-    // jofs = change index - list index (LDS list), pre_k = its count before the slab (HBM list).  j
-    // (uniform): the window's next record.
+                            uint32_t nxt, uint32_t ci, const uint32_t cend, const uint32_t jofs, const uint32_t pre_k,
+                            uint32_t j, uint64_t &fsum) {
+    // lane e, for window exponent e: nxt = slab rank of its next target (kFar: none left), ci = that
+    // target's change index, cend = the end of its changes, jofs = change index - list index (LDS
+    // list), pre_k = its count before the slab (HBM list).  j (uniform): the window's next record.
     // COLD: the stream also sums the slab's weights for the tensor's checksum (codec.py:61-68) into
     // fsum, as it reads them before any write (the verdict's input when no checksum is cached): the odd
     // rows when the histogram pass streamed the slab (it summed the even ones), else every row.
-    // write (LDS list only): the slab's new bits are merged into the rows as they stream by, and every
-    // 128-byte half-row holding a target is stored whole at the end of its batch (a whole line needs no
-    // read of the old one from HBM, where a 2-byte store makes the memory read and rewrite its sector).
     const uint32_t ln = lane();
     // Per 16-bit half, an element's key is (window index << 7) + (its lane's copy << 5): the counter's
     // byte offset << kCntShift, so one shift gives the address.  Exponents below the window wrap past
@@ -1564,13 +1541,11 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
     const uint32_t kb = (((kbase << 7) - rep) & 0xFFFFu) * 0x10001u;
     const uint32_t sp = (((kWin + ln / kSelCopies) << 7) + rep) * 0x10001u;
     char *const cnt = reinterpret_cast<char *>(S.cnt);
-    // the list entry of the target with change index c (below its exponent's end): slab rank |
-    // residual << 16 from the LDS list, the slab rank alone from HBM
+    // slab rank of the target with change index c (below its exponent's end)
     auto target = [&](uint32_t c, uint32_t jo, uint32_t pr) -> uint32_t {
         if (LDS_LIST) return S.list[min(c - jo, CAP - 1)];
         return a.local[c] - pr;
     };
-    auto rank_of = [](uint32_t e) -> uint32_t { return LDS_LIST ? e & 0xFFFFu : e; };
     // Found targets become records, stored in the order found (rows in order) from record j on: the
     // change index c and the element's high word h = offset in the slab | bits << 16.  (Staging them
     // in LDS for one coalesced store per 64 measured slower than these sequential single stores: select
@@ -1579,13 +1554,12 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
         return (unsigned long long)c | ((unsigned long long)h << 32);
     };
 
-    uint32_t prev = 0;   // exponent ln's count before the row
-    uint32_t dirty = 0;  // (uniform) bit 2u + h: half h of the batch's row u holds a target
-    WeightedSum cs;      // COLD: the checksum sum
+    uint32_t prev = 0;  // exponent ln's count before the row
+    WeightedSum cs;     // COLD: the checksum sum
     const bool odd = td.hist_in == nullptr;  // COLD: the histogram pass summed the even rows
     // COLD: z = (index + 1) * golden of this lane's low element in the current row (its high element: + 64)
     uint64_t z = COLD ? (uint64_t)(2 * (int64_t)sl.first - (int64_t)td.lead + ln + 1) * kGolden : 0;
-    auto row = [&](uint32_t r, uint32_t o) __attribute__((always_inline)) -> uint32_t {
+    stream_halves<kSelectRows, kStreamNT>(sl, slab_rsrc(td.frame, sl), [&](uint32_t r, uint32_t o) {
         // both elements' keys; outside the window or the slab: the spare's
         u16x2 c = __builtin_elementwise_min(as16(o & 0x7F807F80u) - as16(kb), as16(sp));
         const uint32_t f = r * kRow + ln;  // the low element's offset; the high one's is f + 64
@@ -1615,7 +1589,7 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
         const uint32_t seen = prev;
         prev = s;
         uint64_t H = ballot(s > nxt);
-        if (!H) return o;
+        if (!H) return;
         wave_fence();
         // window index << 7 of both elements (the copy term cleared)
         const uint32_t kx = key & 0xFF80FF80u, c0 = kx & 0xFFFFu, c1 = kx >> 16;
@@ -1623,43 +1597,31 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
         const uint32_t w0 = (f - sl.f_lo) | (o << 16), w1 = (f + 64 - sl.f_lo) | (o & 0xFFFF0000u);
         const uint32_t q = nxt - seen;  // in-row rank of the next target, for the exponents in H
         const bool hit = s > nxt;       // this lane's exponent is in H
-        const uint32_t du = 2u * (r % (uint32_t)kSelectRows);  // the row's dirty bits
         do {  // the next target of each exponent with targets in this row: exactly one element
             const uint32_t k = (uint32_t)__builtin_ctzll(H), kk = k << 7;
             const uint32_t qk = rdlane(q, k), ck = rdlane(ci, k);
-            const uint32_t zk = write ? rdlane(nz, k) : 0u;
             const bool m0 = c0 == kk;
             const uint64_t M0 = ballot(m0);
             const uint32_t n0 = (uint32_t)__popcll(M0);  // exponent k's low elements in the row
             if (qk < n0) {  // a low element: the one whose rank among them is qk
-                if (m0 && mbcnt(M0) == qk) {
-                    a.rec[j] = record(ck, w0);
-                    if (write) o = (o & 0xFFFF0000u) | new_bits(a, w0 >> 16, zk, ck);
-                }
-                dirty |= 1u << du;
+                if (m0 && mbcnt(M0) == qk) a.rec[j] = record(ck, w0);
             } else {        // a high element: rank qk - n0 among the high ones
                 const bool m1 = c1 == kk;
                 const uint64_t M1 = ballot(m1);  // by every lane: a wave-wide vote
-                if (m1 && mbcnt(M1) == qk - n0) {
-                    a.rec[j] = record(ck, w1);
-                    if (write) o = (o & 0xFFFFu) | (new_bits(a, w1 >> 16, zk, ck) << 16);
-                }
-                dirty |= 2u << du;
+                if (m1 && mbcnt(M1) == qk - n0) a.rec[j] = record(ck, w1);
             }
             ++j;
             clear_bit(H, k);
         } while (H);
         if (hit) {  // every exponent that had one: its next target, lane-parallel
             ++ci;
-            const uint32_t e = ci < cend ? target(ci, jofs, pre_k) : 0u;
-            nxt = ci < cend ? rank_of(e) : (uint32_t)kFar;
-            nz = e >> 16;
+            nxt = ci < cend ? target(ci, jofs, pre_k) : (uint32_t)kFar;
         }
         H = ballot(s > nxt);
-        if (!H) return o;
+        if (!H) return;
         // more targets of an exponent in this row (rare at low densities): publish its elements by
         // in-row rank (other lanes write a slot of their own past the ranks) and take the rest one per
-        // lane; a taker puts the new bits in the slot, and the element's lane merges them afterwards
+        // lane
         wave_fence();
         do {
             const uint32_t k = (uint32_t)__builtin_ctzll(H);
@@ -1672,62 +1634,25 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
             S.slot[m0 ? rr0 : kRow + ln] = w0;
             S.slot[m1 ? rr1 : kRow + ln] = w1;
             wave_fence();
-            uint32_t n, tr, te;
+            uint32_t n, tl;
             do {  // one target per lane (64 more if all lanes take one); the takers are lanes 0 .. n-1
                 const uint32_t c = ck + ln;
-                te = c < ke ? target(c, jo, pr) : 0u;
-                tr = c < ke ? rank_of(te) : (uint32_t)kFar;
-                const bool take = c < ke && tr < after;  // never past the exponent's own targets
+                tl = c < ke ? target(c, jo, pr) : (uint32_t)kFar;
+                const bool take = c < ke && tl < after;  // never past the exponent's own targets
                 n = (uint32_t)__popcll(ballot(take));
-                if (take) {
-                    const uint32_t h = S.slot[tr - seen_k];
-                    a.rec[j + ln] = record(c, h);
-                    if (write) S.slot[tr - seen_k] = (h & 0xFFFFu) | (new_bits(a, h >> 16, te >> 16, c) << 16);
-                }
+                if (take) a.rec[j + ln] = record(c, S.slot[tl - seen_k]);
                 j += n;
                 ck += n;
             } while (n == 64);
-            const uint32_t tc = rdlane(tr, n), tz = rdlane(te, n) >> 16;  // the first target not taken, or kFar
+            const uint32_t tc = rdlane(tl, n);  // the first target not taken, or kFar
             wave_fence();
-            if (write) {  // the elements taken: their lanes merge the new bits
-                const uint32_t n0b = m0 ? S.slot[rr0] >> 16 : 0u, n1b = m1 ? S.slot[rr1] >> 16 : 0u;
-                const bool t0 = m0 && n0b != (w0 >> 16), t1 = m1 && n1b != (w1 >> 16);
-                if (t0) o = (o & 0xFFFF0000u) | n0b;
-                if (t1) o = (o & 0xFFFFu) | (n1b << 16);
-                dirty |= (ballot(t0) ? 1u : 0u) << du;
-                dirty |= (ballot(t1) ? 2u : 0u) << du;
-                wave_fence();  // the slots are read before the next exponent publishes
-            }
             if (ln == k) {
                 nxt = tc;
-                nz = tz;
                 ci = ck;
             }
             clear_bit(H, k);
         } while (H);
-        return o;
-    };
-    // the batch's half-rows that hold targets, stored whole (only the slab's own elements: a row at
-    // either end of the slab is stored in part).  Buffer stores: a flat store would also count among
-    // the LDS operations, and every LDS wait of the stream would then wait for it.
-    const Rsrc wr = slab_rsrc(td.frame, sl);
-    auto flush = [&](uint32_t r0, const u16x2 (&rows)[kSelectRows]) __attribute__((always_inline)) {
-        if (!write || !dirty) {
-            dirty = 0;
-            return;
-        }
-#pragma unroll
-        for (int u = 0; u < kSelectRows; ++u) {
-            const uint32_t f = (r0 + u) * kRow + ln;
-            if ((dirty >> (2 * u)) & 1u)
-                if (f >= sl.f_lo && f < sl.f_hi) __builtin_amdgcn_raw_buffer_store_b16(rows[u].x, wr, 2 * f, 0, 0);
-            if ((dirty >> (2 * u)) & 2u)
-                if (f + 64 >= sl.f_lo && f + 64 < sl.f_hi)
-                    __builtin_amdgcn_raw_buffer_store_b16(rows[u].y, wr, 2 * (f + 64), 0, 0);
-        }
-        dirty = 0;
-    };
-    stream_halves<kSelectRows, kStreamNT>(sl, slab_rsrc(td.frame, sl), row, flush);
+    });
     // every target of this window's exponents is found once its rank is passed: one still pending
     // lies past the slab's elements of its exponent (never so when the local indices were in range)
     if (ci < cend) atomicOr(a.bad, kBadUnplaced);
@@ -1744,10 +1669,8 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
 // waves of the chip are still streaming, takes the partial-sector writes off a pass of their own.
 constexpr uint32_t kWritePer = 2;  // records per lane with their loads in flight together (registers: occupancy)
 
-// store: the records' new bits are stored here as 2-byte stores; otherwise the stream already stored
-// them (in whole half-rows) and this pass only sums.
-__device__ __forceinline__ void write_through(const SelectArgs &a, const TensorDesc &td, uint32_t tau, uint32_t lt, uint32_t r0,
-                              uint32_t r1, bool store) {
+__device__ void write_through(const SelectArgs &a, const TensorDesc &td, uint32_t tau, uint32_t lt, uint32_t r0,
+                              uint32_t r1) {
     // this wave's record stores are complete, and its loads below see them
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -1778,7 +1701,7 @@ __device__ __forceinline__ void write_through(const SelectArgs &a, const TensorD
                 const uint32_t off = (uint32_t)(rc[u] >> 32) & 0xFFFFu, old = (uint32_t)(rc[u] >> 48);
                 const int32_t delta = (int32_t)(zz >> 1) ^ -(int32_t)(zz & 1);
                 const uint32_t nu = (uint32_t)((int32_t)old + delta) & 0xFFFF;
-                if (store && off < extent) base[off] = (uint16_t)nu;
+                if (off < extent) base[off] = (uint16_t)nu;
                 d += (uint64_t)((int64_t)nu - (int64_t)old) * weight(first + off);
                 const uint32_t eo = (old >> 7) & 0xFF, en = (nu >> 7) & 0xFF;
                 if (eo != en && h) {  // the element moves between exponent counts of its slab
@@ -1879,9 +1802,7 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
             // list entry x belongs to the last exponent whose list starts at or before x: mark the starts
             // of the non-empty lists, then a running maximum over the entries, 1024 at a time (16 per
             // lane, in order)
-            // the marks sit in the list's upper half: a round's entries overwrite only its own marks
-            // (read first) and earlier rounds'
-            uint16_t *mark = reinterpret_cast<uint16_t *>(S.list) + CAP;
+            uint16_t *mark = S.list;  // each round reads its marks before its list entries overwrite them
             for (uint32_t x = ln; x < CAP; x += 64) mark[x] = 0;
             wave_fence();
 #pragma unroll
@@ -1917,37 +1838,19 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
                     idx[i] = inf.z + x0 + 16 * ln + i;
                     sub[i] = inf.w;
                 }
-                wave_fence();  // this round's marks are read before its entries overwrite them
+                wave_fence();
 #pragma unroll
-                for (int h = 0; h < 16; h += 8) {  // 8 entries' loads in flight at a time (registers)
-                    uint32_t lv[8], zv[8];
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const bool in = x0 + 16 * ln + h + i < total;
-                        lv[i] = in ? a.local[idx[h + i]] : 0u;
-                        zv[i] = in ? (uint32_t)a.dz[idx[h + i]] : 0u;
-                    }
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const uint32_t x = x0 + 16 * ln + h + i;
-                        if (x < total) S.list[x] = ((lv[i] - sub[h + i]) & 0xFFFFu) | (min(zv[i], 0xFFFFu) << 16);
-                    }
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t x = x0 + 16 * ln + i;
+                    if (x < total) S.list[x] = (uint16_t)(a.local[idx[i]] - sub[i]);
                 }
                 wave_fence();
             }
         }
         wave_fence();
         const uint4 inf = S.info[ln];  // lane ln: window exponent ln
-        uint32_t first = (uint32_t)kFar, first_z = 0;  // its first target's slab rank and residual
-        if (inf.x < inf.y) {
-            if (in_lds) {
-                const uint32_t e = S.list[inf.x];
-                first = e & 0xFFFFu;
-                first_z = e >> 16;
-            } else {
-                first = a.local[inf.z + inf.x] - inf.w;
-            }
-        }
+        uint32_t first = (uint32_t)kFar;
+        if (inf.x < inf.y) first = in_lds ? S.list[inf.x] : a.local[inf.z + inf.x] - inf.w;
         wave_fence();
         for (uint32_t i = ln; i < (kWin + kSpare) * kSelCopies; i += 64) S.cnt[i] = 0;
         wave_fence();
@@ -1956,24 +1859,16 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
         // a slab's first window sums its weights for a cold tensor's checksum
         const bool cold = ANYCOLD && kfirst == 256 && td.cold;
         uint64_t fsum = 0;
-        // a slab streamed once (its first window is its only one) is written now; with the targets in
-        // LDS, in whole half-rows as they stream by
-        const bool write = kfirst == 256 && !a.multi[tau];
         uint32_t jend;
         if (in_lds)
-            jend = cold ? select_slab<CAP, true, ANYCOLD>(a, td, sl, kbase, S, first, first_z, c_first, c_end, inf.z,
-                                                          inf.w, j, write, fsum)
-                        : select_slab<CAP, true, false>(a, td, sl, kbase, S, first, first_z, c_first, c_end, inf.z,
-                                                        inf.w, j, write, fsum);
+            jend = cold ? select_slab<CAP, true, ANYCOLD>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j, fsum)
+                        : select_slab<CAP, true, false>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j, fsum);
         else
-            jend = cold ? select_slab<CAP, false, ANYCOLD>(a, td, sl, kbase, S, first, 0u, c_first, c_end, inf.z,
-                                                           inf.w, j, false, fsum)
-                        : select_slab<CAP, false, false>(a, td, sl, kbase, S, first, 0u, c_first, c_end, inf.z,
-                                                         inf.w, j, false, fsum);
+            jend = cold ? select_slab<CAP, false, ANYCOLD>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j, fsum)
+                        : select_slab<CAP, false, false>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j, fsum);
         if (kfirst == 256 && ln == 0) a.full[tau] = fsum + (cold && !td.hist_in ? a.full[tau] : 0);
-        // its checksum delta, exponent moves and undo count (and, when the targets were read from HBM,
-        // its writes)
-        if (write) write_through(a, td, tau, local_tile, j, jend, !in_lds);
+        // a slab streamed once (its first window is its only one) is written now
+        if (kfirst == 256 && !a.multi[tau]) write_through(a, td, tau, local_tile, j, jend);
     }
 }
 
