@@ -52,7 +52,13 @@ def main():
                     help="workload:rho pairs also measured (in detail.configs); '' for none")
     ap.add_argument("--cpu-baseline-layers", type=int, default=2,
                     help="decoder layers in the CPU baseline sample (0 disables it)")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="host threads of the CPU baseline (0: up to 16)")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="host threads of the CPU baseline (0: the physical cores this process may use, at most 16)")
+    ap.add_argument("--cpu-baseline-full", action="store_true",
+                    help="also run the CPU baseline on the 1.5B workload in full (7 chained steps) and one cold and "
+                         "one warm step of the 7B workload in full (minutes of host time)")
+    ap.add_argument("--cpu-cap-s", type=float, default=600.0,
+                    help="wall-clock cap of each full 7B CPU step (a step past it is reported as capped)")
     ap.add_argument("--host-bytes", action=argparse.BooleanOptionalAction, default=True,
                     help="also time the bytes API (PCIe-inclusive; reported in detail, never in value)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -117,7 +123,7 @@ def main():
     detail["kernels_ms_per_step"] = {n: round(ms, 4) for n, ms in sorted(res["kernels"].items())}
     detail["cold_breakdown_ms"] = res["cold_breakdown"]
     detail["cold2_breakdown_ms"] = res["cold2_breakdown"]
-    for k in ("host_bytes_encode_ms", "host_bytes_apply_ms"):
+    for k in ("host_bytes_encode_ms", "host_bytes_apply_ms", "reference_api_ms"):
         if k in res:
             detail[k] = res[k]
 
@@ -270,6 +276,32 @@ class Run:
             self.exact()
             out["host_bytes_encode_ms"] = round(min(x[0] for x in hb) * 1e3, 3)
             out["host_bytes_apply_ms"] = round(min(x[1] for x in hb) * 1e3, 3)
+            # the reference's own step shape: bytes out of encode_update and into apply_update, the
+            # checksum caches only (the receiver's exponent counts are not kept across updates)
+            from crukx_sync import codec
+            codec._COUNT_CACHE = False
+            ref = []
+            try:
+                for _ in range(3):
+                    old, new = self.states[self.i % 2], self.states[(self.i + 1) % 2]
+                    torch.cuda.synchronize()
+                    ta = time.perf_counter()
+                    data = crukx_sync.encode_update(old, new, self.send_chk)
+                    tb = time.perf_counter()
+                    crukx_sync.apply_update(self.recv, data, self.recv_chk)
+                    torch.cuda.synchronize()
+                    ref.append((tb - ta, time.perf_counter() - tb))
+                    self.i += 1
+            finally:
+                codec._COUNT_CACHE = True
+            self.exact()
+            e, a = sorted(x[0] for x in ref)[1], sorted(x[1] for x in ref)[1]
+            out["reference_api_ms"] = {"encode": round(e * 1e3, 3), "apply": round(a * 1e3, 3),
+                                       "step": round((e + a) * 1e3, 3),
+                                       "shape": "encode_update -> bytes -> apply_update(bytes), checksum caches on "
+                                                "both sides, no receiver exponent-count cache (median of 3)"}
+            log(f"[bench] reference API shape (bytes, checksum caches only): encode {e * 1e3:.2f} ms, "
+                f"apply {a * 1e3:.2f} ms")
         return out
 
 
@@ -328,6 +360,33 @@ def cpu_model():
     return "unknown CPU"
 
 
+def cpu_info() -> dict:
+    """The host's CPU as lscpu reports it, and the CPUs this process may run on."""
+    import subprocess
+    info = {"model": cpu_model()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = {k.strip(): v.strip() for k, v in (l.split(":", 1) for l in out.splitlines() if ":" in l)}
+        sockets, cores = int(kv.get("Socket(s)", 0)), int(kv.get("Core(s) per socket", 0))
+        info.update({"model": kv.get("Model name", info["model"]), "sockets": sockets, "cores_per_socket": cores,
+                     "threads_per_core": int(kv.get("Thread(s) per core", 0)), "logical_cpus": int(kv.get("CPU(s)", 0)),
+                     "physical_cores": sockets * cores})
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    info["cpus_available"] = len(os.sched_getaffinity(0))
+    return info
+
+
+def cpu_threads(args) -> int:
+    """Threads of the CPU baseline: the physical cores, within the CPUs this process may use and the
+    16 host CPUs that go with one GPU here (--cpu-threads overrides)."""
+    if args.cpu_threads:
+        return args.cpu_threads
+    info = cpu_info()
+    cores = info.get("physical_cores") or info["cpus_available"]
+    return max(1, min(cores, info["cpus_available"], 16))
+
+
 def measured_traffic(workload, rho, kernel):
     """HBM bytes per launch of `kernel` (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, calibrated against a 2 GiB
     copy) as recorded by rocprofv3 for this workload in profiles/, or None when not recorded."""
@@ -352,7 +411,7 @@ def cpu_baseline(args, shapes, A, B, N):
     import oracle
     import torch_cpu
 
-    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    threads = cpu_threads(args)
     torch.set_num_threads(threads)
     layers = args.cpu_baseline_layers
     names = [n for n, _, _ in shapes if any(n.startswith(f"model.layers.{i}.") for i in range(layers))]
@@ -383,17 +442,86 @@ def cpu_baseline(args, shapes, A, B, N):
         f"apply {t2 - t1:.2f}s -> {ms / 1e3:.1f}s per full update; C oracle (1 thread) encode {t4 - t3:.2f}s "
         f"apply {t5 - t4:.2f}s; {len(data):,} bytes identical on GPU, restatement and oracle")
     small4 = small4_chain(threads)
-    return {"value": round(ms, 1), "unit": "ms", "cores": threads, "kind": "port",
+    full = cpu_baseline_full(args, threads, torch) if args.cpu_baseline_full else None
+    value, sample = ms, (f"decoder layers 0..{layers - 1} of the same synthetic update ({n_sample} of {N} weights, "
+                         f"warm checksum caches), one encode + one apply on {threads} threads of {cpu_model()}, "
+                         f"time scaled by {scale:.2f} to the whole update")
+    if full and not full["qwen2.5-7b"]["warm"].get("capped"):  # the whole update measured: no scaling
+        w = full["qwen2.5-7b"]["warm"]
+        value = (w["encode_s"] + w["apply_s"]) * 1e3
+        sample = f"the whole update (one warm step, checksum caches on both sides) on {threads} threads"
+    out = {"value": round(value, 1), "unit": "ms", "cores": threads, "kind": "port",
             "impl": "torch-CPU restatement of the reference's CPU path (oracle/torch_cpu.py): slab-wise stable "
                     "argsort ranking, 256-step vectorised block decode, index_put_ scatter",
-            "sample": f"decoder layers 0..{layers - 1} of the same synthetic update ({n_sample} of {N} weights, "
-                      f"warm checksum caches), one encode + one apply on {threads} threads of {cpu_model()}, "
-                      f"time scaled by {scale:.2f} to the whole update",
-            "sample_encode_s": round(t1 - t0, 3), "sample_apply_s": round(t2 - t1, 3),
-            "sample_bytes_identical": True,
+            "sample": sample, "host": cpu_info(),
+            "layers_sample": {"weights": n_sample, "encode_s": round(t1 - t0, 3), "apply_s": round(t2 - t1, 3),
+                              "scaled_ms": round(ms, 1), "bytes_identical": True},
             "c_oracle_1_thread": {"sample_encode_s": round(t4 - t3, 3), "sample_apply_s": round(t5 - t4, 3),
                                   "value_ms": round((t5 - t3) * scale * 1e3, 1)},
             "small4_chain": small4}
+    if full:
+        out["full"] = full
+    return out
+
+
+def cpu_baseline_full(args, threads, torch):
+    """The CPU restatement on whole workloads (--cpu-baseline-full): the 1.5B state dict over seven
+    chained steps (the first without caches, the rest with both checksum caches), and the 7B state dict
+    over one cold and one warm step, each phase under a wall-clock cap; encode and apply timed apart.
+    Every step's bytes are compared with the GPU's."""
+    import crukx_sync
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import torch_cpu
+    from crukx_sync import workloads
+
+    def chain(workload, steps, cap):
+        shapes = workloads.shapes_for(workload)
+        n = workloads.numel(shapes)
+        t0 = time.perf_counter()
+        prev_g = workloads.make_weights(shapes, seed=0, device="cuda")
+        prev = {k: v.cpu() for k, v in prev_g.items()}
+        recv = {k: v.clone() for k, v in prev.items()}
+        log(f"[cpu] {workload}: {n:,} weights on the host in {time.perf_counter() - t0:.1f}s")
+        send_c, recv_c, send_g = {}, {}, {}
+        rows = []
+        for k in range(1, steps + 1):
+            cur_g = workloads.make_step(prev_g, k, rho=0.01, p_one=args.p_one, seed=0)
+            cur = {kk: v.cpu() for kk, v in cur_g.items()}
+            gpu = crukx_sync.encode_update(prev_g, cur_g, send_g)
+            ta = time.perf_counter()
+            data = torch_cpu.encode_update(prev, cur, send_c)
+            tb = time.perf_counter()
+            row = {"step": k, "caches": k > 1, "encode_s": round(tb - ta, 3), "bytes_identical": data == gpu}
+            log(f"[cpu] {workload} step {k}: encode {tb - ta:.2f}s, {len(data):,} bytes")
+            assert data == gpu, f"{workload} step {k}: the restatement's bytes differ from the GPU's"
+            if tb - ta > cap:
+                row["capped"] = True
+                rows.append(row)
+                break
+            torch_cpu.apply_update(recv, data, recv_c)
+            tc = time.perf_counter()
+            row["apply_s"] = round(tc - tb, 3)
+            row["capped"] = tc - tb > cap
+            rows.append(row)
+            log(f"[cpu] {workload} step {k} ({'warm' if k > 1 else 'cold'}): apply {tc - tb:.2f}s on {threads} threads")
+            prev, prev_g = cur, cur_g
+            if row["capped"]:
+                break
+        if not any(r.get("capped") for r in rows):
+            for kk in recv:
+                assert torch.equal(recv[kk].view(torch.int16), prev[kk].view(torch.int16)), kk
+        del prev, recv
+        torch.cuda.empty_cache()
+        return n, rows
+
+    out = {"threads": threads}
+    n, rows = chain("qwen2.5-1.5b", 7, float("inf"))
+    warm = [r for r in rows if r["caches"]]
+    out["qwen2.5-1.5b"] = {"weights": n, "steps": rows,
+                           "warm_mean_ms": round(sum(r["encode_s"] + r["apply_s"] for r in warm) / len(warm) * 1e3, 1)}
+    n, rows = chain("qwen2.5-7b", 2, args.cpu_cap_s)
+    out["qwen2.5-7b"] = {"weights": n, "cold": rows[0], "warm": rows[1] if len(rows) > 1 else {"capped": True}}
+    return out
 
 
 def small4_chain(threads):

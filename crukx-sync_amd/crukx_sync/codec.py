@@ -346,6 +346,11 @@ def _encode_call(names, A, B, numels, pa, pb, has, vals, dev):
 
 # ---------------------------------------------------------------- apply
 
+# Whether apply keeps the receiver's exponent counts across updates (below).  The reference has no such
+# cache (its apply re-sorts the receiver's weights every time); turning it off gives the reference's
+# semantics exactly: only the checksum cache carries over between updates.
+_COUNT_CACHE = True
+
 # Receiver-side exponent counts per slab, kept on the device across updates of the same tensors:
 # id(tensor) -> (weakref, _version after our last write, device buffer, slab size, device, buffer
 # address).  They are used only with the same slab size and a checksum-cache hit for the tensor (the
@@ -481,7 +486,7 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     err = _native.errbuf()
     changed = ctypes.c_uint64()
     # exponent counts carried across updates: only for tensors updated in place with a trusted cache
-    keep = checksums is not None and staged is targets
+    keep = checksums is not None and staged is targets and _COUNT_CACHE
     slab = int(_SLAB)
     hist_in, hist_out, bufs = [], [], []
     if keep:

@@ -16,8 +16,9 @@ torch operations, as the wire format (docs/FORMAT.md) and the reference's call s
   64-bit window continue window by window, codec.py:539-575), finds each change's position by the
   same slab sorts of the receiver's weights (codec.py:654-694), verifies the checksums (full ones
   through 2^24-element chunks, codec.py:61-68) and writes with index_put_ (codec.py:713-714).
-One difference in launch structure only: tensors of at most 2^22 elements are ranked one by one
-here, where the reference batches them into shared sorts (codec.py:150-194).
+Tensors of at most 2^22 elements are ranked, in encode and in apply, by shared stable sorts on
+(tensor, exponent) keys over groups of at most 127 tensors and 2^24 elements, as the reference batches
+them (codec.py:150-194, 659-678).
 """
 
 from __future__ import annotations
@@ -29,6 +30,8 @@ import numpy as np
 import torch
 
 SLAB = 1 << 24       # elements per stable sort
+SMALL_TENSOR = 1 << 22  # tensors up to this size share sorts with others
+MAX_SEGS = 127       # tensors per shared sort: (tensor, exponent) keys fit int16
 CHUNK = 1 << 24      # elements per checksum chunk
 BLOCK = 256
 MAX_LEN = 17
@@ -162,6 +165,51 @@ def _ranks_of_changes(e: torch.Tensor, changed: torch.Tensor):
     return pos[o], ex[o], rank[o], before
 
 
+def _small_groups(sizes: list[int]) -> list[list[int]]:
+    """Indices of the tensors of at most SMALL_TENSOR (and SLAB) elements, in order, grouped so that
+    each group holds at most SLAB elements and MAX_SEGS tensors (codec.py:154-168)."""
+    groups, cur, total = [], [], 0
+    for i, n in enumerate(sizes):
+        if n > min(SMALL_TENSOR, SLAB):
+            continue
+        if cur and (total + n > SLAB or len(cur) == MAX_SEGS):
+            groups.append(cur)
+            cur, total = [], 0
+        cur.append(i)
+        total += n
+    if cur:
+        groups.append(cur)
+    return groups
+
+
+def _shared_sort(es: list[torch.Tensor]):
+    """One stable sort of several tensors' exponents on (tensor, exponent) keys: the sort order (indices
+    into the concatenation), each tensor's offset there, and where each key starts in the order
+    ([len(es) * 256 + 1])."""
+    sizes = torch.tensor([e.numel() for e in es], dtype=torch.int64)
+    seg = torch.repeat_interleave(torch.arange(len(es), dtype=torch.int16), sizes)
+    key = (seg << 8) | torch.cat(es).to(torch.int16)
+    order = torch.sort(key, stable=True).indices
+    cnt = torch.bincount(key.to(torch.int64), minlength=len(es) * 256)
+    starts = torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(cnt, 0)])
+    offs = torch.cumsum(sizes, 0) - sizes
+    return order, offs, starts
+
+
+def _ranks_of_changes_many(es: list[torch.Tensor], changed: list[torch.Tensor]):
+    """_ranks_of_changes for several small tensors with one shared sort (codec.py:171-194)."""
+    order, offs, starts = _shared_sort(es)
+    j = torch.nonzero(torch.cat(changed)[order]).view(-1)   # sorted slots holding a change
+    p = order[j]
+    t = torch.searchsorted(offs, p, right=True) - 1           # tensor of each change
+    k = ((t << 8) | torch.cat(es).to(torch.int64)[p])
+    rank = j - starts[k]
+    pos = p - offs[t]
+    # rows are tensor-major, then (exponent, position) within a tensor: (exponent, rank) order
+    per = torch.bincount(t, minlength=len(es)).tolist()
+    return [(p_, k_ & 255, r_) for p_, k_, r_ in zip(pos.split(per), k.split(per), rank.split(per))]
+
+
 # ---------------------------------------------------------------- encode
 
 def _rice(gaps: torch.Tensor, seg: torch.Tensor, counts: torch.Tensor) -> list[int]:
@@ -203,16 +251,22 @@ def encode_update(old: dict, new: dict, checksums: dict | None = None) -> bytes:
     """encode_update on CPU tensors; `checksums` (name -> int) is the sender cache, updated once the
     bytes exist."""
     names = list(old)
-    tensors = []  # (name, numel, pos, exp, rank, old_u, new_u)
+    todo = []  # (name, old bits, new bits, changed) of the tensors with a change
     for name in names:
         a = old[name].reshape(-1).view(torch.int16)
         b = new[name].reshape(-1).view(torch.int16)
         if a.numel() != b.numel():
             raise ValueError(f"{name}: old and new differ in shape")
         changed = a != b
-        if not bool(changed.any()):
-            continue
-        pos, ex, rank, _ = _ranks_of_changes(_exp(a), changed)
+        if bool(changed.any()):
+            todo.append((name, a, b, changed))
+    ranked = {}
+    for grp in _small_groups([a.numel() for _, a, _, _ in todo]):
+        res = _ranks_of_changes_many([_exp(todo[i][1]) for i in grp], [todo[i][3] for i in grp])
+        ranked.update(zip(grp, res))
+    tensors = []  # (name, numel, pos, exp, rank, old_u, new_u)
+    for i, (name, a, b, changed) in enumerate(todo):
+        pos, ex, rank = ranked[i] if i in ranked else _ranks_of_changes(_exp(a), changed)[:3]
         tensors.append((name, a.numel(), pos, ex, rank, a[pos].to(torch.int64) & 0xFFFF,
                         b[pos].to(torch.int64) & 0xFFFF))
     new_chk = {}
@@ -502,7 +556,7 @@ def apply_update(weights: dict, update: bytes, checksums: dict | None = None) ->
     tables, tensors, bb, payload = _parse(update)
     groups = [g for t in tensors for g in t[3]]
     gaps, zz = _decode(tables, groups, bb, payload)
-    plans = []
+    work = []  # per tensor: (weights as int16, name, checksum, group exponents and counts, locals, exponents, zz)
     at = 0
     for name, numel, chk, tg in tensors:
         a = weights[name].reshape(-1).view(torch.int16)
@@ -517,31 +571,47 @@ def apply_update(weights: dict, update: bytes, checksums: dict | None = None) ->
         cs = torch.cumsum(step, 0)
         gstart = torch.cumsum(gcnt, 0) - gcnt
         local = cs - (cs[gstart] - step[gstart])[seg] - 1   # group-local index of each change
-        ex = gexp[seg]
-        e_all = _exp(a)
-        # the receiver's stable exponent order, slab by slab: which slab holds each change, then
-        # its place in that slab's sorted order
-        nsl = (numel + SLAB - 1) // SLAB
-        cnts = torch.stack([torch.bincount(e_all[lo:lo + SLAB], minlength=256)
-                            for lo in range(0, numel, SLAB)])      # [slabs, 256]
-        incl = torch.cumsum(cnts, 0)
-        size = incl[-1]
-        if bool((gcnt > size[gexp]).any()) or bool((local >= size[ex]).any()):
-            raise Corrupt("a change lies outside its exponent group")
-        flat = (incl.t() + torch.arange(256).view(-1, 1) * (numel + 1)).reshape(-1)  # ascending
-        sl = torch.searchsorted(flat, ex * (numel + 1) + local, right=True) - ex * nsl
-        pos = torch.empty_like(local)
-        for s in range(nsl):
-            m = torch.nonzero(sl == s).view(-1)
-            if m.numel() == 0:
-                continue
-            lo = s * SLAB
-            key = e_all[lo:lo + SLAB]
-            order = torch.sort(key, stable=True).indices
-            start = torch.cumsum(cnts[s], 0) - cnts[s]
-            before = incl[s] - cnts[s]
-            k = ex[m]
-            pos[m] = lo + order[start[k] + local[m] - before[k]]
+        work.append((a, name, chk, gexp, gcnt, local, gexp[seg], z_))
+        at += n
+    positions = {}
+    # small tensors: one shared sort per group on (tensor, exponent) keys (codec.py:659-678)
+    for grp in _small_groups([w[0].numel() for w in work]):
+        order, offs, starts = _shared_sort([_exp(work[i][0]) for i in grp])
+        for si, i in enumerate(grp):
+            a, name, chk, gexp, gcnt, local, ex, z_ = work[i]
+            size = starts[si * 256 + 1:si * 256 + 257] - starts[si * 256:si * 256 + 256]
+            if bool((gcnt > size[gexp]).any()) or bool((local >= size[ex]).any()):
+                raise Corrupt("a change lies outside its exponent group")
+            positions[i] = order[starts[si * 256 + ex] + local] - offs[si]
+    plans = []
+    for i, (a, name, chk, gexp, gcnt, local, ex, z_) in enumerate(work):
+        numel = a.numel()
+        pos = positions.get(i)
+        if pos is None:
+            # the receiver's stable exponent order, slab by slab: which slab holds each change, then
+            # its place in that slab's sorted order
+            e_all = _exp(a)
+            nsl = (numel + SLAB - 1) // SLAB
+            cnts = torch.stack([torch.bincount(e_all[lo:lo + SLAB], minlength=256)
+                                for lo in range(0, numel, SLAB)])      # [slabs, 256]
+            incl = torch.cumsum(cnts, 0)
+            size = incl[-1]
+            if bool((gcnt > size[gexp]).any()) or bool((local >= size[ex]).any()):
+                raise Corrupt("a change lies outside its exponent group")
+            flat = (incl.t() + torch.arange(256).view(-1, 1) * (numel + 1)).reshape(-1)  # ascending
+            sl = torch.searchsorted(flat, ex * (numel + 1) + local, right=True) - ex * nsl
+            pos = torch.empty_like(local)
+            for s in range(nsl):
+                m = torch.nonzero(sl == s).view(-1)
+                if m.numel() == 0:
+                    continue
+                lo = s * SLAB
+                key = e_all[lo:lo + SLAB]
+                order = torch.sort(key, stable=True).indices
+                start = torch.cumsum(cnts[s], 0) - cnts[s]
+                before = incl[s] - cnts[s]
+                k = ex[m]
+                pos[m] = lo + order[start[k] + local[m] - before[k]]
         ou = a[pos].to(torch.int64) & 0xFFFF
         d = torch.where(z_ & 1 == 1, -((z_ + 1) >> 1), z_ >> 1)
         nu = (ou + d) & 0xFFFF
@@ -551,7 +621,6 @@ def apply_update(weights: dict, update: bytes, checksums: dict | None = None) ->
         if (old_chk + _delta(pos, ou, nu)) & MASK64 != chk:
             raise Corrupt(f"update does not verify (checksum mismatch: [{name!r}])")
         plans.append((a, pos, nu, name, chk))
-        at += n
     changed = 0
     for a, pos, nu, name, chk in plans:  # every tensor verified: write
         a.index_put_((pos,), nu.to(torch.int16))

@@ -89,3 +89,34 @@ def test_checksum_and_rejections():
     with pytest.raises(ValueError):  # a wrong receiver cache
         torch_cpu.apply_update(w, bytes(upd), {"w": 12345})
     assert torch.equal(w["w"].view(torch.int16), a.view(torch.int16))
+
+
+def test_shared_sorts_of_many_small_tensors():
+    """Hundreds of small tensors ranked in shared sorts (groups cut by tensor count and by size), with
+    a large tensor between them: the same bytes as the oracle, which ranks tensor by tensor, and an
+    exact apply; the grouping never changes the bytes."""
+    g = torch.Generator().manual_seed(7)
+    old, new = {}, {}
+    for i in range(300):
+        n = int(torch.randint(1, 3000, (1,), generator=g)) if i != 150 else 70_000
+        a = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+        b = a.clone()
+        k = torch.randperm(n, generator=g)[:max(1, n // 50)]
+        b.view(torch.int16)[k] += torch.randint(-3, 4, (k.numel(),), generator=g, dtype=torch.int16)
+        old[f"t{i}"], new[f"t{i}"] = a, b
+    want = oracle.encode_update(old, new)
+    assert torch_cpu.encode_update(old, new) == want
+    w = {k: v.clone() for k, v in old.items()}
+    torch_cpu.apply_update(w, want)
+    assert _equal(w, new)
+    grouped = torch_cpu._small_groups([t.numel() for t in old.values()])
+    assert len(grouped) >= 3 and all(len(x) <= torch_cpu.MAX_SEGS for x in grouped)
+    saved = torch_cpu.MAX_SEGS, torch_cpu.SLAB
+    try:
+        torch_cpu.MAX_SEGS, torch_cpu.SLAB = 5, 20_000   # smaller groups, and the large tensor slab-wise
+        assert torch_cpu.encode_update(old, new) == want
+        w = {k: v.clone() for k, v in old.items()}
+        torch_cpu.apply_update(w, want)
+        assert _equal(w, new)
+    finally:
+        torch_cpu.MAX_SEGS, torch_cpu.SLAB = saved
