@@ -15,9 +15,11 @@ Prints one JSON line.
   (the median of three such steps, each after a warm step).
 - `detail.configs`: the same measurement at other sizes and densities.
 - `cpu_baseline`: a torch-CPU restatement of the reference's CPU path (oracle/torch_cpu.py, bytes
-  checked against the reference's golden vectors by the tests) on the host cores, over a sample of
-  the same update scaled to the whole; the sample's bytes from the GPU, the restatement and the C
-  oracle must be identical.
+  checked against the reference's golden vectors by the tests) on the host's physical cores: `value` is
+  one warm step of the whole update (encode and apply timed apart, bytes identical to the GPU's);
+  beside it the 1.5B workload's seven chained steps, the small4 chain, and a layer sample also run by
+  the single-threaded C oracle (the sample's bytes from the GPU, the restatement and the oracle must be
+  identical).  `--cpu-baseline full` adds the 7B cold step; `sample` keeps only the sample and small4.
 """
 
 from __future__ import annotations
@@ -54,11 +56,13 @@ def main():
                     help="decoder layers in the CPU baseline sample (0 disables it)")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="host threads of the CPU baseline (0: the physical cores this process may use, at most 16)")
-    ap.add_argument("--cpu-baseline-full", action="store_true",
-                    help="also run the CPU baseline on the 1.5B workload in full (7 chained steps) and one cold and "
-                         "one warm step of the 7B workload in full (minutes of host time)")
-    ap.add_argument("--cpu-cap-s", type=float, default=600.0,
-                    help="wall-clock cap of each full 7B CPU step (a step past it is reported as capped)")
+    ap.add_argument("--cpu-baseline", choices=("sample", "standard", "full"), default="standard",
+                    help="sample: the layer sample and the small4 chain only; standard: also one warm step of the "
+                         "whole 7B update and the 1.5B workload's seven chained steps (about 2.5 minutes of host "
+                         "time); full: also the 7B cold step")
+    ap.add_argument("--cpu-cap-s", type=float, default=300.0,
+                    help="wall-clock cap of each phase of a whole-update CPU step (past it the step is reported as "
+                         "capped and the next phase is skipped)")
     ap.add_argument("--host-bytes", action=argparse.BooleanOptionalAction, default=True,
                     help="also time the bytes API (PCIe-inclusive; reported in detail, never in value)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -442,85 +446,127 @@ def cpu_baseline(args, shapes, A, B, N):
         f"apply {t2 - t1:.2f}s -> {ms / 1e3:.1f}s per full update; C oracle (1 thread) encode {t4 - t3:.2f}s "
         f"apply {t5 - t4:.2f}s; {len(data):,} bytes identical on GPU, restatement and oracle")
     small4 = small4_chain(threads)
-    full = cpu_baseline_full(args, threads, torch) if args.cpu_baseline_full else None
     value, sample = ms, (f"decoder layers 0..{layers - 1} of the same synthetic update ({n_sample} of {N} weights, "
                          f"warm checksum caches), one encode + one apply on {threads} threads of {cpu_model()}, "
                          f"time scaled by {scale:.2f} to the whole update")
-    if full and not full["qwen2.5-7b"]["warm"].get("capped"):  # the whole update measured: no scaling
-        w = full["qwen2.5-7b"]["warm"]
-        value = (w["encode_s"] + w["apply_s"]) * 1e3
-        sample = f"the whole update (one warm step, checksum caches on both sides) on {threads} threads"
-    out = {"value": round(value, 1), "unit": "ms", "cores": threads, "kind": "port",
-            "impl": "torch-CPU restatement of the reference's CPU path (oracle/torch_cpu.py): slab-wise stable "
-                    "argsort ranking, 256-step vectorised block decode, index_put_ scatter",
-            "sample": sample, "host": cpu_info(),
-            "layers_sample": {"weights": n_sample, "encode_s": round(t1 - t0, 3), "apply_s": round(t2 - t1, 3),
-                              "scaled_ms": round(ms, 1), "bytes_identical": True},
-            "c_oracle_1_thread": {"sample_encode_s": round(t4 - t3, 3), "sample_apply_s": round(t5 - t4, 3),
-                                  "value_ms": round((t5 - t3) * scale * 1e3, 1)},
-            "small4_chain": small4}
-    if full:
-        out["full"] = full
+    out = {"unit": "ms", "cores": threads, "kind": "port",
+           "impl": "torch-CPU restatement of the reference's CPU path (oracle/torch_cpu.py): slab-wise stable "
+                   "argsort ranking (small tensors in shared sorts), 256-step vectorised block decode, index_put_ "
+                   "scatter",
+           "host": cpu_info(), "cap_s": args.cpu_cap_s,
+           "layers_sample": {"weights": n_sample, "encode_s": round(t1 - t0, 3), "apply_s": round(t2 - t1, 3),
+                             "scaled_ms": round(ms, 1), "bytes_identical": True},
+           "c_oracle_1_thread": {"sample_encode_s": round(t4 - t3, 3), "sample_apply_s": round(t5 - t4, 3),
+                                 "value_ms": round((t5 - t3) * scale * 1e3, 1)},
+           "small4_chain": small4}
+    if args.cpu_baseline != "sample":
+        warm = whole_update_step(args, threads, A, B, names=[n for n, _, _ in shapes])
+        out["whole_update_warm"] = warm
+        if not warm["capped"]:  # the whole update measured: no scaling
+            value = (warm["encode_s"] + warm["apply_s"]) * 1e3
+            sample = (f"the whole update: one warm step (checksum caches on both sides), encode and apply, on "
+                      f"{threads} threads of {cpu_model()}; bytes identical to the GPU's")
+        out["qwen2.5-1.5b_chain"] = cpu_chain(args, threads, "qwen2.5-1.5b", 7)
+        if args.cpu_baseline == "full":
+            out["qwen2.5-7b_cold"] = cpu_chain(args, threads, "qwen2.5-7b", 1)
+    out["value"] = round(value, 1)
+    out["sample"] = sample
     return out
 
 
-def cpu_baseline_full(args, threads, torch):
-    """The CPU restatement on whole workloads (--cpu-baseline-full): the 1.5B state dict over seven
-    chained steps (the first without caches, the rest with both checksum caches), and the 7B state dict
-    over one cold and one warm step, each phase under a wall-clock cap; encode and apply timed apart.
-    Every step's bytes are compared with the GPU's."""
+def whole_update_step(args, threads, A, B, names):
+    """One warm step of the restatement over the whole update the GPU steps run (every tensor, embed and
+    lm_head included): both checksum caches hold the old state's checksums (computed on the GPU), encode
+    and apply timed apart, each under the wall-clock cap; bytes compared with the GPU's, the receiver
+    compared with the new state."""
+    import torch
+
+    import crukx_sync
+    from crukx_sync import codec
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import torch_cpu
+
+    t0 = time.perf_counter()
+    old = {n: A[n].cpu() for n in names}
+    new = {n: B[n].cpu() for n in names}
+    cache = {n: codec.checksum(A[n]) for n in names}
+    gpu = crukx_sync.encode_update(A, B, dict(cache))
+    recv = {n: v.clone() for n, v in old.items()}
+    log(f"[cpu] whole update on the host in {time.perf_counter() - t0:.1f}s; warm step on {threads} threads")
+    ta = time.perf_counter()
+    data = torch_cpu.encode_update(old, new, dict(cache))
+    tb = time.perf_counter()
+    assert data == gpu, "whole update: the restatement's bytes differ from the GPU's"
+    row = {"weights": sum(v.numel() for v in old.values()), "tensors": len(names), "caches": True,
+           "encode_s": round(tb - ta, 3), "bytes_identical": True, "capped": tb - ta > args.cpu_cap_s}
+    log(f"[cpu] whole update, warm: encode {tb - ta:.2f}s, {len(data):,} bytes identical to the GPU's")
+    if not row["capped"]:
+        torch_cpu.apply_update(recv, data, dict(cache))
+        tc = time.perf_counter()
+        row["apply_s"] = round(tc - tb, 3)
+        row["capped"] = tc - tb > args.cpu_cap_s
+        for n in names:
+            assert torch.equal(recv[n].view(torch.int16), new[n].view(torch.int16)), n
+        log(f"[cpu] whole update, warm: apply {tc - tb:.2f}s; receiver equals the new state")
+    return row
+
+
+def cpu_chain(args, threads, workload, steps):
+    """The restatement over `steps` chained steps of a whole workload (the first without caches, the
+    rest with both checksum caches), encode and apply timed apart, each phase under the wall-clock cap
+    (a phase past it ends the chain, reported as capped).  Every step's bytes are compared with the
+    GPU's, and the receiver with the last state."""
+    import torch
+
     import crukx_sync
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import torch_cpu
     from crukx_sync import workloads
 
-    def chain(workload, steps, cap):
-        shapes = workloads.shapes_for(workload)
-        n = workloads.numel(shapes)
-        t0 = time.perf_counter()
-        prev_g = workloads.make_weights(shapes, seed=0, device="cuda")
-        prev = {k: v.cpu() for k, v in prev_g.items()}
-        recv = {k: v.clone() for k, v in prev.items()}
-        log(f"[cpu] {workload}: {n:,} weights on the host in {time.perf_counter() - t0:.1f}s")
-        send_c, recv_c, send_g = {}, {}, {}
-        rows = []
-        for k in range(1, steps + 1):
-            cur_g = workloads.make_step(prev_g, k, rho=0.01, p_one=args.p_one, seed=0)
-            cur = {kk: v.cpu() for kk, v in cur_g.items()}
-            gpu = crukx_sync.encode_update(prev_g, cur_g, send_g)
-            ta = time.perf_counter()
-            data = torch_cpu.encode_update(prev, cur, send_c)
-            tb = time.perf_counter()
-            row = {"step": k, "caches": k > 1, "encode_s": round(tb - ta, 3), "bytes_identical": data == gpu}
-            log(f"[cpu] {workload} step {k}: encode {tb - ta:.2f}s, {len(data):,} bytes")
-            assert data == gpu, f"{workload} step {k}: the restatement's bytes differ from the GPU's"
-            if tb - ta > cap:
-                row["capped"] = True
-                rows.append(row)
-                break
-            torch_cpu.apply_update(recv, data, recv_c)
-            tc = time.perf_counter()
-            row["apply_s"] = round(tc - tb, 3)
-            row["capped"] = tc - tb > cap
-            rows.append(row)
-            log(f"[cpu] {workload} step {k} ({'warm' if k > 1 else 'cold'}): apply {tc - tb:.2f}s on {threads} threads")
-            prev, prev_g = cur, cur_g
-            if row["capped"]:
-                break
-        if not any(r.get("capped") for r in rows):
-            for kk in recv:
-                assert torch.equal(recv[kk].view(torch.int16), prev[kk].view(torch.int16)), kk
-        del prev, recv
-        torch.cuda.empty_cache()
-        return n, rows
-
-    out = {"threads": threads}
-    n, rows = chain("qwen2.5-1.5b", 7, float("inf"))
-    warm = [r for r in rows if r["caches"]]
-    out["qwen2.5-1.5b"] = {"weights": n, "steps": rows,
-                           "warm_mean_ms": round(sum(r["encode_s"] + r["apply_s"] for r in warm) / len(warm) * 1e3, 1)}
-    n, rows = chain("qwen2.5-7b", 2, args.cpu_cap_s)
-    out["qwen2.5-7b"] = {"weights": n, "cold": rows[0], "warm": rows[1] if len(rows) > 1 else {"capped": True}}
+    cap = args.cpu_cap_s
+    shapes = workloads.shapes_for(workload)
+    n = workloads.numel(shapes)
+    t0 = time.perf_counter()
+    prev_g = workloads.make_weights(shapes, seed=0, device="cuda")
+    prev = {k: v.cpu() for k, v in prev_g.items()}
+    recv = {k: v.clone() for k, v in prev.items()}
+    log(f"[cpu] {workload}: {n:,} weights on the host in {time.perf_counter() - t0:.1f}s")
+    send_c, recv_c, send_g = {}, {}, {}
+    rows = []
+    for k in range(1, steps + 1):
+        cur_g = workloads.make_step(prev_g, k, rho=0.01, p_one=args.p_one, seed=0)
+        cur = {kk: v.cpu() for kk, v in cur_g.items()}
+        gpu = crukx_sync.encode_update(prev_g, cur_g, send_g)
+        ta = time.perf_counter()
+        data = torch_cpu.encode_update(prev, cur, send_c)
+        tb = time.perf_counter()
+        assert data == gpu, f"{workload} step {k}: the restatement's bytes differ from the GPU's"
+        row = {"step": k, "caches": k > 1, "encode_s": round(tb - ta, 3), "bytes_identical": True,
+               "capped": tb - ta > cap}
+        log(f"[cpu] {workload} step {k}: encode {tb - ta:.2f}s, {len(data):,} bytes identical to the GPU's")
+        rows.append(row)
+        if row["capped"]:
+            break
+        torch_cpu.apply_update(recv, data, recv_c)
+        tc = time.perf_counter()
+        row["apply_s"] = round(tc - tb, 3)
+        row["capped"] = tc - tb > cap
+        log(f"[cpu] {workload} step {k} ({'warm' if k > 1 else 'cold'}): apply {tc - tb:.2f}s on {threads} threads")
+        prev, prev_g = cur, cur_g
+        if row["capped"]:
+            break
+    done = not any(r["capped"] for r in rows)
+    if done:
+        for kk in recv:
+            assert torch.equal(recv[kk].view(torch.int16), prev[kk].view(torch.int16)), kk
+    del prev, recv, prev_g
+    torch.cuda.empty_cache()
+    out = {"weights": n, "threads": threads, "steps": rows, "receiver_equal": done}
+    warm = [r for r in rows if r["caches"] and not r["capped"]]
+    if warm:
+        med = sorted(r["encode_s"] + r["apply_s"] for r in warm)[len(warm) // 2]
+        out["warm_median_ms"] = round(med * 1e3, 1)
+        out["warm_mean_ms"] = round(sum(r["encode_s"] + r["apply_s"] for r in warm) / len(warm) * 1e3, 1)
     return out
 
 
