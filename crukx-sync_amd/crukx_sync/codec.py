@@ -49,7 +49,6 @@ _DTYPES16 = (torch.bfloat16, torch.int16)
 # with ValueError before any device work (the reference has no such limit).
 _LIMIT = 1 << 32
 _TOO_LONG = "tensors of 2^32 or more elements are not supported"
-_TOO_MANY = "2^32 or more changes in one update are not supported"
 
 
 def _check16(name: str, t) -> torch.Tensor:
@@ -466,8 +465,6 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
             ok = isinstance(hit, tuple) and hit[1] == v
             has.append(1 if ok else 0)
             vals.append(hit[0] & _MASK64 if ok else 0)
-    if u.total_changes >= _LIMIT:
-        raise ValueError(_TOO_MANY)
     if len(devs) == 1 and next(iter(devs)) >= 0:  # all on one GPU
         src = dev = targets[0].device
     else:

@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -324,11 +325,38 @@ struct Arena {
     uint8_t *chunk = nullptr;
     uint64_t used = 0, size = 0;
     uint64_t total = 0;  // bytes handed out by get()
+    // Scoped buffers (the parts of a chunked update, one after another): within a scope every buffer is
+    // an allocation of its own, and at its end they become spares that the next scope's buffers reuse
+    // (the first spare large enough).  A scope ends only once the device is done with its buffers.
+    bool scoped = false;
+    std::vector<std::pair<void *, uint64_t>> live, spare;
 
     void *raw(uint64_t bytes) {
         void *p = fn(ctx, bytes);
         if (!p) throw std::bad_alloc();
         return p;
+    }
+    void begin_scope() { scoped = true; }
+    void end_scope() {
+        spare.insert(spare.end(), live.begin(), live.end());
+        live.clear();
+        scoped = false;
+    }
+    void *scoped_get(uint64_t bytes) {
+        if (g_arena_unpooled) {  // exact bounds for a memory checker: no reuse
+            total += bytes;
+            return raw(std::max<uint64_t>(bytes, 1));
+        }
+        bytes = (std::max<uint64_t>(bytes, 1) + 255) & ~uint64_t(255);
+        total += bytes;
+        for (size_t i = 0; i < spare.size(); ++i)
+            if (spare[i].second >= bytes) {
+                live.push_back(spare[i]);
+                spare.erase(spare.begin() + (ptrdiff_t)i);
+                return live.back().first;
+            }
+        live.emplace_back(raw(bytes), bytes);
+        return live.back().first;
     }
     // one block of `bytes` for the buffers that follow
     void reserve(uint64_t bytes) {
@@ -341,6 +369,7 @@ struct Arena {
     }
     template <typename T>
     T *get(uint64_t count) {
+        if (scoped) return static_cast<T *>(scoped_get(count * sizeof(T)));
         if (g_arena_unpooled) {
             total += count * sizeof(T);
             return static_cast<T *>(raw(std::max<uint64_t>(count * sizeof(T), 1)));
@@ -674,6 +703,348 @@ std::string py_repr(const std::string &s) {
 // rare symbols downloaded with the symbol counts, before their number is known
 constexpr uint64_t kRareFirst = 16384;
 
+// Elements of the tensors of a layout.
+uint64_t layout_elements(const Layout &L) {
+    uint64_t n = 0;
+    for (const TensorDesc &d : L.descs) n += d.numel;
+    return n;
+}
+
+// Elements per part of an update encoded or applied part by part (an update of 2^32 or more changes):
+// each part's changes stay below 2^31, so that every per-part index fits 32 bits; a tensor larger than
+// this is a part of its own (fewer than 2^32 changes).  CRX_PART_ELEMENTS (> 0) sets the size and splits
+// every update larger than it, for tests of the part-wise path at sizes an oracle can check.
+constexpr uint64_t kPartElements = 1ULL << 31;
+uint64_t part_elements_override() {
+    const char *v = std::getenv("CRX_PART_ELEMENTS");
+    return v ? std::strtoull(v, nullptr, 10) : 0;
+}
+
+// Consecutive tensors of the layout in parts of at most `limit` elements (a larger tensor alone).
+std::vector<std::pair<uint32_t, uint32_t>> split_parts(const Layout &L, uint64_t limit) {
+    std::vector<std::pair<uint32_t, uint32_t>> out;
+    uint32_t b = 0;
+    uint64_t acc = 0;
+    for (uint32_t i = 0; i < (uint32_t)L.descs.size(); ++i) {
+        if (i > b && acc + L.descs[i].numel > limit) {
+            out.emplace_back(b, i);
+            b = i;
+            acc = 0;
+        }
+        acc += L.descs[i].numel;
+    }
+    if (b < (uint32_t)L.descs.size()) out.emplace_back(b, (uint32_t)L.descs.size());
+    return out;
+}
+
+// The layout of tensors [d0, d1) of L.
+Layout sub_layout(const Layout &L, uint32_t d0, uint32_t d1, uint32_t slab) {
+    Layout P;
+    P.descs.assign(L.descs.begin() + d0, L.descs.begin() + d1);
+    P.call_index.assign(L.call_index.begin() + d0, L.call_index.begin() + d1);
+    finish_layout(P, slab);
+    return P;
+}
+
+// The changes of the tensors of L ranked (codec.py:124-147,278-341): per slab exponent counts of all
+// elements and of the changed ones, their scans, the groups (tensor, exponent) with their counts, and
+// each slab's change records.  Stops before the records' second pass when the update has `stop_at` or
+// more changes (C says how many; nothing else is then valid).
+struct Ranked {
+    TensorDesc *d_descs = nullptr;
+    ScanDev sd{};
+    EncRankArgs a{};
+    uint32_t *hall = nullptr, *hchg = nullptr, *gbase = nullptr;
+    GroupDev *d_groups = nullptr;
+    uint64_t *delta = nullptr, *full = nullptr;  // [tiles] checksum parts
+    uint64_t G = 0, C = 0;
+};
+
+Ranked rank_changes(const Layout &L, uint32_t slab, hipStream_t s, Arena &ar, HostClock *hc, uint64_t stop_at) {
+    const uint32_t T = (uint32_t)L.descs.size(), tiles = L.tiles;
+    Ranked R;
+    R.d_descs = ar.get<TensorDesc>(T);
+    h2d(R.d_descs, L.descs.data(), T, s);
+    R.hall = ar.get<uint32_t>((uint64_t)tiles * 256);
+    R.hchg = ar.get<uint32_t>((uint64_t)tiles * 256);
+    R.delta = ar.get<uint64_t>(tiles);
+    R.full = ar.get<uint64_t>(tiles);
+    R.sd = upload_scan(ar, L, R.d_descs, s);
+    uint32_t *tot_all = ar.get<uint32_t>((uint64_t)T * 256), *tot_chg = ar.get<uint32_t>((uint64_t)T * 256);
+    R.d_groups = ar.get<GroupDev>((uint64_t)T * 256);
+    R.gbase = ar.get<uint32_t>((uint64_t)T * 256);
+    unsigned long long *gcnt = ar.get<unsigned long long>(2);
+
+    // Each slab stores its change records in a region of its own, sized for 1/24 of its elements
+    // (+64).  If one overflows, the exact counts of that pass give exact regions for a second pass.
+    const uint64_t per_slab = slab / 24 + 64;
+    uint32_t *rec_count = ar.get<uint32_t>(tiles);
+    unsigned int *ovf = ar.get<unsigned int>(1);
+    zero(ovf, 1, s);
+    R.a = EncRankArgs{R.d_descs, R.sd.tile_tensor, T, slab, R.hall, R.hchg, ar.get<uint64_t>((uint64_t)tiles * per_slab),
+                      nullptr, per_slab, rec_count, ovf, R.delta, R.full};
+    launch_enc_rank(R.a, tiles, s);
+    if (hc) hc->mark("enc_setup");
+    // the scans and groups need only the counts, which are exact even when a slab's records overflowed
+    // their region; the overflow flag is read with the group totals, and on overflow the rank pass runs
+    // again into exact regions (rewriting the counts, so they are scanned again)
+    unsigned int hovf1 = 0;
+    unsigned long long gc[2];
+    for (int pass = 0;; ++pass) {
+        launch_scan_tables(R.d_descs, R.hall, R.sd.chunks, R.sd.n_chunks, R.sd.tcb, T, R.sd.csum, tot_all, s);
+        launch_scan_tables(R.d_descs, R.hchg, R.sd.chunks, R.sd.n_chunks, R.sd.tcb, T, R.sd.csum, tot_chg, s);
+        launch_enc_groups(tot_chg, T, R.d_groups, R.gbase, gcnt, s);
+        d2h(&hovf1, ovf, 1, s);
+        d2h(gc, gcnt, 2, s);
+        sync(s);
+        R.G = gc[0];
+        R.C = gc[1];
+        if (!hovf1 || R.C >= stop_at) break;
+        if (pass) throw DeviceError("change records overflowed exact regions");
+        unsigned long long *rec_base = ar.get<unsigned long long>(tiles + 1);
+        launch_scan_u32(rec_count, tiles, rec_base, ar.get<unsigned long long>(scan_parts(tiles)), s);
+        unsigned long long total = 0;
+        d2h(&total, rec_base + tiles, 1, s);
+        sync(s);
+        R.a.rec = ar.get<uint64_t>(total);
+        R.a.rec_base = rec_base;
+        zero(ovf, 1, s);
+        launch_enc_rank(R.a, tiles, s);
+    }
+    return R;
+}
+
+// Rice parameters of the groups, chosen from their three candidate costs (codec.py:354-360), and their
+// first blocks; returns the bits of their gap codes.
+uint64_t choose_rice(std::vector<GroupDev> &groups, const std::vector<unsigned long long> &hcost) {
+    uint64_t blk = 0, bits = 0;
+    for (uint64_t g = 0; g < groups.size(); ++g) {
+        GroupDev &gr = groups[g];
+        const int c[3] = {(int)(gr.r0 ? gr.r0 - 1 : 0), (int)gr.r0, (int)std::min<uint32_t>(gr.r0 + 1, kMaxRice)};
+        const uint64_t sh[3] = {hcost[g * 3], hcost[g * 3 + 1], hcost[g * 3 + 2]};
+        gr.rice = (uint32_t)rice_choose(gr.count, c, sh);
+        const int k = gr.rice == (uint32_t)c[0] ? 0 : gr.rice == (uint32_t)c[1] ? 1 : 2;
+        bits += sh[k] + (uint64_t)gr.count * (1 + gr.rice);
+        gr.blk_base = (uint32_t)blk;
+        blk += n_blocks(gr.count);
+    }
+    return bits;
+}
+
+// One canonical Huffman table per exponent with residuals (codec.py:369-392), symbols ascending, from
+// the counts of the dense symbols ([256][kDense]) and of the rare ones ((exponent << 17 | zz, count),
+// keys ascending); appended to E.tables.  lut gets (code << 5) | length of the dense symbols, rkeys and
+// rvals those of the rare ones.  Returns the bits of all residual codes.
+uint64_t build_tables(const std::vector<uint64_t> &dense, const std::vector<std::pair<uint32_t, uint64_t>> &rare,
+                      crx_encoded &E, std::vector<uint32_t> &lut, std::vector<uint32_t> &rkeys,
+                      std::vector<uint32_t> &rvals) {
+    lut.assign(256 * kDense, 0);
+    rkeys.clear();
+    rvals.clear();
+    uint64_t bits = 0;
+    std::vector<uint32_t> syms;
+    std::vector<uint64_t> counts;
+    size_t ri = 0;
+    for (int e = 0; e < 256; ++e) {
+        syms.clear();
+        counts.clear();
+        for (int z = 0; z < kDense; ++z)
+            if (dense[e * kDense + z]) {
+                syms.push_back(z);
+                counts.push_back(dense[e * kDense + z]);
+            }
+        for (; ri < rare.size() && (int)(rare[ri].first >> 17) == e; ++ri) {
+            syms.push_back(rare[ri].first & 0x1FFFF);
+            counts.push_back(rare[ri].second);
+        }
+        if (syms.empty()) continue;
+        const std::vector<int> len = huffman_lengths(counts);
+        const std::vector<uint32_t> code = canonical_codes(len);
+        Table tb;
+        tb.exponent = e;
+        tb.symbols = syms;
+        tb.lengths.resize(syms.size());
+        for (size_t k = 0; k < syms.size(); ++k) {
+            tb.lengths[k] = (uint8_t)len[k];
+            bits += counts[k] * (uint64_t)len[k];
+            const uint32_t v = (code[k] << 5) | (uint32_t)len[k];
+            if (syms[k] < (uint32_t)kDense) lut[e * kDense + syms[k]] = v;
+            else {
+                rkeys.push_back(((uint32_t)e << 17) | syms[k]);
+                rvals.push_back(v);
+            }
+        }
+        E.tables.push_back(std::move(tb));
+    }
+    return bits;
+}
+
+// An update encoded part by part (more changes than one pass indexes in 32 bits, or parts asked for):
+// the tensors in parts of at most `limit` elements.  Pass 1 ranks each part for its groups, symbol
+// counts and checksum parts; the tables are built from the whole update's counts (codec.py:362-392);
+// pass 2 ranks each part again and codes it at its bit offset in the one payload (the reference's
+// batches join mid-byte the same way, codec.py:394-410).  The bytes are those of a single pass.  A
+// part's buffers are reused by the next part's (Arena scopes).
+void encode_parts(const Layout &L, uint64_t limit, uint32_t slab, const int32_t *has_cache, const uint64_t *cache_vals,
+                  hipStream_t s, Arena &ar, crx_encoded &E) {
+    const std::vector<std::pair<uint32_t, uint32_t>> ranges = split_parts(L, limit);
+    struct Part {
+        Layout L;
+        std::vector<GroupDev> groups;  // Rice parameters and part-relative first blocks chosen on the host
+        std::vector<uint32_t> dense;   // [256][kDense] symbol counts
+        std::vector<std::pair<uint32_t, uint64_t>> rare;  // (exponent << 17 | zz, count), keys ascending
+        uint64_t C = 0, B = 0, blk0 = 0, bits = 0, bit0 = 0;
+    };
+    std::vector<Part> parts(ranges.size());
+    std::vector<uint64_t> dense(256 * kDense, 0);
+    std::vector<std::pair<uint32_t, uint64_t>> rare;
+    uint64_t C_all = 0, B_all = 0;
+    for (size_t k = 0; k < parts.size(); ++k) {
+        Part &p = parts[k];
+        p.L = sub_layout(L, ranges[k].first, ranges[k].second, slab);
+        const uint32_t T = (uint32_t)p.L.descs.size();
+        std::vector<uint64_t> hdelta(T), hfull(T);
+        std::vector<unsigned long long> hcost;
+        ar.begin_scope();
+        const Ranked R = rank_changes(p.L, slab, s, ar, nullptr, UINT64_MAX);
+        p.C = R.C;
+        uint64_t *t_delta = ar.get<uint64_t>(T), *t_full = ar.get<uint64_t>(T);
+        launch_tensor_sums(R.d_descs, T, R.delta, t_delta, s);
+        launch_tensor_sums(R.d_descs, T, R.full, t_full, s);
+        d2h(hdelta.data(), t_delta, T, s);
+        d2h(hfull.data(), t_full, T, s);
+        unsigned long long hs[2] = {0, 0};
+        uint32_t *d_rare = nullptr;
+        if (R.C) {
+            uint64_t *sorted = ar.get<uint64_t>(R.C);
+            launch_place(R.a, p.L.tiles, R.sd.tile_tensor, R.hall, R.hchg, R.gbase, sorted, R.C, s);
+            uint32_t *cmap = ar.get<uint32_t>((R.C + kElemsPerThread - 1) / kElemsPerThread);
+            launch_chunk_map(R.d_groups, (uint32_t)R.G, cmap, s);
+            launch_r0(R.d_groups, (uint32_t)R.G, sorted, s);
+            uint32_t *d_dense = ar.get<uint32_t>(256 * kDense);
+            d_rare = ar.get<uint32_t>(R.C);
+            unsigned long long *scnt = ar.get<unsigned long long>(2), *cost = ar.get<unsigned long long>(R.G * 3);
+            zero(d_dense, 256 * kDense, s);
+            zero(scnt, 2, s);
+            zero(cost, R.G * 3, s);
+            StatsArgs st{sorted, R.C, R.d_groups, (uint32_t)R.G, cmap, d_dense, d_rare, R.C, scnt, cost};
+            launch_stats(st, s);
+            p.groups.resize(R.G);
+            hcost.resize(R.G * 3);
+            p.dense.resize(256 * kDense);
+            d2h(p.groups.data(), R.d_groups, R.G, s);
+            d2h(hcost.data(), cost, R.G * 3, s);
+            d2h(p.dense.data(), d_dense, 256 * kDense, s);
+            d2h(hs, scnt, 2, s);
+        }
+        sync(s);
+        if (hs[1]) throw DeviceError("rare symbol list overflowed");
+        std::vector<uint32_t> hrare(hs[0]);
+        if (hs[0]) {
+            d2h(hrare.data(), d_rare, hs[0], s);
+            sync(s);
+        }
+        ar.end_scope();
+        std::sort(hrare.begin(), hrare.end());
+        for (size_t i = 0; i < hrare.size();) {
+            size_t j = i;
+            while (j < hrare.size() && hrare[j] == hrare[i]) ++j;
+            p.rare.emplace_back(hrare[i], (uint64_t)(j - i));
+            i = j;
+        }
+        if (p.C) {
+            p.bits = choose_rice(p.groups, hcost);
+            p.B = p.groups.back().blk_base + n_blocks(p.groups.back().count);
+        }
+        for (uint32_t d = 0; d < T; ++d) {  // checksums (codec.py:344-352) and groups of the part's tensors
+            const int32_t t = p.L.call_index[d];
+            E.checksum[t] = (has_cache && has_cache[t]) ? cache_vals[t] + hdelta[d] : hfull[d];
+        }
+        for (const GroupDev &gr : p.groups) {
+            const int32_t t = p.L.call_index[gr.tensor];
+            E.present[t] = 1;
+            E.groups[t].push_back(Group{(int)gr.exponent, gr.count, (int)gr.rice});
+        }
+        p.blk0 = B_all;
+        B_all += p.B;
+        C_all += p.C;
+        for (size_t i = 0; i < p.dense.size(); ++i) dense[i] += p.dense[i];
+        rare.insert(rare.end(), p.rare.begin(), p.rare.end());
+    }
+    E.total_changes = C_all;
+    if (!C_all) return;
+    // one table per exponent from the whole update's symbol counts
+    std::sort(rare.begin(), rare.end());
+    size_t w = 0;
+    for (size_t i = 0; i < rare.size(); ++i) {
+        if (w && rare[w - 1].first == rare[i].first) rare[w - 1].second += rare[i].second;
+        else rare[w++] = rare[i];
+    }
+    rare.resize(w);
+    std::vector<uint32_t> lut, rkeys, rvals;
+    build_tables(dense, rare, E, lut, rkeys, rvals);
+    // each part's bits: its gap codes (chosen above) and its residual codes; then its first bit
+    uint64_t total_bits = 0;
+    for (Part &p : parts) {
+        for (size_t i = 0; i < p.dense.size(); ++i) p.bits += (uint64_t)p.dense[i] * (lut[i] & 31u);
+        for (const auto &kc : p.rare) {
+            const size_t at = (size_t)(std::lower_bound(rkeys.begin(), rkeys.end(), kc.first) - rkeys.begin());
+            p.bits += kc.second * (rvals[at] & 31u);
+        }
+        p.bit0 = total_bits;
+        total_bits += p.bits;
+    }
+
+    // the payload and the block table of the whole update, written part by part
+    const uint64_t n_words = (total_bits + 31) / 32 + 4;
+    uint32_t *words = ar.get<uint32_t>(n_words);
+    uint32_t *bb = ar.get<uint32_t>(B_all);
+    uint32_t *d_lut = ar.get<uint32_t>(256 * kDense);
+    uint32_t *d_rk = ar.get<uint32_t>(rkeys.size()), *d_rv = ar.get<uint32_t>(rvals.size());
+    h2d(d_lut, lut.data(), lut.size(), s);
+    h2d(d_rk, rkeys.data(), rkeys.size(), s);
+    h2d(d_rv, rvals.data(), rvals.size(), s);
+    zero(words, n_words, s);
+    for (Part &p : parts) {
+        if (!p.C) continue;
+        const uint64_t G = p.groups.size();
+        ar.begin_scope();
+        const Ranked R = rank_changes(p.L, slab, s, ar, nullptr, UINT64_MAX);
+        if (R.C != p.C || R.G != G) throw DeviceError("a part of the update ranked differently the second time");
+        uint64_t *sorted = ar.get<uint64_t>(p.C);
+        launch_place(R.a, p.L.tiles, R.sd.tile_tensor, R.hall, R.hchg, R.gbase, sorted, p.C, s);
+        GroupDev *d_groups = ar.get<GroupDev>(G);
+        h2d(d_groups, p.groups.data(), G, s);
+        const uint64_t n_thr = (p.C + kElemsPerThread - 1) / kElemsPerThread;
+        uint32_t *cmap = ar.get<uint32_t>(n_thr);
+        launch_chunk_map(d_groups, (uint32_t)G, cmap, s);
+        unsigned long long *tsum = ar.get<unsigned long long>(n_thr), *toff = ar.get<unsigned long long>(n_thr + 1);
+        unsigned long long *bstart = ar.get<unsigned long long>(p.B + 1);
+        unsigned int *bovf = ar.get<unsigned int>(1);
+        CodeArgs ca{sorted, p.C, d_groups, (uint32_t)G, d_lut, d_rk, d_rv, (uint32_t)rkeys.size(), cmap, tsum, toff,
+                    words, bstart, n_words, bovf, p.bit0};
+        launch_code_lengths(ca, s);
+        launch_scan_u64(tsum, n_thr, toff, ar.get<unsigned long long>(scan_parts(n_thr)), s);
+        zero(bovf, 1, s);
+        const unsigned long long end = p.bit0 + p.bits;  // the block starts are payload bits: so is the end
+        h2d(bstart + p.B, &end, 1, s);
+        launch_pack(ca, s);
+        launch_block_bits(bstart, p.B, bb + p.blk0, bovf, s);
+        unsigned int hovf = 0;
+        unsigned long long dev_bits = 0;
+        d2h(&hovf, bovf, 1, s);
+        d2h(&dev_bits, toff + n_thr, 1, s);
+        sync(s);
+        ar.end_scope();
+        if (hovf & 2u || dev_bits != p.bits) throw DeviceError("the packed payload's size differs from its codes' lengths");
+        if (hovf) throw Invalid("a block exceeds 2^32 bits; the update cannot be represented");
+    }
+    E.n_blocks = B_all;
+    E.d_block_bits = bb;
+    E.payload_len = (total_bits + 7) / 8;
+    E.d_payload = reinterpret_cast<const uint8_t *>(words);
+}
+
 void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news, const uint64_t *numels,
             const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab_req, hipStream_t s, Arena &ar,
             crx_encoded &E) {
@@ -697,60 +1068,31 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     }
     if (L.descs.empty()) return;
     finish_layout(L, slab);
+    const uint64_t forced = part_elements_override();
+    if (forced && layout_elements(L) > forced) {  // parts asked for (tests of the part-wise path)
+        encode_parts(L, forced, slab, has_cache, cache_vals, s, ar, E);
+        return;
+    }
     const uint32_t T = (uint32_t)L.descs.size(), tiles = L.tiles;
     const uint64_t hint_key = tiles;
     ar.reserve(g_encode_hint.get(hint_key));
     hc.mark("enc_layout");
 
-    TensorDesc *d_descs = ar.get<TensorDesc>(T);
-    h2d(d_descs, L.descs.data(), T, s);
-    uint32_t *hall = ar.get<uint32_t>((uint64_t)tiles * 256), *hchg = ar.get<uint32_t>((uint64_t)tiles * 256);
-    uint64_t *delta = ar.get<uint64_t>(tiles), *full = ar.get<uint64_t>(tiles);
-    ScanDev sd = upload_scan(ar, L, d_descs, s);
-    uint32_t *tot_all = ar.get<uint32_t>((uint64_t)T * 256), *tot_chg = ar.get<uint32_t>((uint64_t)T * 256);
-    GroupDev *d_groups = ar.get<GroupDev>((uint64_t)T * 256);
-    uint32_t *gbase = ar.get<uint32_t>((uint64_t)T * 256);
-    unsigned long long *gcnt = ar.get<unsigned long long>(2);
-
-    // Each slab stores its change records in a region of its own, sized for 1/24 of its elements
-    // (+64).  If one overflows, the exact counts of that pass give exact regions for a second pass.
-    const uint64_t per_slab = slab / 24 + 64;
-    uint32_t *rec_count = ar.get<uint32_t>(tiles);
-    unsigned int *ovf = ar.get<unsigned int>(1);
-    zero(ovf, 1, s);
-    EncRankArgs a{d_descs, sd.tile_tensor, T, slab, hall, hchg, ar.get<uint64_t>((uint64_t)tiles * per_slab), nullptr,
-                  per_slab, rec_count, ovf, delta, full};
-    launch_enc_rank(a, tiles, s);
-    hc.mark("enc_setup");
-    // the scans and groups need only the counts, which are exact even when a slab's records overflowed
-    // their region; the overflow flag is read with the group totals, and on overflow the rank pass runs
-    // again into exact regions (rewriting the counts, so they are scanned again)
-    unsigned int hovf1 = 0;
-    unsigned long long gc[2];
-    for (int pass = 0;; ++pass) {
-        launch_scan_tables(d_descs, hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_all, s);
-        launch_scan_tables(d_descs, hchg, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, tot_chg, s);
-        launch_enc_groups(tot_chg, T, d_groups, gbase, gcnt, s);
-        d2h(&hovf1, ovf, 1, s);
-        d2h(gc, gcnt, 2, s);
-        sync(s);
-        if (!hovf1) break;
-        if (pass) throw DeviceError("change records overflowed exact regions");
-        unsigned long long *rec_base = ar.get<unsigned long long>(tiles + 1);
-        launch_scan_u32(rec_count, tiles, rec_base, ar.get<unsigned long long>(scan_parts(tiles)), s);
-        unsigned long long total = 0;
-        d2h(&total, rec_base + tiles, 1, s);
-        sync(s);
-        a.rec = ar.get<uint64_t>(total);
-        a.rec_base = rec_base;
-        zero(ovf, 1, s);
-        launch_enc_rank(a, tiles, s);
-    }
+    Ranked R = rank_changes(L, slab, s, ar, &hc, 1ULL << 32);
     hc.mark("enc_wait_groups");
-    const uint64_t G = gc[0], C = gc[1];
+    if (R.C >= (1ULL << 32)) {  // too many changes for one pass: the update is encoded part by part
+        encode_parts(L, kPartElements, slab, has_cache, cache_vals, s, ar, E);
+        return;
+    }
+    const uint64_t G = R.G, C = R.C;
     E.total_changes = C;
     if (C == 0) return;
-    if (C >= (1ULL << 32)) throw Invalid("2^32 or more changes in one update are not supported");
+    TensorDesc *const d_descs = R.d_descs;
+    GroupDev *const d_groups = R.d_groups;
+    uint64_t *const delta = R.delta, *const full = R.full;
+    const EncRankArgs &a = R.a;
+    const ScanDev &sd = R.sd;
+    uint32_t *const hall = R.hall, *const hchg = R.hchg, *const gbase = R.gbase;
 
     uint64_t *sorted = ar.get<uint64_t>(C);
     launch_place(a, tiles, sd.tile_tensor, hall, hchg, gbase, sorted, C, s);
@@ -796,63 +1138,22 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     }
     hc.mark("enc_wait_rare");
     std::sort(hrare.begin(), hrare.end());
+    std::vector<std::pair<uint32_t, uint64_t>> rare_runs;
+    for (size_t i = 0; i < hrare.size();) {
+        size_t j = i;
+        while (j < hrare.size() && hrare[j] == hrare[i]) ++j;
+        rare_runs.emplace_back(hrare[i], (uint64_t)(j - i));
+        i = j;
+    }
 
     // What the code kernels need first: Rice parameters and first blocks of the groups (codec.py:354-360),
     // and one canonical Huffman table per exponent, symbols ascending (codec.py:369-392).  The payload's
     // length follows from them: a group's gap codes take its chosen cost, its symbols their code lengths.
-    uint64_t blk = 0, total_bits = 0;
-    for (uint64_t g = 0; g < G; ++g) {
-        GroupDev &gr = groups[g];
-        const int c[3] = {(int)(gr.r0 ? gr.r0 - 1 : 0), (int)gr.r0, (int)std::min<uint32_t>(gr.r0 + 1, kMaxRice)};
-        const uint64_t sh[3] = {hcost[g * 3], hcost[g * 3 + 1], hcost[g * 3 + 2]};
-        gr.rice = (uint32_t)rice_choose(gr.count, c, sh);
-        const int k = gr.rice == (uint32_t)c[0] ? 0 : gr.rice == (uint32_t)c[1] ? 1 : 2;
-        total_bits += sh[k] + (uint64_t)gr.count * (1 + gr.rice);
-        gr.blk_base = (uint32_t)blk;
-        blk += n_blocks(gr.count);
-    }
-    const uint64_t B = blk;
-    std::vector<uint32_t> lut(256 * kDense, 0), rkeys, rvals;
-    std::vector<uint32_t> syms;
-    std::vector<uint64_t> counts;
-    size_t ri = 0;
-    for (int e = 0; e < 256; ++e) {
-        syms.clear();
-        counts.clear();
-        for (int z = 0; z < kDense; ++z)
-            if (hdense[e * kDense + z]) {
-                syms.push_back(z);
-                counts.push_back(hdense[e * kDense + z]);
-            }
-        while (ri < hrare.size() && (int)(hrare[ri] >> 17) == e) {
-            const uint32_t z = hrare[ri] & 0x1FFFF;
-            uint64_t c = 0;
-            while (ri < hrare.size() && hrare[ri] == (((uint32_t)e << 17) | z)) {
-                ++c;
-                ++ri;
-            }
-            syms.push_back(z);
-            counts.push_back(c);
-        }
-        if (syms.empty()) continue;
-        const std::vector<int> len = huffman_lengths(counts);
-        const std::vector<uint32_t> code = canonical_codes(len);
-        Table tb;
-        tb.exponent = e;
-        tb.symbols = syms;
-        tb.lengths.resize(syms.size());
-        for (size_t k = 0; k < syms.size(); ++k) {
-            tb.lengths[k] = (uint8_t)len[k];
-            total_bits += counts[k] * (uint64_t)len[k];
-            const uint32_t v = (code[k] << 5) | (uint32_t)len[k];
-            if (syms[k] < (uint32_t)kDense) lut[e * kDense + syms[k]] = v;
-            else {
-                rkeys.push_back(((uint32_t)e << 17) | syms[k]);
-                rvals.push_back(v);
-            }
-        }
-        E.tables.push_back(std::move(tb));
-    }
+    uint64_t total_bits = choose_rice(groups, hcost);
+    const uint64_t B = groups.empty() ? 0 : groups.back().blk_base + n_blocks(groups.back().count);
+    std::vector<uint64_t> dense64(hdense.begin(), hdense.end());
+    std::vector<uint32_t> lut, rkeys, rvals;
+    total_bits += build_tables(dense64, rare_runs, E, lut, rkeys, rvals);
     hc.mark("enc_tables");
 
     // the code lengths, their offsets and the bits, with no wait: the payload's size is known
@@ -909,113 +1210,58 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
 // codec.apply (codec.py:578-717) on the device: decode, locate, verify, then write.
 uint32_t apply_slab(int32_t slab_req) { return slab_size(slab_req); }
 
-void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets, const uint64_t *numels,
-           const int32_t *has_cache, const uint64_t *cache_vals, uint32_t *const *hist_in, uint32_t *const *hist_out,
-           int32_t slab_req, hipStream_t s, Arena &ar, uint64_t *changed) {
-    *changed = 0;
-    const uint32_t T = (uint32_t)u.tensors.size();
-    if (!T) return;
-    HostClock hc;
-    const uint32_t slab = apply_slab(slab_req);
-    const uint64_t C = u.total_changes;
-    if (C >= (1ULL << 32)) throw Invalid("2^32 or more changes in one update are not supported");
-    Layout L;
-    for (uint32_t t = 0; t < T; ++t) {
-        if (numels[t] != u.tensors[t].numel) throw Invalid(u.tensors[t].name + ": numel mismatch");
-        TensorDesc d = make_desc(targets[t], numels[t]);
-        d.cold = (has_cache && has_cache[t]) ? 0u : 1u;
-        d.hist_in = hist_in ? hist_in[t] : nullptr;
-        d.hist_out = hist_out ? hist_out[t] : nullptr;
-        L.descs.push_back(d);
-        L.call_index.push_back((int32_t)t);
-    }
-    finish_layout(L, slab);
-    const uint32_t tiles = L.tiles;
-    const uint64_t hint_key = (uint64_t)tiles + C / 256;
-    ar.reserve(g_apply_hint.get(hint_key));
-    hc.mark("apply_layout");
+// The update's device state that its parts share: the decoding tables, the payload, the block table and
+// each block's first payload bit.
+struct ApplyShared {
+    uint32_t *lim = nullptr, *off = nullptr, *syms = nullptr;
+    uint32_t n_syms = 0;
+    uint64_t *pay = nullptr;
+    uint64_t pay_words = 0;
+    uint32_t *bb = nullptr;            // [blocks] bits of each block
+    unsigned long long *boff = nullptr;  // [blocks + 1] first payload bit of each block
+};
 
-    // groups, decoding tables and the group lookup (codec.py:594-625)
-    int table_of[256];
-    std::fill(table_of, table_of + 256, -1);
-    // per table and code length l: lim = end of the length-l codes left-justified to 17 bits (the
-    // canonical ranges are consecutive, so the length of a 17-bit peek p is 1 + #{l : lim[l] <= p}),
-    // off = symbol index of the length-l code 0
-    std::vector<uint32_t> lim(u.tables.size() * 17, 0), off(u.tables.size() * 17, 0), syms;
-    for (size_t ti = 0; ti < u.tables.size(); ++ti) {
-        const Table &tb = u.tables[ti];
-        table_of[tb.exponent] = (int)ti;
-        uint32_t per_len[kMaxCodeLen + 1] = {};
-        for (uint8_t l : tb.lengths) per_len[l]++;
-        std::vector<uint32_t> order(tb.symbols.size());
-        for (size_t k = 0; k < order.size(); ++k) order[k] = (uint32_t)k;
-        std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return tb.lengths[a] < tb.lengths[b]; });
-        uint32_t code = 0, idx = (uint32_t)syms.size();
-        for (int l = 1; l <= kMaxCodeLen; ++l) {
-            lim[ti * 17 + l - 1] = (code + per_len[l]) << (kMaxCodeLen - l);
-            off[ti * 17 + l - 1] = idx - code;
-            code = (code + per_len[l]) << 1;
-            idx += per_len[l];
-        }
-        for (uint32_t k : order) syms.push_back(tb.symbols[k]);
-    }
+// A part of an update: tensors [t0, t1) of the update, their groups with element and block bases
+// counted from the part's first change and block, and the part's blocks [b0, b0 + B) of the update.
+struct ApplyPart {
+    uint32_t t0 = 0, t1 = 0;
     std::vector<GroupDev> groups;
-    std::vector<int32_t> group_of((uint64_t)T * 256, -1);
-    uint64_t elem = 0, blk = 0;
-    for (uint32_t t = 0; t < T; ++t)
-        for (const Group &g : u.tensors[t].groups) {
-            GroupDev gd{};
-            gd.tensor = t;
-            gd.exponent = (uint32_t)g.exponent;
-            gd.count = (uint32_t)g.count;
-            gd.elem_base = (uint32_t)elem;
-            gd.blk_base = (uint32_t)blk;
-            gd.rice = (uint32_t)g.rice;
-            gd.table = (uint32_t)table_of[g.exponent];
-            group_of[(uint64_t)t * 256 + g.exponent] = (int32_t)groups.size();
-            groups.push_back(gd);
-            elem += g.count;
-            blk += n_blocks(g.count);
-        }
-    const uint64_t G = groups.size(), B = blk;
-    std::vector<uint32_t> tensor_chg(T + 1, (uint32_t)C);  // first change of each tensor (its changes are contiguous)
-    for (int64_t gi = (int64_t)G - 1; gi >= 0; --gi) tensor_chg[groups[gi].tensor] = groups[gi].elem_base;
-    for (int64_t t = (int64_t)T - 1; t >= 0; --t) tensor_chg[t] = std::min(tensor_chg[t], tensor_chg[t + 1]);
+    std::vector<int32_t> group_of;  // [tensors of the part][256]: group of (tensor, exponent), or -1
+    uint64_t C = 0, B = 0, b0 = 0;
+};
 
-    hc.mark("apply_tables");
+// What one part's pass found: error flags, and per tensor of the part the checksum delta and (for
+// tensors without a cached checksum) the full checksum of the receiver's weights before the update.
+struct PartCheck {
+    unsigned int bad = 0;
+    std::vector<uint64_t> delta, full;
+};
+
+// One part of an update, or the whole of it (codec.py:578-717): decode, locate, verify, then write.
+// dry: the part is only verified; nothing is written (no write-through, no commit, and the receiver's
+// exponent counts are not kept up to date).
+PartCheck apply_part(const Update &u, const Layout &L, const ApplyPart &P, const ApplyShared &sh,
+                     const int32_t *has_cache, const uint64_t *cache_vals, uint32_t slab, int32_t slab_req, bool dry,
+                     hipStream_t s, Arena &ar, HostClock &hc) {
+    const uint32_t T = (uint32_t)L.descs.size(), tiles = L.tiles;
+    const uint64_t G = P.groups.size(), B = P.B, C = P.C;
+    std::vector<uint32_t> tensor_chg(T + 1, (uint32_t)C);  // first change of each tensor (its changes are contiguous)
+    for (int64_t gi = (int64_t)G - 1; gi >= 0; --gi) tensor_chg[P.groups[gi].tensor] = P.groups[gi].elem_base;
+    for (int64_t t = (int64_t)T - 1; t >= 0; --t) tensor_chg[t] = std::min(tensor_chg[t], tensor_chg[t + 1]);
+    std::vector<TensorDesc> descs = L.descs;
+    if (dry)
+        for (TensorDesc &d : descs) d.hist_out = nullptr;
+
     // what the decoder needs goes first: it starts while the rest is enqueued
     TensorDesc *d_descs = ar.get<TensorDesc>(T);
-    h2d(d_descs, L.descs.data(), T, s);
+    h2d(d_descs, descs.data(), T, s);
     GroupDev *d_groups = ar.get<GroupDev>(G);
-    h2d(d_groups, groups.data(), G, s);
+    h2d(d_groups, P.groups.data(), G, s);
     uint32_t *bmap = ar.get<uint32_t>(B);
     BlockInfo *binfo = ar.get<BlockInfo>(B);
     launch_block_map(d_groups, (uint32_t)G, bmap, binfo, s);
-    uint32_t *d_lim = ar.get<uint32_t>(lim.size()), *d_off = ar.get<uint32_t>(off.size());
-    uint32_t *d_syms = ar.get<uint32_t>(syms.size());
-    h2d(d_lim, lim.data(), lim.size(), s);
-    h2d(d_off, off.data(), off.size(), s);
-    h2d(d_syms, syms.data(), syms.size(), s);
-    uint32_t *d_bb = ar.get<uint32_t>(B);
-    if (payload_dev)  // the update is in device memory: its block table precedes the payload there
-        HIP_OK(hipMemcpyAsync(d_bb, payload_dev - (u.payload_offset - u.block_table_offset), 4 * B,
-                              hipMemcpyDeviceToDevice, s));
-    else
-        HIP_OK(hipMemcpyAsync(d_bb, u.block_table, 4 * B, hipMemcpyHostToDevice, s));
-    const uint64_t pay_words = (u.payload_len + 7) / 8 + 2;
-    uint64_t *pay = ar.get<uint64_t>(pay_words);
-    // the copy fills whole words up to payload_len / 8; the rest (partial last word, two pad words) is zeroed
-    zero(pay + u.payload_len / 8, pay_words - u.payload_len / 8, s);
-    if (u.payload_len) {
-        if (payload_dev)
-            HIP_OK(hipMemcpyAsync(pay, payload_dev, u.payload_len, hipMemcpyDeviceToDevice, s));
-        else
-            copy_from_host(reinterpret_cast<uint8_t *>(pay), u.payload_host, u.payload_len, s);
-    }
     unsigned int *bad = ar.get<unsigned int>(1);
     zero(bad, 1, s);
-    unsigned long long *boff = ar.get<unsigned long long>(B + 1);
-    launch_scan_u32(d_bb, B, boff, ar.get<unsigned long long>(scan_parts(B)), s);
 
     // The decoder needs nothing from the receiver's weights: it runs on the auxiliary stream while
     // the main stream takes the exponent counts (pass A) and their scans.
@@ -1023,8 +1269,8 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     unsigned long long *blk_sum = ar.get<unsigned long long>(B), *blk_prefix = ar.get<unsigned long long>(B + 1);
     hc.mark("apply_upload");
     Fork fork(s);
-    DecodeArgs da{d_descs, pay, pay_words, d_bb, boff, B, d_groups, (uint32_t)G, bmap, d_lim, d_off, d_syms,
-                  (uint32_t)syms.size(), dz, blk_sum, bad};
+    DecodeArgs da{d_descs, sh.pay, sh.pay_words, sh.bb + P.b0, sh.boff + P.b0, B, d_groups, (uint32_t)G, bmap,
+                  sh.lim, sh.off, sh.syms, sh.n_syms, dz, blk_sum, bad};
     launch_decode(da, fork.aux);
     launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), fork.aux);
 
@@ -1033,7 +1279,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     ScanDev sd = upload_scan(ar, L, d_descs, s);
     uint32_t *sizes = ar.get<uint32_t>((uint64_t)T * 256);
     int32_t *d_gof = ar.get<int32_t>((uint64_t)T * 256);
-    h2d(d_gof, group_of.data(), group_of.size(), s);
+    h2d(d_gof, P.group_of.data(), P.group_of.size(), s);
     uint32_t *local = ar.get<uint32_t>(C);
     unsigned long long *rec = ar.get<unsigned long long>(C);  // the select pass's records, slab by slab
     uint32_t *pn = ar.get<uint32_t>(C);                       // offset in the slab | new bits << 16
@@ -1047,7 +1293,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     // of old checksums not cached: the select pass sums the rest as it streams the weights); cached
     // counts are read by the scan in place (copied only to a separate hist_out)
     std::vector<uint32_t> hist_list;
-    for (const TensorDesc &d : L.descs) {
+    for (const TensorDesc &d : descs) {
         const bool cached = d.hist_in != nullptr;
         if (!cached || (d.hist_out && d.hist_out != d.hist_in))
             for (uint32_t i = 0; i < d.n_tiles; ++i) hist_list.push_back(d.tile_begin + i);
@@ -1075,63 +1321,229 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     uint32_t *done = ar.get<uint32_t>(tiles);
     // the verdict's inputs, set up before the select pass writes anything: between its writes and the
     // commit that can undo them, the host only launches
-    std::vector<uint64_t> want(T), cached(T, 0);
-    std::vector<int32_t> has(T, 0);
-    for (uint32_t t = 0; t < T; ++t) {
-        want[t] = u.tensors[t].checksum;
-        has[t] = (has_cache && has_cache[t]) ? 1 : 0;
-        if (has[t]) cached[t] = cache_vals[t];
+    uint64_t *d_want = nullptr, *d_cached = nullptr;
+    int32_t *d_has = nullptr;
+    unsigned int *ok = nullptr;
+    if (!dry) {
+        std::vector<uint64_t> want(T), cached(T, 0);
+        std::vector<int32_t> has(T, 0);
+        for (uint32_t d = 0; d < T; ++d) {
+            const uint32_t t = P.t0 + d;
+            want[d] = u.tensors[t].checksum;
+            has[d] = (has_cache && has_cache[t]) ? 1 : 0;
+            if (has[d]) cached[d] = cache_vals[t];
+        }
+        d_want = ar.get<uint64_t>(T);
+        d_cached = ar.get<uint64_t>(T);
+        d_has = ar.get<int32_t>(T);
+        ok = ar.get<unsigned int>(1);
+        h2d(d_want, want.data(), T, s);
+        h2d(d_cached, cached.data(), T, s);
+        h2d(d_has, has.data(), T, s);
     }
-    uint64_t *d_want = ar.get<uint64_t>(T), *d_cached = ar.get<uint64_t>(T);
-    int32_t *d_has = ar.get<int32_t>(T);
-    unsigned int *ok = ar.get<unsigned int>(1);
-    h2d(d_want, want.data(), T, s);
-    h2d(d_cached, cached.data(), T, s);
-    h2d(d_has, has.data(), T, s);
     SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, rec, rstart, tchg, bad, more,
                   n_more, (uint32_t)std::min<uint64_t>(1024, (uint64_t)kSelMoreWindows * tiles), dz, sdelta, multi,
                   done, (uint32_t)C, full};
     launch_locate(sa, tiles, s);
+    // a dry pass marks every slab as one of several windows: the select pass then writes nothing, and
+    // the verify pass takes every slab's checksum delta
+    if (dry) HIP_OK(hipMemsetAsync(multi, 1, tiles, s));
     // slabs streamed in one window are written through by the select pass, before the verdict: the
     // commit below undoes those writes if the update does not verify
     bool any_cold = false;
-    for (const TensorDesc &d : L.descs) any_cold |= d.cold != 0;
+    for (const TensorDesc &d : descs) any_cold |= d.cold != 0;
     launch_select(sa, tiles, C > kSelectDenseTargets * tiles, any_cold, s);
     SlabArgs sla{d_descs, sd.tile_tensor, slab, rstart, rec, dz, pn, sdelta, bad, nullptr, (uint32_t)C, multi, done};
     launch_verify(sla, tiles, s);
     launch_tensor_sums(d_descs, T, sdelta, tdelta, s);
     launch_tensor_sums(d_descs, T, full, t_full, s);  // the select pass summed the cold slabs
-    // the verdict on the device too, and the commit behind it (the remaining writes if the update
-    // verifies, the undoing of the select pass's if not); the host waits for the verdict's data only
-    launch_verdict(T, reinterpret_cast<const unsigned long long *>(tdelta), t_full, d_has, d_cached, d_want, bad, ok,
-                   s);
-    sla.ok = ok;
-    launch_commit(sla, tiles, s);  // next to the verdict: nothing on the host can fail in between
+    if (!dry) {
+        // the verdict on the device too, and the commit behind it (the remaining writes if the update
+        // verifies, the undoing of the select pass's if not); the host waits for the verdict's data only
+        launch_verdict(T, reinterpret_cast<const unsigned long long *>(tdelta), t_full, d_has, d_cached, d_want, bad,
+                       ok, s);
+        sla.ok = ok;
+        launch_commit(sla, tiles, s);  // next to the verdict: nothing on the host can fail in between
+    }
     hc.mark("apply_launch");
 
-    unsigned int hbad = 0;
-    std::vector<uint64_t> hdelta(T), hfull(T);
-    d2h(&hbad, bad, 1, s);
-    d2h(hdelta.data(), tdelta, T, s);
-    d2h(hfull.data(), t_full, T, s);
+    PartCheck r;
+    r.delta.resize(T);
+    r.full.resize(T);
+    d2h(&r.bad, bad, 1, s);
+    d2h(r.delta.data(), tdelta, T, s);
+    d2h(r.full.data(), t_full, T, s);
     t_stage.finish();  // the downloads above (behind the commit, which exits at once when the update verifies)
     hc.mark("apply_wait_verify");
-    // the reference's verdict (codec.py:598-604,696-712): the group-size check first, then any
-    // checksum mismatch (naming up to three tensors), then any other inconsistency
-    if (hbad & kBadGroup) throw Corrupt("group has more changes than elements");
+    return r;
+}
+
+// The reference's verdict (codec.py:598-604,696-712) from the passes' findings over the whole update:
+// the group-size check first, then any checksum mismatch (naming up to three tensors), then any other
+// inconsistency.  Returns when the whole update verifies.
+void raise_verdict(const Update &u, unsigned int bad, const std::vector<uint64_t> &delta,
+                   const std::vector<uint64_t> &full, const int32_t *has_cache, const uint64_t *cache_vals) {
+    if (bad & kBadGroup) throw Corrupt("group has more changes than elements");
     std::vector<std::string> wrong;
-    for (uint32_t t = 0; t < T; ++t) {
-        const uint64_t old = (has_cache && has_cache[t]) ? cache_vals[t] : hfull[t];
-        if (old + hdelta[t] != u.tensors[t].checksum) wrong.push_back(u.tensors[t].name);
+    for (uint32_t t = 0; t < (uint32_t)u.tensors.size(); ++t) {
+        const uint64_t old = (has_cache && has_cache[t]) ? cache_vals[t] : full[t];
+        if (old + delta[t] != u.tensors[t].checksum) wrong.push_back(u.tensors[t].name);
     }
     if (!wrong.empty()) {
         std::string m = "update does not verify (checksum mismatch: [";
         for (size_t i = 0; i < std::min<size_t>(3, wrong.size()); ++i) m += (i ? ", " : "") + py_repr(wrong[i]);
         throw Corrupt(m + "])");
     }
-    if (hbad) throw Corrupt("payload positions outside their exponent groups");
-    g_apply_hint.put(hint_key, ar.total);
-    // the verdict is final, and the writes behind it are done (the downloads above followed them)
+    if (bad) throw Corrupt("payload positions outside their exponent groups");
+}
+
+void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets, const uint64_t *numels,
+           const int32_t *has_cache, const uint64_t *cache_vals, uint32_t *const *hist_in, uint32_t *const *hist_out,
+           int32_t slab_req, hipStream_t s, Arena &ar, uint64_t *changed) {
+    *changed = 0;
+    const uint32_t T = (uint32_t)u.tensors.size();
+    if (!T) return;
+    HostClock hc;
+    const uint32_t slab = apply_slab(slab_req);
+    const uint64_t C = u.total_changes;
+    Layout L;
+    for (uint32_t t = 0; t < T; ++t) {
+        if (numels[t] != u.tensors[t].numel) throw Invalid(u.tensors[t].name + ": numel mismatch");
+        TensorDesc d = make_desc(targets[t], numels[t]);
+        d.cold = (has_cache && has_cache[t]) ? 0u : 1u;
+        d.hist_in = hist_in ? hist_in[t] : nullptr;
+        d.hist_out = hist_out ? hist_out[t] : nullptr;
+        L.descs.push_back(d);
+        L.call_index.push_back((int32_t)t);
+    }
+    finish_layout(L, slab);
+    // an update of 2^32 or more changes is applied part by part (each part's changes indexed in 32 bits)
+    const uint64_t forced = part_elements_override();
+    const bool split = C >= (1ULL << 32) || (forced && layout_elements(L) > forced);
+    const std::vector<std::pair<uint32_t, uint32_t>> ranges =
+        split ? split_parts(L, forced ? forced : kPartElements) : std::vector<std::pair<uint32_t, uint32_t>>{{0, T}};
+    const uint32_t tiles = L.tiles;
+    const uint64_t hint_key = (uint64_t)tiles + C / 256;
+    if (!split) ar.reserve(g_apply_hint.get(hint_key));
+    hc.mark("apply_layout");
+
+    // groups, decoding tables and the group lookup (codec.py:594-625)
+    int table_of[256];
+    std::fill(table_of, table_of + 256, -1);
+    // per table and code length l: lim = end of the length-l codes left-justified to 17 bits (the
+    // canonical ranges are consecutive, so the length of a 17-bit peek p is 1 + #{l : lim[l] <= p}),
+    // off = symbol index of the length-l code 0
+    std::vector<uint32_t> lim(u.tables.size() * 17, 0), off(u.tables.size() * 17, 0), syms;
+    for (size_t ti = 0; ti < u.tables.size(); ++ti) {
+        const Table &tb = u.tables[ti];
+        table_of[tb.exponent] = (int)ti;
+        uint32_t per_len[kMaxCodeLen + 1] = {};
+        for (uint8_t l : tb.lengths) per_len[l]++;
+        std::vector<uint32_t> order(tb.symbols.size());
+        for (size_t k = 0; k < order.size(); ++k) order[k] = (uint32_t)k;
+        std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return tb.lengths[a] < tb.lengths[b]; });
+        uint32_t code = 0, idx = (uint32_t)syms.size();
+        for (int l = 1; l <= kMaxCodeLen; ++l) {
+            lim[ti * 17 + l - 1] = (code + per_len[l]) << (kMaxCodeLen - l);
+            off[ti * 17 + l - 1] = idx - code;
+            code = (code + per_len[l]) << 1;
+            idx += per_len[l];
+        }
+        for (uint32_t k : order) syms.push_back(tb.symbols[k]);
+    }
+    std::vector<ApplyPart> parts(ranges.size());
+    uint64_t B_all = 0;
+    for (size_t k = 0; k < ranges.size(); ++k) {
+        ApplyPart &P = parts[k];
+        P.t0 = ranges[k].first;
+        P.t1 = ranges[k].second;
+        P.group_of.assign((uint64_t)(P.t1 - P.t0) * 256, -1);
+        uint64_t elem = 0, blk = 0;
+        for (uint32_t t = P.t0; t < P.t1; ++t)
+            for (const Group &g : u.tensors[t].groups) {
+                GroupDev gd{};
+                gd.tensor = t - P.t0;
+                gd.exponent = (uint32_t)g.exponent;
+                gd.count = (uint32_t)g.count;
+                gd.elem_base = (uint32_t)elem;
+                gd.blk_base = (uint32_t)blk;
+                gd.rice = (uint32_t)g.rice;
+                gd.table = (uint32_t)table_of[g.exponent];
+                P.group_of[(uint64_t)(t - P.t0) * 256 + g.exponent] = (int32_t)P.groups.size();
+                P.groups.push_back(gd);
+                elem += g.count;
+                blk += n_blocks(g.count);
+            }
+        // a part's changes are at most its elements (the parser checks each tensor's), below 2^32
+        if (elem >= (1ULL << 32)) throw Invalid("a part of the update has 2^32 or more changes");
+        P.C = elem;
+        P.B = blk;
+        P.b0 = B_all;
+        B_all += blk;
+    }
+    hc.mark("apply_tables");
+
+    ApplyShared sh;
+    sh.lim = ar.get<uint32_t>(lim.size());
+    sh.off = ar.get<uint32_t>(off.size());
+    sh.syms = ar.get<uint32_t>(syms.size());
+    sh.n_syms = (uint32_t)syms.size();
+    h2d(sh.lim, lim.data(), lim.size(), s);
+    h2d(sh.off, off.data(), off.size(), s);
+    h2d(sh.syms, syms.data(), syms.size(), s);
+    sh.bb = ar.get<uint32_t>(B_all);
+    if (payload_dev)  // the update is in device memory: its block table precedes the payload there
+        HIP_OK(hipMemcpyAsync(sh.bb, payload_dev - (u.payload_offset - u.block_table_offset), 4 * B_all,
+                              hipMemcpyDeviceToDevice, s));
+    else
+        HIP_OK(hipMemcpyAsync(sh.bb, u.block_table, 4 * B_all, hipMemcpyHostToDevice, s));
+    sh.pay_words = (u.payload_len + 7) / 8 + 2;
+    sh.pay = ar.get<uint64_t>(sh.pay_words);
+    // the copy fills whole words up to payload_len / 8; the rest (partial last word, two pad words) is zeroed
+    zero(sh.pay + u.payload_len / 8, sh.pay_words - u.payload_len / 8, s);
+    if (u.payload_len) {
+        if (payload_dev)
+            HIP_OK(hipMemcpyAsync(sh.pay, payload_dev, u.payload_len, hipMemcpyDeviceToDevice, s));
+        else
+            copy_from_host(reinterpret_cast<uint8_t *>(sh.pay), u.payload_host, u.payload_len, s);
+    }
+    sh.boff = ar.get<unsigned long long>(B_all + 1);
+    launch_scan_u32(sh.bb, B_all, sh.boff, ar.get<unsigned long long>(scan_parts(B_all)), s);
+
+    if (!split) {
+        const PartCheck r = apply_part(u, L, parts[0], sh, has_cache, cache_vals, slab, slab_req, false, s, ar, hc);
+        raise_verdict(u, r.bad, r.delta, r.full, has_cache, cache_vals);
+        g_apply_hint.put(hint_key, ar.total);
+        // the verdict is final, and the writes behind it are done (the downloads above followed them)
+        *changed = C;
+        return;
+    }
+    // Part by part: every part verified first without writing, the verdict taken on the whole update,
+    // then each part applied (its own verification passes again: the same inputs).  Each part's buffers
+    // are reused by the next part's.
+    unsigned int bad = 0;
+    std::vector<uint64_t> delta(T, 0), full(T, 0);
+    std::vector<Layout> layouts;
+    for (const ApplyPart &P : parts) layouts.push_back(sub_layout(L, P.t0, P.t1, slab));
+    for (size_t k = 0; k < parts.size(); ++k) {
+        ar.begin_scope();
+        const PartCheck r = apply_part(u, layouts[k], parts[k], sh, has_cache, cache_vals, slab, slab_req, true, s, ar, hc);
+        ar.end_scope();
+        bad |= r.bad;
+        std::copy(r.delta.begin(), r.delta.end(), delta.begin() + parts[k].t0);
+        std::copy(r.full.begin(), r.full.end(), full.begin() + parts[k].t0);
+    }
+    raise_verdict(u, bad, delta, full, has_cache, cache_vals);
+    for (size_t k = 0; k < parts.size(); ++k) {
+        ar.begin_scope();
+        const PartCheck r = apply_part(u, layouts[k], parts[k], sh, has_cache, cache_vals, slab, slab_req, false, s, ar, hc);
+        ar.end_scope();
+        bool same = r.bad == 0;
+        for (uint32_t d = 0; same && d < (uint32_t)r.delta.size(); ++d) same = r.delta[d] == delta[parts[k].t0 + d];
+        if (!same)  // the receiver's weights changed between the passes (another writer)
+            throw DeviceError("a part of the update did not verify when written after the whole update had; the "
+                              "parts before it are written");
+    }
     *changed = C;
 }
 

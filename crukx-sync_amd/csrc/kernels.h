@@ -119,6 +119,7 @@ struct CodeArgs {
     unsigned long long *bstart;     // [blocks + 1] bit offset of each block
     uint64_t n_words;               // words allocated: a workgroup whose bits end past them writes nothing
     unsigned int *overflow;         // |= 2 when that happens
+    uint64_t bit_base;              // payload bit of these changes' first bit (a part of a chunked update)
 };
 
 struct DecodeArgs {

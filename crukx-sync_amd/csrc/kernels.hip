@@ -972,9 +972,9 @@ __global__ __launch_bounds__(256) void k_pack(CodeArgs a) {
     ThreadCodes tc;
     thread_codes(a, rec, wbase, tc);
     const uint64_t t0 = (uint64_t)blockIdx.x * 256, n_thr = (a.n + kElemsPerThread - 1) / kElemsPerThread;
-    const unsigned long long b_lo = a.toff[t0], b_hi = a.toff[min64(t0 + 256, n_thr)];
+    const unsigned long long b_lo = a.bit_base + a.toff[t0], b_hi = a.bit_base + a.toff[min64(t0 + 256, n_thr)];
     const uint64_t w0 = b_lo >> 5, nw = ((b_hi + 31) >> 5) - w0;
-    const unsigned long long off = tc.n ? a.toff[t0 + threadIdx.x] : 0ULL;
+    const unsigned long long off = tc.n ? a.bit_base + a.toff[t0 + threadIdx.x] : 0ULL;
     if (w0 + nw > a.n_words) {  // uniform: the payload was sized from other lengths than these
         if (threadIdx.x == 0) atomicOr(a.overflow, 2u);
         return;

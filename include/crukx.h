@@ -101,9 +101,13 @@ uint64_t crx_update_total_changes(const crx_update *u);
  * after the device's verdict makes the remaining writes if the update verifies, and otherwise puts
  * the old bits back (from the located changes), so later work on `stream` sees either all of the
  * update or none of it.  `targets[i]` is the receiver tensor for update tensor i (crx_update_tensor
- * order) with `numels[i]` elements (below 2^32; the update's changes too: CRX_INVALID otherwise);
- * the tensors must not overlap.  `has_cache[i]`/`cache_vals[i]` give a trusted old checksum (else
- * one is computed from the weights).  `payload_dev` is NULL to upload the payload (and block table)
+ * order) with `numels[i]` elements (below 2^32: CRX_INVALID otherwise); the tensors must not
+ * overlap.  An update of 2^32 or more changes is applied part by part, consecutive tensors of at
+ * most 2^31 elements (a larger tensor alone) per part: every part is first verified without
+ * writing anything, the verdict is taken on the whole update, then the parts are written one after
+ * another (each verified again as it is; should that fail, because the weights changed between the
+ * passes, CRX_DEVICE reports it with the parts before it written).  `has_cache[i]`/`cache_vals[i]`
+ * give a trusted old checksum (else one is computed from the weights).  `payload_dev` is NULL to upload the payload (and block table)
  * from the parsed host bytes, or the address of the payload inside a device-resident copy of the
  * whole update (the block table, which precedes the payload, is read from there too).  On
  * CRX_INVALID and CRX_NOMEM nothing is written; on CRX_CORRUPT the weights end as they were (for a
@@ -139,7 +143,13 @@ uint64_t crx_apply_hist_words(uint64_t numel, int32_t slab);
  * gaps and residuals, per-group Rice parameters, one canonical Huffman table per exponent, bit
  * packing and the block table.  Tensors in caller order; `has_cache`/`cache_vals` give the
  * sender's cached checksum of old (new checksum = cache + delta), else the checksum of new is
- * computed in full.  Fails with CRX_INVALID if a block reaches 2^32 bits (codec.py:417-419). */
+ * computed in full.  Fails with CRX_INVALID if a block reaches 2^32 bits (codec.py:417-419).  An update
+ * of 2^32 or more changes is encoded part by part, as the reference packs batches of changes
+ * (codec.py:214,337-341,394-410): consecutive tensors of at most 2^31 elements per part, each ranked
+ * once for the symbol counts of the whole update's tables and again to be coded at its bit offset in
+ * the one payload; the bytes are those of a single pass.  The environment variable
+ * CRX_PART_ELEMENTS (a positive element count) makes encode and apply split every update larger than
+ * it into parts of that size, so that the part-wise path can be tested at small sizes. */
 int32_t crx_encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news, const uint64_t *numels,
                    const int32_t *has_cache, const uint64_t *cache_vals, int32_t slab, void *stream,
                    crx_alloc_fn alloc, void *alloc_ctx, crx_encoded **out, char *err, uint64_t errlen);

@@ -122,85 +122,21 @@ def scenario_parity() -> None:
         print(f"parity {name}: {len(upd)} bytes", flush=True)
 
 
-def scenario_small4_flips(first: int = 0, count: int = -1, every: int = 1) -> None:
-    """The four-tensor exhaustive corruption sequence of tests/test_full_sizes.py, on the model: the
-    same weights (seed 7), steps, caches, device-resident update and flips in the same order.  Flips
-    [first, first + count) of the list are applied (every `every`-th), starting from the warm state."""
-    import random
+def scenario_small4_flips(first: int = 0, count: int = -1, every: int = 1, widened: int = 0) -> None:
+    """The four-tensor exhaustive corruption sequences of tests/test_full_sizes.py (tests/corruption.py),
+    on the model: the same weights, steps, caches, device-resident update and flips in the same order.
+    Flips [first, first + count) of the list are applied (every `every`-th; SMALL4_LIST: an explicit
+    list of flip indices), starting from the warm state.  widened=1: the widened sequence, with
+    16,384-element slabs."""
+    import corruption
+    from crukx_sync import codec
 
-    import torch
-
-    import crukx_sync
-    from crukx_sync import CorruptUpdate, _native, wire, workloads
-
-    def equal(x, y):
-        return all(torch.equal(x[k].view(torch.int16), y[k].view(torch.int16)) for k in x)
-
-    def varint_len(v):
-        n = 1
-        while v >= 0x80:
-            v >>= 7
-            n += 1
-        return n
-
-    shapes = workloads.small4_shapes()
-    p0 = workloads.make_weights(shapes, seed=7, device="cpu")
-    p1 = workloads.make_step(p0, 1, rho=0.01, seed=7)
-    p2 = workloads.make_step(p1, 2, rho=0.01, seed=7)
-    send, rc = {}, {}
-    recv = {k: v.clone() for k, v in p0.items()}
-    crukx_sync.apply_update(recv, crukx_sync.encode_update_device(p0, p1, send), rc)
-    assert equal(recv, p1)
-    chk1 = {k: v[0] for k, v in rc.items()}
-    buf = crukx_sync.encode_update_device(p1, p2, send)
-    u, L = wire.parse(buf), _native.lib()
-    n_blocks = L.crx_update_n_blocks(u.handle)
-    pay, pay_len = L.crx_update_payload_offset(u.handle), L.crx_update_payload_len(u.handle)
-    bt = pay - varint_len(pay_len) - 4 * n_blocks
-    del u
-    rnd = random.Random(11)
-    offsets = list(range(bt))
-    for b in range(n_blocks):
-        offsets += [bt + 4 * b, bt + 4 * b + 3]
-    offsets += list(range(bt + 4 * n_blocks, pay))
-    offsets += [pay, pay + pay_len - 1] + rnd.sample(range(pay + 1, pay + pay_len - 1), 10_000)
-    print(f"small4: {len(offsets)} flips ({bt} header bytes, {n_blocks} blocks, {pay_len} payload bytes)", flush=True)
-    end = len(offsets) if count < 0 else min(len(offsets), first + count)
-    verbose = bool(os.environ.get("SMALL4_VERBOSE"))
-    rejected = applied = 0
-    order = range(first, end, every)
-    if os.environ.get("SMALL4_LIST"):  # an explicit list of flip indices
-        order = [int(v) for v in os.environ["SMALL4_LIST"].split(",")]
-        end = max(order) + 1
-    for j in order:
-        i = offsets[j]
-        x = (0x01, 0x80, 0xFF)[j % 3]
-        if verbose:
-            print(f"small4: flip {j}: byte {i} ^ {x:#x}", flush=True)
-        buf[i:i + 1].bitwise_xor_(x)
-        try:
-            crukx_sync.apply_update(recv, buf, rc)
-        except (CorruptUpdate, ValueError) as e:
-            rejected += 1
-            if verbose:
-                print(f"small4:   {type(e).__name__}: {e}", flush=True)
-        else:
-            applied += 1
-            assert equal(recv, p2), (i, x)
-            for k in recv:
-                recv[k].copy_(p1[k])
-            rc.update({k: (chk1[k], recv[k]._version) for k in recv})
-        buf[i:i + 1].bitwise_xor_(x)
-        assert equal(recv, p1), f"a write after the flip of byte {i} by {x:#x} (flip {j})"
-        if verbose:
-            import hashlib
-            print(f"small4:   update bytes {hashlib.sha1(buf.numpy().tobytes()).hexdigest()[:12]}", flush=True)
-        if verbose or (j - first) % (50 * every) == 0 or j + every >= end:
-            print(f"small4: flip {j} (byte {i} ^ {x:#x}): {rejected} rejected, {applied} applied", flush=True)
-    crukx_sync.apply_update(recv, buf, rc)
-    assert equal(recv, p2)
-    assert send == {k: v[0] for k, v in rc.items()}
-    print(f"small4 done: flips {first}..{end}: {rejected} rejected, {applied} applied", flush=True)
+    if widened:
+        codec._SLAB = 1 << 14
+    only = [int(v) for v in os.environ["SMALL4_LIST"].split(",")] if os.environ.get("SMALL4_LIST") else None
+    rejected, applied = corruption.run("cpu", bool(widened), lambda m: print(m, flush=True), first, count, every,
+                                       check_every=1, verbose=bool(os.environ.get("SMALL4_VERBOSE")), only=only)
+    print(f"small4 done: {rejected} rejected, {applied} applied", flush=True)
 
 
 def scenario_rejected_early() -> None:
@@ -289,8 +225,62 @@ def scenario_group_message() -> None:
     print(f"group message: {msgs}", flush=True)
 
 
+def scenario_parts() -> None:
+    """The part-wise encode and apply (CRX_PART_ELEMENTS=60000: parts of one to three tensors) on the
+    multi-tensor scenarios: the bytes equal the oracle's single-pass bytes (also with the sender's
+    checksum cache), two chained applies with both caches are exact (the receiver's exponent counts kept
+    part by part), and a corruption in the last part is rejected with every tensor unchanged (the
+    verdict is taken on the whole update before any part is written)."""
+    import torch
+
+    import crukx_sync
+    import oracle
+    import scenarios
+    from crukx_sync import CorruptUpdate
+
+    def equal(x, y):
+        return all(torch.equal(x[k].view(torch.int16), y[k].view(torch.int16)) for k in y)
+
+    os.environ["CRX_PART_ELEMENTS"] = "60000"
+    sc = scenarios.single_scenarios()
+    for name in ("many_tensors", "three_tensors"):
+        old, new = sc[name]
+        ref = oracle.encode_update(old, new)
+        assert crukx_sync.encode_update(old, new) == ref, name
+        assert bytes(crukx_sync.encode_update_device(old, new).numpy()) == ref, name
+        send, rc = {}, {}
+        w = {k: v.clone() for k, v in old.items()}
+        crukx_sync.apply_update(w, crukx_sync.encode_update(old, new, send), rc)
+        assert equal(w, new), name
+        chk = dict(send)
+        back = crukx_sync.encode_update(new, old, send)
+        assert back == oracle.encode_update(new, old, dict(chk)), name
+        # bytes near the payload's end (blocks of the last part), until one that parses is rejected by
+        # the device passes
+        found = None
+        for k in range(2, 40):
+            bad = bytearray(back)
+            bad[-k] ^= 0x10
+            try:
+                crukx_sync.apply_update(w, bytes(bad), rc)
+            except CorruptUpdate as e:
+                if "verify" in str(e) or "outside" in str(e):
+                    found = (k, str(e))
+            else:
+                raise AssertionError(f"{name}: a corrupted update applied")
+            assert equal(w, new), (name, k)
+            if found:
+                break
+        assert found, name
+        print(f"parts {name}: byte -{found[0]} flipped, rejected by the device passes ({found[1]})", flush=True)
+        crukx_sync.apply_update(w, back, rc)
+        assert equal(w, old), name
+        assert send == {k: v[0] for k, v in rc.items()}, name
+        print(f"parts {name}: {len(ref)} bytes as the oracle's; chained applies exact", flush=True)
+
+
 SCENARIOS = {"parity": scenario_parity, "small4_flips": scenario_small4_flips, "rejected_early": scenario_rejected_early,
-             "group_message": scenario_group_message}
+             "group_message": scenario_group_message, "parts": scenario_parts}
 
 if __name__ == "__main__":
     install()

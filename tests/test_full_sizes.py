@@ -7,7 +7,8 @@ size-independent properties are checked:
 - the change-density / step-size sweep (rho in {0.5, 1, 2, 3}%, P(|k| = 1) in {0.95, 0.87, 0.70});
 - the 7B shape at rho = 1% and 2% over two chained steps;
 - the four-tensor case: single-byte flips of every header byte, every block-table entry and 10,000
-  payload bytes, each raising with the receiver unchanged or applying exactly;
+  payload bytes, each raising with the receiver unchanged or applying exactly; again with small
+  slabs, slabs of several windows, an LDS-overflowing dense patch and flips inside those blocks;
 - 32B shape with edge values (+-0, subnormals, +-max-finite) injected at 1e-4 density and smaller
   slabs: single-byte corruptions across the header, the block table and the payload either raise
   with the receiver unchanged or (if the flip happens to be harmless) apply exactly.
@@ -18,6 +19,7 @@ import random
 import pytest
 import torch
 
+import corruption
 import crukx_sync
 from crukx_sync import CorruptUpdate, _native, codec, wire, workloads
 
@@ -111,6 +113,51 @@ def test_qwen25_7b_chained(rho):
     assert send["lm_head.weight"] == codec.checksum(prev["lm_head.weight"])
 
 
+def test_update_of_more_than_2_32_changes():
+    """Three tensors of 1.6e9 weights and one of 100,000, 97% of their elements changed by +-1 or +-2
+    in their bit patterns: 4.66e9 changes, more than 2^32, so encode and apply go part by part (one
+    tensor per part for the large ones).  The header counts each tensor's changes as torch counts them,
+    a byte flipped in the last part's payload is rejected with every tensor unchanged (the first part
+    included), and the update applies exactly, with both checksum caches equal to full checksums."""
+    shapes = [(n, (1_600_000_000,), "linear") for n in ("a", "b", "c")] + [("d", (100_000,), "norm")]
+    old = workloads.make_weights(shapes, seed=3, device="cuda")
+    new, want = {}, {}
+    g = torch.Generator(device="cuda").manual_seed(5)
+    for k, t in old.items():
+        r = torch.randint(0, 100, t.shape, generator=g, device="cuda", dtype=torch.int16)
+        d = torch.where(r < 3, 0, (1 + (r & 1)) * (1 - 2 * ((r >> 1) & 1))).to(torch.int16)
+        del r
+        want[k] = int((d != 0).sum())
+        new[k] = (t.view(torch.int16) + d).view(torch.bfloat16)
+        del d
+    total = sum(want.values())
+    assert total > 1 << 32
+    _say(f"2^32+: {total:,} changes")
+    send, rc = {}, {}
+    upd = crukx_sync.encode_update_device(old, new, send)
+    u = wire.parse(upd)
+    assert u.total_changes == total
+    assert {t.name: sum(g.count for g in t.groups) for t in u.tensors} == want
+    del u
+    _say(f"2^32+: {upd.numel():,} bytes")
+    recv = {k: v.clone() for k, v in old.items()}
+    rejected = 0
+    for k in (2, 3, 5):  # bytes near the payload's end: blocks of the last part
+        upd[-k:upd.numel() - k + 1].bitwise_xor_(0x10)
+        try:
+            crukx_sync.apply_update(recv, upd, rc)
+        except CorruptUpdate:
+            rejected += 1
+        upd[-k:upd.numel() - k + 1].bitwise_xor_(0x10)
+        assert _equal(recv, old), k
+    assert rejected == 3
+    _say("2^32+: corrupted updates rejected, receiver unchanged")
+    crukx_sync.apply_update(recv, upd, rc)
+    assert _equal(recv, new)
+    assert send == {k: v[0] for k, v in rc.items()}
+    assert all(send[k] == codec.checksum(new[k]) for k in new)
+
+
 def test_qwen25_32b_edge_values_and_corruptions(monkeypatch):
     """The 32B shape (771 tensors, 65.5 GB per copy) with edge values in both states and 16K-weight
     slabs.  A first update warms the receiver's caches; then single-byte flips of the second update
@@ -170,54 +217,19 @@ def test_qwen25_32b_edge_values_and_corruptions(monkeypatch):
     assert send == {k: v[0] for k, v in rc.items()}
 
 
-@pytest.mark.skip(reason="the first GPU run that held this test faulted the GPU, and its log was lost with the "
-                         "box; a bounds-checked CPU emulation of the decoder and the local-index pass over the "
-                         "same flips of a CPU-made update found no out-of-bounds access; kept off the GPU until "
-                         "a cause is shown")
 def test_small4_every_header_byte_every_block_boundary_and_10k_payload_flips():
     """The four-tensor case (26.6M weights, receiver caches warm): single-byte flips of every header
     byte, both ends of every block-table entry, the payload length and 10,000 random payload bytes.
     Each flip either raises with the receiver unchanged or (a harmless flip) applies exactly."""
-    shapes = workloads.small4_shapes()
-    p0 = workloads.make_weights(shapes, seed=7, device="cuda")
-    p1 = workloads.make_step(p0, 1, rho=0.01, seed=7)
-    p2 = workloads.make_step(p1, 2, rho=0.01, seed=7)
-    send, rc = {}, {}
-    recv = {k: v.clone() for k, v in p0.items()}
-    crukx_sync.apply_update(recv, crukx_sync.encode_update_device(p0, p1, send), rc)
-    assert _equal(recv, p1)
-    chk1 = {k: v[0] for k, v in rc.items()}
-    buf = crukx_sync.encode_update_device(p1, p2, send)
-    u, L = wire.parse(buf), _native.lib()
-    n_blocks = L.crx_update_n_blocks(u.handle)
-    pay, pay_len = L.crx_update_payload_offset(u.handle), L.crx_update_payload_len(u.handle)
-    bt = pay - _varint_len(pay_len) - 4 * n_blocks
-    del u
-    rnd = random.Random(11)
-    offsets = list(range(bt))                                                       # header
-    for b in range(n_blocks):                                                       # block table
-        offsets += [bt + 4 * b, bt + 4 * b + 3]
-    offsets += list(range(bt + 4 * n_blocks, pay))                                  # payload_len
-    offsets += [pay, pay + pay_len - 1] + rnd.sample(range(pay + 1, pay + pay_len - 1), 10_000)
-    _say(f"small4: {len(offsets)} flips ({bt} header bytes, {n_blocks} blocks, {pay_len} payload bytes)")
-    rejected = 0
-    for j, i in enumerate(offsets):
-        x = (0x01, 0x80, 0xFF)[j % 3]
-        buf[i:i + 1].bitwise_xor_(x)
-        try:
-            crukx_sync.apply_update(recv, buf, rc)
-        except (CorruptUpdate, ValueError):
-            rejected += 1
-        else:  # a harmless flip: the result must be exact; start over from the old state
-            assert _equal(recv, p2), (i, x)
-            for k in recv:
-                recv[k].copy_(p1[k])
-            rc.update({k: (chk1[k], recv[k]._version) for k in recv})
-        buf[i:i + 1].bitwise_xor_(x)
-        if j % 500 == 499 or j == len(offsets) - 1:
-            assert _equal(recv, p1), f"a write after one of the flips at offsets {offsets[j - 499:j + 1]}"
-            _say(f"small4: {j + 1} flips, {rejected} rejected")
-    assert rejected >= 0.9 * len(offsets)
-    crukx_sync.apply_update(recv, buf, rc)
-    assert _equal(recv, p2)
-    assert send == {k: v[0] for k, v in rc.items()}
+    rejected, applied = corruption.run("cuda", False, _say)
+    assert rejected >= 0.9 * (rejected + applied)
+
+
+def test_small4_widened_flips_with_small_slabs(monkeypatch):
+    """The same flips with 16,384-element slabs (every tensor takes the group-size check; many slabs
+    per tensor), edge values whose exponent-0 changes put slabs across several 64-exponent windows, a
+    dense patch whose windows overflow the select pass's LDS list, the receiver's caches warm, and
+    2,000 more payload flips inside the blocks of those slabs."""
+    monkeypatch.setattr(codec, "_SLAB", 1 << 14)
+    rejected, applied = corruption.run("cuda", True, _say)
+    assert rejected >= 0.9 * (rejected + applied)

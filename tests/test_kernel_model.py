@@ -60,3 +60,11 @@ def test_updates_rejected_by_the_decoder_write_nothing(model):
 def test_group_size_check_follows_the_slab_knob(model):
     out = _run(model, "group_message")
     assert "group has more changes than elements" in out
+
+
+def test_part_wise_encode_and_apply_match_the_oracle(model):
+    """CRX_PART_ELEMENTS splits updates into parts of one to three tensors: the bytes are the oracle's
+    single-pass bytes, chained applies with both caches are exact, and a corruption in the last part is
+    rejected by the verification of the whole update with every tensor unchanged."""
+    out = _run(model, "parts")
+    assert out.count("chained applies exact") == 2 and out.count("rejected by the device passes") == 2
