@@ -1214,7 +1214,7 @@ uint32_t apply_slab(int32_t slab_req) { return slab_size(slab_req); }
 // each block's first payload bit.
 struct ApplyShared {
     uint32_t *lim = nullptr, *off = nullptr, *syms = nullptr;
-    uint32_t n_syms = 0;
+    uint32_t n_syms = 0, n_tables = 0;
     uint64_t *pay = nullptr;
     uint64_t pay_words = 0;
     uint32_t *bb = nullptr;            // [blocks] bits of each block
@@ -1270,7 +1270,7 @@ PartCheck apply_part(const Update &u, const Layout &L, const ApplyPart &P, const
     hc.mark("apply_upload");
     Fork fork(s);
     DecodeArgs da{d_descs, sh.pay, sh.pay_words, sh.bb + P.b0, sh.boff + P.b0, B, d_groups, (uint32_t)G, bmap,
-                  sh.lim, sh.off, sh.syms, sh.n_syms, dz, blk_sum, bad};
+                  sh.lim, sh.off, sh.syms, sh.n_syms, dz, blk_sum, bad, sh.n_tables};
     launch_decode(da, fork.aux);
     launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), fork.aux);
 
@@ -1488,6 +1488,7 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     sh.off = ar.get<uint32_t>(off.size());
     sh.syms = ar.get<uint32_t>(syms.size());
     sh.n_syms = (uint32_t)syms.size();
+    sh.n_tables = (uint32_t)(lim.size() / 17);
     h2d(sh.lim, lim.data(), lim.size(), s);
     h2d(sh.off, off.data(), off.size(), s);
     h2d(sh.syms, syms.data(), syms.size(), s);

@@ -139,6 +139,7 @@ struct DecodeArgs {
     unsigned long long *dz;         // [changes] zz | (block-relative local index << 32)
     unsigned long long *blk_sum;    // [blocks] sum of (gap + 1) per block
     unsigned int *bad;
+    uint32_t n_tables;              // tables: lim and off hold 17 entries each
 };
 
 struct SelectArgs {
@@ -238,9 +239,9 @@ void launch_verdict(uint32_t n, const unsigned long long *delta, const uint64_t 
 void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint64_t *per_tile, uint64_t *out,
                         hipStream_t s);
 void launch_decode(const DecodeArgs &a, hipStream_t s);
-constexpr uint32_t kDecSyms = 2048;  // decoding symbols staged in LDS when they fit
+constexpr uint32_t kDecSyms = 2048;  // decoding symbols staged in LDS when they fit (with the first indices)
 // Dynamic LDS of the decoder for n_syms symbols.
-inline uint32_t decode_lds_bytes(uint32_t n_syms) { return n_syms <= kDecSyms ? n_syms * 4u : 0u; }
+inline uint32_t decode_lds_bytes(uint32_t n_syms, uint32_t n_tables) { return n_syms <= kDecSyms ? (n_syms + 17u * n_tables) * 4u : 0u; }
 void launch_local_fix(const BlockArgs &a, uint64_t n_blocks, hipStream_t s);
 void launch_locate(const SelectArgs &a, uint32_t tiles, hipStream_t s);
 // tile_tensor[tile] = tensor of every slab of the layout

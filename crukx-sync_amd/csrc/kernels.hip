@@ -1116,14 +1116,18 @@ __global__ __launch_bounds__(256) void k_sum_parts(const unsigned long long *par
 
 // ================================================================== apply: block decode
 // One lane per 256-change block (codec.py:504-575), 64 consecutive blocks per wavefront.  Each lane
-// reads its block's payload bits from HBM (BitReader below); the decoding symbols are staged in LDS
-// when they fit.  A change normally costs one 64-bit window of the stream (unary run, remainder and
-// Huffman peek together) and one LDS read of its symbol; code lengths come from comparisons of the 17-bit peek with the canonical limits
-// held in registers.  The decoder does not read the receiver's weights or counts (positions are
+// reads its block's payload bits from HBM (BitReader below); the decoding symbols and each table's
+// symbol index of the first code of every length are staged in LDS when they fit.  A change normally
+// costs one 64-bit window of the stream (unary run, remainder and Huffman peek together) and two LDS
+// reads (its length's first index, then its symbol); code lengths come from comparisons of the 17-bit
+// peek with the canonical limits held in registers (the first indices in registers as well took 17
+// more registers and a select tree per change: 0.63 ms against 0.56 with them in LDS and 16 changes
+// per store burst).  The decoder does not read the receiver's weights or counts (positions are
 // checked against those by k_local_fix), so it can run beside the exponent-count pass.  Each lane
 // keeps kDecBuf decoded changes in registers and stores them together: storing one change at a time
-// left each lane's output lines half-written in L2, and they reached HBM several times over.
-constexpr uint32_t kDecBuf = 8;          // changes decoded per lane between stores
+// left each lane's output lines half-written in L2, and they reached HBM several times over; 16 at a
+// time (128 bytes) also spaces out the stores that the next payload load waits behind.
+constexpr uint32_t kDecBuf = 16;         // changes decoded per lane between stores
 
 // A lane's reader of its block's bits: the two 64-bit words around the read position in registers
 // (hi, lo) and the next one already loading (nx), so each word's load has the decoding of the 64 bits
@@ -1174,7 +1178,7 @@ __device__ void decode_blocks(const DecodeArgs &a, const uint32_t *S_syms) {
     const uint32_t ln = lane();
     const uint64_t b = (uint64_t)blockIdx.x * 64 + ln;
     if (b >= a.n_blocks) return;
-    uint32_t lim[17], off[17];
+    uint32_t lim[17];
     const uint32_t g = a.bmap[b];
     const GroupDev gr = a.groups[g];
     const uint64_t kb = b - gr.blk_base;
@@ -1193,7 +1197,6 @@ __device__ void decode_blocks(const DecodeArgs &a, const uint32_t *S_syms) {
 #pragma unroll
     for (int l = 0; l < 17; ++l) {
         lim[l] = a.lim[(uint64_t)gr.table * 17 + l];
-        off[l] = a.off[(uint64_t)gr.table * 17 + l];
     }
     uint64_t rel = 0;  // sum of (gap + 1) so far in this block
     // decodes change s of the block into out: zz | (block-relative local << 32); false once bad
@@ -1229,15 +1232,10 @@ __device__ void decode_blocks(const DecodeArgs &a, const uint32_t *S_syms) {
         for (int w = 1; w < 17; w <<= 1)
 #pragma unroll
             for (int l = 0; l + w < 17; l += 2 * w) t[l] += t[l + w];
-        const uint32_t L = 1 + t[0], li = L - 1;
-        uint32_t o[17];
-#pragma unroll
-        for (int l = 0; l < 17; ++l) o[l] = off[l];
-#pragma unroll
-        for (int w = 1; w < 17; w <<= 1)
-#pragma unroll
-            for (int l = 0; l + w < 17; l += 2 * w) o[l] = (li & w) ? o[l + w] : o[l];
-        const uint32_t idx = o[0] + (L <= 17 ? peek >> (17 - L) : 0u);
+        const uint32_t L = 1 + t[0], li = min(L - 1, 16u);
+        const uint32_t oi = gr.table * 17 + li;
+        const uint32_t o0 = LDS_SYMS ? S_syms[a.n_syms + oi] : a.off[oi];
+        const uint32_t idx = o0 + (L <= 17 ? peek >> (17 - L) : 0u);
         const uint64_t gap = (q << rice) | rem;
         if (q > qmax || cur + q >= end || L > 17 || gap >= size) {
             bad = true;  // positions past the group's exponent count are caught by k_local_fix
@@ -1274,10 +1272,12 @@ __device__ void decode_blocks(const DecodeArgs &a, const uint32_t *S_syms) {
 
 template <bool LDS_SYMS>
 __global__ __launch_bounds__(64) void k_decode(DecodeArgs a) {
-    CRX_DYNAMIC_LDS(uint32_t, dyn_lds);  // the symbols, when they fit
+    CRX_DYNAMIC_LDS(uint32_t, dyn_lds);  // the symbols, then the tables' first indices, when they fit
     const uint32_t ln = lane();
-    if (LDS_SYMS)
+    if (LDS_SYMS) {
         for (uint32_t i = ln; i < a.n_syms; i += 64) dyn_lds[i] = a.syms[i];
+        for (uint32_t i = ln; i < 17 * a.n_tables; i += 64) dyn_lds[a.n_syms + i] = a.off[i];
+    }
     wave_fence();
     decode_blocks<LDS_SYMS>(a, dyn_lds);
 }
@@ -2121,7 +2121,7 @@ void launch_tensor_sums(const TensorDesc *descs, uint32_t n_tensors, const uint6
 }
 
 void launch_decode(const DecodeArgs &a, hipStream_t s) {
-    const uint32_t grid = grid1(a.n_blocks, 64), lds = decode_lds_bytes(a.n_syms);
+    const uint32_t grid = grid1(a.n_blocks, 64), lds = decode_lds_bytes(a.n_syms, a.n_tables);
     if (!grid) return;
     timing_begin("decode", s);
     if (a.n_syms <= kDecSyms) hipLaunchKernelGGL(k_decode<true>, dim3(grid), dim3(64), lds, s, a);
