@@ -327,7 +327,7 @@ struct Arena {
     uint64_t total = 0;  // bytes handed out by get()
     // Scoped buffers (the parts of a chunked update, one after another): within a scope every buffer is
     // an allocation of its own, and at its end they become spares that the next scope's buffers reuse
-    // (the first spare large enough).  A scope ends only once the device is done with its buffers.
+    // (the smallest spare large enough).  A scope ends only once the device is done with its buffers.
     bool scoped = false;
     std::vector<std::pair<void *, uint64_t>> live, spare;
 
@@ -349,12 +349,14 @@ struct Arena {
         }
         bytes = (std::max<uint64_t>(bytes, 1) + 255) & ~uint64_t(255);
         total += bytes;
+        size_t best = spare.size();
         for (size_t i = 0; i < spare.size(); ++i)
-            if (spare[i].second >= bytes) {
-                live.push_back(spare[i]);
-                spare.erase(spare.begin() + (ptrdiff_t)i);
-                return live.back().first;
-            }
+            if (spare[i].second >= bytes && (best == spare.size() || spare[i].second < spare[best].second)) best = i;
+        if (best < spare.size()) {
+            live.push_back(spare[best]);
+            spare.erase(spare.begin() + (ptrdiff_t)best);
+            return live.back().first;
+        }
         live.emplace_back(raw(bytes), bytes);
         return live.back().first;
     }
@@ -1321,9 +1323,10 @@ PartCheck apply_part(const Update &u, const Layout &L, const ApplyPart &P, const
     uint32_t *done = ar.get<uint32_t>(tiles);
     // the verdict's inputs, set up before the select pass writes anything: between its writes and the
     // commit that can undo them, the host only launches
-    uint64_t *d_want = nullptr, *d_cached = nullptr;
-    int32_t *d_has = nullptr;
-    unsigned int *ok = nullptr;
+    // (allocated in a dry pass too: a part's write pass then asks for exactly the buffers its dry pass had)
+    uint64_t *d_want = ar.get<uint64_t>(T), *d_cached = ar.get<uint64_t>(T);
+    int32_t *d_has = ar.get<int32_t>(T);
+    unsigned int *ok = ar.get<unsigned int>(1);
     if (!dry) {
         std::vector<uint64_t> want(T), cached(T, 0);
         std::vector<int32_t> has(T, 0);
@@ -1333,10 +1336,6 @@ PartCheck apply_part(const Update &u, const Layout &L, const ApplyPart &P, const
             has[d] = (has_cache && has_cache[t]) ? 1 : 0;
             if (has[d]) cached[d] = cache_vals[t];
         }
-        d_want = ar.get<uint64_t>(T);
-        d_cached = ar.get<uint64_t>(T);
-        d_has = ar.get<int32_t>(T);
-        ok = ar.get<unsigned int>(1);
         h2d(d_want, want.data(), T, s);
         h2d(d_cached, cached.data(), T, s);
         h2d(d_has, has.data(), T, s);
@@ -1537,7 +1536,13 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     raise_verdict(u, bad, delta, full, has_cache, cache_vals);
     for (size_t k = 0; k < parts.size(); ++k) {
         ar.begin_scope();
-        const PartCheck r = apply_part(u, layouts[k], parts[k], sh, has_cache, cache_vals, slab, slab_req, false, s, ar, hc);
+        PartCheck r;
+        try {
+            r = apply_part(u, layouts[k], parts[k], sh, has_cache, cache_vals, slab, slab_req, false, s, ar, hc);
+        } catch (const std::bad_alloc &) {
+            if (!k) throw;  // nothing written yet
+            throw DeviceError("out of memory while writing a part of the update; the parts before it are written");
+        }
         ar.end_scope();
         bool same = r.bad == 0;
         for (uint32_t d = 0; same && d < (uint32_t)r.delta.size(); ++d) same = r.delta[d] == delta[parts[k].t0 + d];

@@ -106,10 +106,11 @@ uint64_t crx_update_total_changes(const crx_update *u);
  * most 2^31 elements (a larger tensor alone) per part: every part is first verified without
  * writing anything, the verdict is taken on the whole update, then the parts are written one after
  * another (each verified again as it is; should that fail, because the weights changed between the
- * passes, CRX_DEVICE reports it with the parts before it written).  `has_cache[i]`/`cache_vals[i]`
- * give a trusted old checksum (else one is computed from the weights).  `payload_dev` is NULL to upload the payload (and block table)
- * from the parsed host bytes, or the address of the payload inside a device-resident copy of the
- * whole update (the block table, which precedes the payload, is read from there too).  On
+ * passes, or device memory runs out after the first part is written, CRX_DEVICE reports it with the
+ * parts before it written).  `has_cache[i]`/`cache_vals[i]` give a trusted old checksum (else one is
+ * computed from the weights).  `payload_dev` is NULL to upload the payload (and block table) from
+ * the parsed host bytes, or the address of the payload inside a device-resident copy of the whole
+ * update (the block table, which precedes the payload, is read from there too).  On
  * CRX_INVALID and CRX_NOMEM nothing is written; on CRX_CORRUPT the weights end as they were (for a
  * checksum mismatch, after the undo enqueued on `stream`); on CRX_OK the remaining writes are
  * enqueued on `stream`.  CRX_DEVICE (a HIP runtime error) leaves the weights unspecified: some writes
