@@ -504,6 +504,40 @@ void sync(hipStream_t s) {
     t_stage.finish();
 }
 
+// Small uploads issued as one copy: add() places each host array in one pinned range and its device
+// buffer at the same offset of one allocation (each copy issued costs the device several microseconds
+// between kernels, and the host a runtime call).  at<T>(i) is item i's device address after commit().
+struct UploadBatch {
+    struct Item {
+        const void *src;  // nullptr: zeros
+        uint64_t off, bytes;
+    };
+    std::vector<Item> items;
+    uint64_t total = 0;
+    uint8_t *dev = nullptr;
+
+    template <typename T>
+    size_t add(const T *src, uint64_t n) {
+        items.push_back({src, total, n * sizeof(T)});
+        total += (std::max<uint64_t>(n * sizeof(T), 1) + 255) & ~uint64_t(255);
+        return items.size() - 1;
+    }
+    template <typename T>
+    size_t add_zeros(uint64_t n) { return add(static_cast<const T *>(nullptr), n); }
+    void commit(Arena &ar, hipStream_t s) {
+        dev = ar.get<uint8_t>(total);
+        uint8_t *p = t_stage.get(total);
+        for (const Item &it : items) {
+            if (it.src) std::memcpy(p + it.off, it.src, it.bytes);
+            else std::memset(p + it.off, 0, it.bytes);
+        }
+        HIP_OK(hipMemcpyAsync(dev, p, total, hipMemcpyHostToDevice, s));
+        t_stage.copied(s);
+    }
+    template <typename T>
+    T *at(size_t i) const { return reinterpret_cast<T *>(dev + items[i].off); }
+};
+
 // The caller's `slab` is the reference's _SLAB (codec.py:30): tensors of more elements get the exact
 // group-size check before decoding (codec.py:598-604); 0 or less means its default, 2^24.
 uint64_t group_check_numel(int32_t slab) { return slab > 0 ? (uint64_t)slab : (1ULL << 24); }
@@ -563,16 +597,17 @@ struct ScanDev {
     uint32_t *tile_tensor;  // [tiles]
 };
 
-ScanDev upload_scan(Arena &ar, const Layout &L, const TensorDesc *d_descs, hipStream_t s) {
+// The scan's tables on the device, with its chunk list and the tensors' first chunks already uploaded
+// (chunks, tcb); the slab-to-tensor map is built here.
+ScanDev scan_buffers(Arena &ar, const Layout &L, const TensorDesc *d_descs, ScanChunk *chunks, uint32_t *tcb,
+                     hipStream_t s) {
     ScanDev sd;
     sd.tile_tensor = ar.get<uint32_t>(L.tiles);
     launch_tile_map(d_descs, (uint32_t)L.descs.size(), sd.tile_tensor, s);
     sd.n_chunks = (uint32_t)L.chunks.size();
-    sd.chunks = ar.get<ScanChunk>(sd.n_chunks);
-    sd.tcb = ar.get<uint32_t>(L.tensor_chunk_begin.size());
+    sd.chunks = chunks;
+    sd.tcb = tcb;
     sd.csum = ar.get<uint32_t>((uint64_t)sd.n_chunks * 256);
-    h2d(sd.chunks, L.chunks.data(), sd.n_chunks, s);
-    h2d(sd.tcb, L.tensor_chunk_begin.data(), L.tensor_chunk_begin.size(), s);
     return sd;
 }
 
@@ -765,13 +800,17 @@ struct Ranked {
 Ranked rank_changes(const Layout &L, uint32_t slab, hipStream_t s, Arena &ar, HostClock *hc, uint64_t stop_at) {
     const uint32_t T = (uint32_t)L.descs.size(), tiles = L.tiles;
     Ranked R;
-    R.d_descs = ar.get<TensorDesc>(T);
-    h2d(R.d_descs, L.descs.data(), T, s);
+    UploadBatch ub;  // the tensors, the scan's chunks and a zeroed overflow flag in one copy
+    const size_t i_descs = ub.add(L.descs.data(), T), i_chunks = ub.add(L.chunks.data(), L.chunks.size()),
+                 i_tcb = ub.add(L.tensor_chunk_begin.data(), L.tensor_chunk_begin.size()),
+                 i_ovf = ub.add_zeros<unsigned int>(1);
+    ub.commit(ar, s);
+    R.d_descs = ub.at<TensorDesc>(i_descs);
     R.hall = ar.get<uint32_t>((uint64_t)tiles * 256);
     R.hchg = ar.get<uint32_t>((uint64_t)tiles * 256);
     R.delta = ar.get<uint64_t>(tiles);
     R.full = ar.get<uint64_t>(tiles);
-    R.sd = upload_scan(ar, L, R.d_descs, s);
+    R.sd = scan_buffers(ar, L, R.d_descs, ub.at<ScanChunk>(i_chunks), ub.at<uint32_t>(i_tcb), s);
     uint32_t *tot_all = ar.get<uint32_t>((uint64_t)T * 256), *tot_chg = ar.get<uint32_t>((uint64_t)T * 256);
     R.d_groups = ar.get<GroupDev>((uint64_t)T * 256);
     R.gbase = ar.get<uint32_t>((uint64_t)T * 256);
@@ -781,8 +820,7 @@ Ranked rank_changes(const Layout &L, uint32_t slab, hipStream_t s, Arena &ar, Ho
     // (+64).  If one overflows, the exact counts of that pass give exact regions for a second pass.
     const uint64_t per_slab = slab / 24 + 64;
     uint32_t *rec_count = ar.get<uint32_t>(tiles);
-    unsigned int *ovf = ar.get<unsigned int>(1);
-    zero(ovf, 1, s);
+    unsigned int *ovf = ub.at<unsigned int>(i_ovf);
     R.a = EncRankArgs{R.d_descs, R.sd.tile_tensor, T, slab, R.hall, R.hchg, ar.get<uint64_t>((uint64_t)tiles * per_slab),
                       nullptr, per_slab, rec_count, ovf, R.delta, R.full};
     launch_enc_rank(R.a, tiles, s);
@@ -1102,38 +1140,42 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     uint32_t *cmap = ar.get<uint32_t>(n_thr);
     launch_chunk_map(d_groups, (uint32_t)G, cmap, s);
     launch_r0(d_groups, (uint32_t)G, sorted, s);
-    uint32_t *dense = ar.get<uint32_t>(256 * kDense);
-    uint32_t *rare = ar.get<uint32_t>(C);
-    unsigned long long *scnt = ar.get<unsigned long long>(2);
-    unsigned long long *cost = ar.get<unsigned long long>(G * 3);
-    uint64_t *t_delta = ar.get<uint64_t>(T), *t_full = ar.get<uint64_t>(T);
-    zero(dense, 256 * kDense, s);
-    zero(scnt, 2, s);
-    zero(cost, G * 3, s);
+    // what the host reads back after the symbol counts, in one block so that one copy brings it (the
+    // first kRareFirst rare symbols with it): cost | dense | scnt | t_delta | t_full | rare
+    const uint64_t o_dense = G * 3 * 8, o_scnt = o_dense + 256 * kDense * 4, o_delta = o_scnt + 16,
+                   o_full = o_delta + 8 * (uint64_t)T, o_rare = o_full + 8 * (uint64_t)T;
+    uint8_t *dl = ar.get<uint8_t>(o_rare + 4 * C);
+    unsigned long long *cost = reinterpret_cast<unsigned long long *>(dl);
+    uint32_t *dense = reinterpret_cast<uint32_t *>(dl + o_dense);
+    unsigned long long *scnt = reinterpret_cast<unsigned long long *>(dl + o_scnt);
+    uint64_t *t_delta = reinterpret_cast<uint64_t *>(dl + o_delta), *t_full = reinterpret_cast<uint64_t *>(dl + o_full);
+    uint32_t *rare = reinterpret_cast<uint32_t *>(dl + o_rare);
+    zero(dl, o_delta, s);  // cost, dense and scnt; the sums are written whole
     StatsArgs st{sorted, C, d_groups, (uint32_t)G, cmap, dense, rare, C, scnt, cost};
     launch_stats(st, s);
     launch_tensor_sums(d_descs, T, delta, t_delta, s);
     launch_tensor_sums(d_descs, T, full, t_full, s);
 
     std::vector<GroupDev> groups(G);
+    d2h(groups.data(), d_groups, G, s);
+    // the first rare symbols in the same wait (an update has few); the rest, if any, after it
+    const uint64_t rare_first = std::min<uint64_t>(C, kRareFirst);
+    std::vector<uint8_t> hdl(o_rare + 4 * rare_first);
+    d2h(hdl.data(), dl, hdl.size(), s);
+    sync(s);
+    hc.mark("enc_wait_stats");
     std::vector<unsigned long long> hcost(G * 3);
     std::vector<uint32_t> hdense(256 * kDense);
     std::vector<uint64_t> hdelta(T), hfull(T);
     unsigned long long hs[2];
-    d2h(groups.data(), d_groups, G, s);
-    d2h(hcost.data(), cost, G * 3, s);
-    d2h(hdense.data(), dense, 256 * kDense, s);
-    d2h(hdelta.data(), t_delta, T, s);
-    d2h(hfull.data(), t_full, T, s);
-    d2h(hs, scnt, 2, s);
-    // the first rare symbols in the same wait (an update has few); the rest, if any, after it
-    const uint64_t rare_first = std::min<uint64_t>(C, kRareFirst);
-    std::vector<uint32_t> hrare(rare_first);
-    d2h(hrare.data(), rare, rare_first, s);
-    sync(s);
-    hc.mark("enc_wait_stats");
+    std::memcpy(hcost.data(), hdl.data(), o_dense);
+    std::memcpy(hdense.data(), hdl.data() + o_dense, 256 * kDense * 4);
+    std::memcpy(hs, hdl.data() + o_scnt, 16);
+    std::memcpy(hdelta.data(), hdl.data() + o_delta, 8 * (uint64_t)T);
+    std::memcpy(hfull.data(), hdl.data() + o_full, 8 * (uint64_t)T);
     if (hs[1]) throw DeviceError("rare symbol list overflowed");
-    hrare.resize(hs[0]);
+    std::vector<uint32_t> hrare(hs[0]);
+    if (hs[0]) std::memcpy(hrare.data(), hdl.data() + o_rare, 4 * std::min<uint64_t>(hs[0], rare_first));
     if (hs[0] > rare_first) {
         d2h(hrare.data() + rare_first, rare + rare_first, hs[0] - rare_first, s);
         sync(s);
@@ -1159,25 +1201,24 @@ void encode(int32_t n, const uint16_t *const *olds, const uint16_t *const *news,
     hc.mark("enc_tables");
 
     // the code lengths, their offsets and the bits, with no wait: the payload's size is known
-    GroupDev *d_groups2 = ar.get<GroupDev>(G);
-    uint32_t *d_lut = ar.get<uint32_t>(256 * kDense);
-    uint32_t *d_rk = ar.get<uint32_t>(rkeys.size()), *d_rv = ar.get<uint32_t>(rvals.size());
-    h2d(d_groups2, groups.data(), G, s);
-    h2d(d_lut, lut.data(), lut.size(), s);
-    h2d(d_rk, rkeys.data(), rkeys.size(), s);
-    h2d(d_rv, rvals.data(), rvals.size(), s);
+    UploadBatch ub;  // the groups with their Rice parameters, the code tables, a zeroed overflow flag
+    const size_t i_groups = ub.add(groups.data(), G), i_lut = ub.add(lut.data(), lut.size()),
+                 i_rk = ub.add(rkeys.data(), rkeys.size()), i_rv = ub.add(rvals.data(), rvals.size()),
+                 i_ovf = ub.add_zeros<unsigned int>(1);
+    ub.commit(ar, s);
+    GroupDev *d_groups2 = ub.at<GroupDev>(i_groups);
+    uint32_t *d_lut = ub.at<uint32_t>(i_lut), *d_rk = ub.at<uint32_t>(i_rk), *d_rv = ub.at<uint32_t>(i_rv);
     unsigned long long *tsum = ar.get<unsigned long long>(n_thr), *toff = ar.get<unsigned long long>(n_thr + 1);
     const uint64_t n_words = (total_bits + 31) / 32 + 4;
     uint32_t *words = ar.get<uint32_t>(n_words);
     unsigned long long *bstart = ar.get<unsigned long long>(B + 1);
     uint32_t *bb = ar.get<uint32_t>(B);
-    unsigned int *bovf = ar.get<unsigned int>(1);
+    unsigned int *bovf = ub.at<unsigned int>(i_ovf);
     CodeArgs ca{sorted, C, d_groups2, (uint32_t)G, d_lut, d_rk, d_rv, (uint32_t)rkeys.size(), cmap, tsum, toff,
                 words, bstart, n_words, bovf};
     launch_code_lengths(ca, s);
     launch_scan_u64(tsum, n_thr, toff, ar.get<unsigned long long>(scan_parts(n_thr)), s);
     zero(words, n_words, s);
-    zero(bovf, 1, s);
     HIP_OK(hipMemcpyAsync(bstart + B, toff + n_thr, sizeof(unsigned long long), hipMemcpyDeviceToDevice, s));
     launch_pack(ca, s);
     launch_block_bits(bstart, B, bb, bovf, s);
@@ -1253,17 +1294,32 @@ PartCheck apply_part(const Update &u, const Layout &L, const ApplyPart &P, const
     std::vector<TensorDesc> descs = L.descs;
     if (dry)
         for (TensorDesc &d : descs) d.hist_out = nullptr;
+    // the verdict's inputs (unused by a dry pass, which uploads them all the same: its write pass then
+    // asks for exactly the buffers the dry pass had)
+    std::vector<uint64_t> want(T), cached(T, 0);
+    std::vector<int32_t> has(T, 0);
+    for (uint32_t d = 0; d < T; ++d) {
+        const uint32_t t = P.t0 + d;
+        want[d] = u.tensors[t].checksum;
+        has[d] = (has_cache && has_cache[t]) ? 1 : 0;
+        if (has[d]) cached[d] = cache_vals[t];
+    }
 
-    // what the decoder needs goes first: it starts while the rest is enqueued
-    TensorDesc *d_descs = ar.get<TensorDesc>(T);
-    h2d(d_descs, descs.data(), T, s);
-    GroupDev *d_groups = ar.get<GroupDev>(G);
-    h2d(d_groups, P.groups.data(), G, s);
+    // every small upload of the part in one copy, ahead of the decoder, which starts at once
+    UploadBatch ub;
+    const size_t i_descs = ub.add(descs.data(), T), i_groups = ub.add(P.groups.data(), G),
+                 i_gof = ub.add(P.group_of.data(), P.group_of.size()), i_tchg = ub.add(tensor_chg.data(), T + 1),
+                 i_chunks = ub.add(L.chunks.data(), L.chunks.size()),
+                 i_tcb = ub.add(L.tensor_chunk_begin.data(), L.tensor_chunk_begin.size()),
+                 i_want = ub.add(want.data(), T), i_cached = ub.add(cached.data(), T), i_has = ub.add(has.data(), T),
+                 i_bad = ub.add_zeros<unsigned int>(1), i_nmore = ub.add_zeros<unsigned int>(1);
+    ub.commit(ar, s);
+    TensorDesc *d_descs = ub.at<TensorDesc>(i_descs);
+    GroupDev *d_groups = ub.at<GroupDev>(i_groups);
+    unsigned int *bad = ub.at<unsigned int>(i_bad);
     uint32_t *bmap = ar.get<uint32_t>(B);
     BlockInfo *binfo = ar.get<BlockInfo>(B);
     launch_block_map(d_groups, (uint32_t)G, bmap, binfo, s);
-    unsigned int *bad = ar.get<unsigned int>(1);
-    zero(bad, 1, s);
 
     // The decoder needs nothing from the receiver's weights: it runs on the auxiliary stream while
     // the main stream takes the exponent counts (pass A) and their scans.
@@ -1278,17 +1334,15 @@ PartCheck apply_part(const Update &u, const Layout &L, const ApplyPart &P, const
 
     uint32_t *hall = ar.get<uint32_t>((uint64_t)tiles * 256);
     uint64_t *full = ar.get<uint64_t>(tiles), *t_full = ar.get<uint64_t>(T);
-    ScanDev sd = upload_scan(ar, L, d_descs, s);
+    ScanDev sd = scan_buffers(ar, L, d_descs, ub.at<ScanChunk>(i_chunks), ub.at<uint32_t>(i_tcb), s);
     uint32_t *sizes = ar.get<uint32_t>((uint64_t)T * 256);
-    int32_t *d_gof = ar.get<int32_t>((uint64_t)T * 256);
-    h2d(d_gof, P.group_of.data(), P.group_of.size(), s);
+    int32_t *d_gof = ub.at<int32_t>(i_gof);
     uint32_t *local = ar.get<uint32_t>(C);
     unsigned long long *rec = ar.get<unsigned long long>(C);  // the select pass's records, slab by slab
     uint32_t *pn = ar.get<uint32_t>(C);                       // offset in the slab | new bits << 16
     uint32_t *rstart = ar.get<uint32_t>((uint64_t)tiles + 1);
     uint64_t *sdelta = ar.get<uint64_t>(tiles), *tdelta = ar.get<uint64_t>(T);
-    uint32_t *tchg = ar.get<uint32_t>(T + 1);
-    h2d(tchg, tensor_chg.data(), T + 1, s);
+    uint32_t *tchg = ub.at<uint32_t>(i_tchg);
     uint32_t *lb = ar.get<uint32_t>((uint64_t)(tiles + 1) * 256);  // row tiles: read, never used
 
     // pass A: slabs of tensors without cached counts are streamed for their counts (and the even rows
@@ -1317,29 +1371,15 @@ PartCheck apply_part(const Update &u, const Layout &L, const ApplyPart &P, const
                  group_check_numel(slab_req)};
     launch_local_fix(ba, B, s);
     uint2 *more = ar.get<uint2>((uint64_t)kSelMoreWindows * tiles);  // windows after the first, per slab
-    unsigned int *n_more = ar.get<unsigned int>(1);
-    zero(n_more, 1, s);
+    unsigned int *n_more = ub.at<unsigned int>(i_nmore);
     uint8_t *multi = ar.get<uint8_t>(tiles);
     uint32_t *done = ar.get<uint32_t>(tiles);
     // the verdict's inputs, set up before the select pass writes anything: between its writes and the
     // commit that can undo them, the host only launches
     // (allocated in a dry pass too: a part's write pass then asks for exactly the buffers its dry pass had)
-    uint64_t *d_want = ar.get<uint64_t>(T), *d_cached = ar.get<uint64_t>(T);
-    int32_t *d_has = ar.get<int32_t>(T);
+    uint64_t *d_want = ub.at<uint64_t>(i_want), *d_cached = ub.at<uint64_t>(i_cached);
+    int32_t *d_has = ub.at<int32_t>(i_has);
     unsigned int *ok = ar.get<unsigned int>(1);
-    if (!dry) {
-        std::vector<uint64_t> want(T), cached(T, 0);
-        std::vector<int32_t> has(T, 0);
-        for (uint32_t d = 0; d < T; ++d) {
-            const uint32_t t = P.t0 + d;
-            want[d] = u.tensors[t].checksum;
-            has[d] = (has_cache && has_cache[t]) ? 1 : 0;
-            if (has[d]) cached[d] = cache_vals[t];
-        }
-        h2d(d_want, want.data(), T, s);
-        h2d(d_cached, cached.data(), T, s);
-        h2d(d_has, has.data(), T, s);
-    }
     SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, rec, rstart, tchg, bad, more,
                   n_more, (uint32_t)std::min<uint64_t>(1024, (uint64_t)kSelMoreWindows * tiles), dz, sdelta, multi,
                   done, (uint32_t)C, full};
@@ -1483,14 +1523,15 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
     hc.mark("apply_tables");
 
     ApplyShared sh;
-    sh.lim = ar.get<uint32_t>(lim.size());
-    sh.off = ar.get<uint32_t>(off.size());
-    sh.syms = ar.get<uint32_t>(syms.size());
+    UploadBatch tb;  // the decoding tables, in one copy
+    const size_t i_lim = tb.add(lim.data(), lim.size()), i_off = tb.add(off.data(), off.size()),
+                 i_syms = tb.add(syms.data(), syms.size());
+    tb.commit(ar, s);
+    sh.lim = tb.at<uint32_t>(i_lim);
+    sh.off = tb.at<uint32_t>(i_off);
+    sh.syms = tb.at<uint32_t>(i_syms);
     sh.n_syms = (uint32_t)syms.size();
     sh.n_tables = (uint32_t)(lim.size() / 17);
-    h2d(sh.lim, lim.data(), lim.size(), s);
-    h2d(sh.off, off.data(), off.size(), s);
-    h2d(sh.syms, syms.data(), syms.size(), s);
     sh.bb = ar.get<uint32_t>(B_all);
     if (payload_dev)  // the update is in device memory: its block table precedes the payload there
         HIP_OK(hipMemcpyAsync(sh.bb, payload_dev - (u.payload_offset - u.block_table_offset), 4 * B_all,

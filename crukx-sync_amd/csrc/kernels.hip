@@ -1128,6 +1128,28 @@ __global__ __launch_bounds__(256) void k_sum_parts(const unsigned long long *par
 // left each lane's output lines half-written in L2, and they reached HBM several times over; 16 at a
 // time (128 bytes) also spaces out the stores that the next payload load waits behind.
 constexpr uint32_t kDecBuf = 16;         // changes decoded per lane between stores
+// s_waitcnt operand (gfx9 encoding) that waits for every vector memory operation: vmcnt 0, expcnt and
+// lgkmcnt at their maxima (no wait)
+constexpr int kWaitVmem = 0x0F70;
+
+// dst[0, n) = src[0, n) by one wavefront, 16 loads per lane in flight before any LDS write (a loop that
+// loads one value and writes it before the next load costs one memory latency per 64 values)
+__device__ __forceinline__ void stage_lds(uint32_t *dst, const uint32_t *src, uint32_t n) {
+    constexpr uint32_t U = 16;
+    const uint32_t ln = lane();
+    for (uint32_t i0 = 0; i0 < n; i0 += 64 * U) {
+        uint32_t v[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            v[u] = src[min(i0 + u * 64 + ln, n - 1)];  // clamped, not branched: all U loads issue
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t i = i0 + u * 64 + ln;
+            if (i < n) dst[i] = v[u];
+        }
+    }
+}
 
 // A lane's reader of its block's bits: the two 64-bit words around the read position in registers
 // (hi, lo) and the next one already loading (nx), so each word's load has the decoding of the 64 bits
@@ -1198,6 +1220,10 @@ __device__ void decode_blocks(const DecodeArgs &a, const uint32_t *S_syms) {
     for (int l = 0; l < 17; ++l) {
         lim[l] = a.lim[(uint64_t)gr.table * 17 + l];
     }
+    // every load above is complete before the first change: otherwise the compiler, which cannot tell
+    // the first pass through the loop from the others, waits for these limits inside each change, and
+    // with them for every payload load and store issued since (vmcnt counts both, in order)
+    __builtin_amdgcn_s_waitcnt(kWaitVmem);
     uint64_t rel = 0;  // sum of (gap + 1) so far in this block
     // decodes change s of the block into out: zz | (block-relative local << 32); false once bad
     auto step = [&](uint32_t s, unsigned long long &out) {
@@ -1273,10 +1299,9 @@ __device__ void decode_blocks(const DecodeArgs &a, const uint32_t *S_syms) {
 template <bool LDS_SYMS>
 __global__ __launch_bounds__(64) void k_decode(DecodeArgs a) {
     CRX_DYNAMIC_LDS(uint32_t, dyn_lds);  // the symbols, then the tables' first indices, when they fit
-    const uint32_t ln = lane();
     if (LDS_SYMS) {
-        for (uint32_t i = ln; i < a.n_syms; i += 64) dyn_lds[i] = a.syms[i];
-        for (uint32_t i = ln; i < 17 * a.n_tables; i += 64) dyn_lds[a.n_syms + i] = a.off[i];
+        stage_lds(dyn_lds, a.syms, a.n_syms);
+        stage_lds(dyn_lds + a.n_syms, a.off, 17 * a.n_tables);
     }
     wave_fence();
     decode_blocks<LDS_SYMS>(a, dyn_lds);
@@ -1338,96 +1363,132 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
 // number of same-exponent elements before the slab.  Also lists the slab's exponent windows after
 // its first one (the select pass streams the slab once per window): windows of kSelWin exponents,
 // each starting at the lowest exponent with targets past the previous window.
-constexpr uint32_t kLocTiles = 2;  // slabs per wavefront: their searches share the lanes
+// The searches are chains of dependent loads, so the pass is bound by how many are in flight: each
+// wavefront takes kLocTiles slabs, packs the (slab, exponent) pairs that have a group into a list,
+// and each lane runs kLocPer of the list's searches side by side (their loads issued together).  The
+// LDS footprint stays small (6 KiB) so that many wavefronts are resident.
+constexpr uint32_t kLocTiles = 4;  // slabs per wavefront
+constexpr uint32_t kLocPer = 4;    // searches per lane in flight
 __global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
-    __shared__ uint4 arg[kLocTiles * 256];     // searches, packed: (target, next, group, slot = 256 u + exponent)
-    __shared__ uint32_t res[kLocTiles * 256];  // per slot: the first change at or past the slab (kNone: no group)
-    __shared__ uint8_t has[kLocTiles * 256];   // per slot: the slab holds at least one of its changes
-    __shared__ uint32_t before[kLocTiles];     // per slab: its tensor's changes positioned before it
-    const uint32_t ln = lane();
+    __shared__ uint32_t arg_g[kLocTiles * 256];          // the searches, packed: group
+    __shared__ uint16_t arg_s[kLocTiles * 256];          // and slot = 256 u + exponent
+    __shared__ unsigned long long hasw[kLocTiles * 4];   // per slab: bit k % 64 of word k / 64, exponent k has targets
+    __shared__ uint32_t before[kLocTiles];               // per slab: its tensor's changes positioned before it
+    __shared__ uint32_t last_of[kLocTiles];               // per slab: the last of its tensor
+    const uint32_t ln = lane(), tau0 = blockIdx.x * kLocTiles;
     // nothing written through yet, whether or not the select pass runs (k_commit reads these)
-    if (ln < kLocTiles && blockIdx.x * kLocTiles + ln < tiles) {
-        a.done[blockIdx.x * kLocTiles + ln] = 0;
-        a.multi[blockIdx.x * kLocTiles + ln] = 0;
+    if (ln < kLocTiles && tau0 + ln < tiles) {
+        a.done[tau0 + ln] = 0;
+        a.multi[tau0 + ln] = 0;
     }
     if (*a.bad) {  // an update already rejected: no records; rstart defined all the same
-        if (ln < kLocTiles && blockIdx.x * kLocTiles + ln < tiles) a.rstart[blockIdx.x * kLocTiles + ln] = 0;
+        if (ln < kLocTiles && tau0 + ln < tiles) a.rstart[tau0 + ln] = 0;
         if (ln == 0 && blockIdx.x == 0) a.rstart[tiles] = 0;
         return;
     }
-    if (ln < kLocTiles) before[ln] = 0;
     // slab u of the wavefront, exponents ln + 64 q: those with a group are packed into consecutive
-    // entries, so that the lower-bound searches (one per lane) take as few load instructions as the
-    // slabs have groups
+    // entries; the others have no first change (kNone).  All loads are issued before any is used.
+    uint32_t tt[kLocTiles];
+#pragma unroll
+    for (uint32_t u = 0; u < kLocTiles; ++u) tt[u] = a.tile_tensor[min(tau0 + u, tiles - 1)];
+    int32_t g[kLocTiles][4];
+#pragma unroll
+    for (uint32_t u = 0; u < kLocTiles; ++u)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) g[u][q] = a.group_of[(uint64_t)tt[u] * 256 + ln + 64 * q];
+    if (ln < kLocTiles) {
+        const TensorDesc &d = a.descs[a.tile_tensor[min(tau0 + ln, tiles - 1)]];
+        before[ln] = 0;
+        last_of[ln] = tau0 + ln + 1 >= d.tile_begin + d.n_tiles ? 1u : 0u;
+    }
+    if (ln < kLocTiles * 4) hasw[ln] = 0;
     uint32_t n_act = 0;
 #pragma unroll
     for (uint32_t u = 0; u < kLocTiles; ++u) {
-        const uint32_t tau = blockIdx.x * kLocTiles + u;
+        const uint32_t tau = tau0 + u;
         if (tau >= tiles) break;
-        const uint32_t t = a.tile_tensor[tau];
-        const bool last = tau + 1 >= a.descs[t].tile_begin + a.descs[t].n_tiles;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t k = ln + 64 * q;
-            const int32_t g = a.group_of[(uint64_t)t * 256 + k];
-            const uint32_t target = a.pre[(uint64_t)tau * 256 + k];
-            const uint32_t next = last ? kNone : a.pre[(uint64_t)(tau + 1) * 256 + k];
-            res[256 * u + k] = kNone;
-            has[256 * u + k] = 0;
-            const uint64_t m = ballot(g >= 0);
-            if (g >= 0) arg[n_act + mbcnt(m)] = make_uint4(target, next, (uint32_t)g, 256 * u + k);
+            if (g[u][q] < 0) ((uint32_t *)a.lb)[(uint64_t)tau * 256 + k] = kNone;
+            const uint64_t m = ballot(g[u][q] >= 0);
+            if (g[u][q] >= 0) {
+                arg_g[n_act + mbcnt(m)] = (uint32_t)g[u][q];
+                arg_s[n_act + mbcnt(m)] = (uint16_t)(256 * u + k);
+            }
             n_act += (uint32_t)__popcll(m);
         }
     }
     wave_fence();
-    for (uint32_t i0 = 0; i0 < n_act; i0 += 64) {
-        const bool on = i0 + ln < n_act;
-        uint4 x = make_uint4(0u, 0u, 0u, 0u);
-        uint32_t lo = 0, hi = 0, end = 0, vhi = kNone;  // vhi: local[hi] once hi has moved
-        uint32_t gbase = 0;
-        if (on) {
-            x = arg[i0 + ln];
-            const GroupDev gr = a.groups[x.z];
-            lo = gbase = gr.elem_base;
-            hi = end = gr.elem_base + gr.count;
+    for (uint32_t i0 = 0; i0 < n_act; i0 += 64 * kLocPer) {
+        uint32_t lo[kLocPer], hi[kLocPer], end[kLocPer], vhi[kLocPer], gb[kLocPer], tgt[kLocPer], nxt[kLocPer],
+            slot[kLocPer];
+        bool on[kLocPer];
+        GroupDev gr[kLocPer];
+#pragma unroll
+        for (uint32_t p = 0; p < kLocPer; ++p) {  // the searches' bounds: every load issued before any use
+            const uint32_t j = i0 + 64 * p + ln;
+            on[p] = j < n_act;
+            const uint32_t jj = on[p] ? j : n_act - 1;
+            slot[p] = arg_s[jj];
+            const uint32_t u = slot[p] >> 8, k = slot[p] & 255u, tau = tau0 + u;
+            gr[p] = a.groups[arg_g[jj]];
+            tgt[p] = a.pre[(uint64_t)tau * 256 + k];
+            // the count before the next slab (kNone for a tensor's last slab, whose row is read in its place)
+            nxt[p] = a.pre[(uint64_t)(last_of[u] ? tau : tau + 1) * 256 + k];
         }
-        while (__any(lo < hi)) {
-            if (lo < hi) {
-                const uint32_t mid = lo + ((hi - lo) >> 1), v = a.local[mid];
-                if (v < x.x) {
-                    lo = mid + 1;
-                } else {
-                    hi = mid;
-                    vhi = v;
-                }
+#pragma unroll
+        for (uint32_t p = 0; p < kLocPer; ++p) {
+            if (last_of[slot[p] >> 8]) nxt[p] = kNone;
+            lo[p] = gb[p] = gr[p].elem_base;
+            end[p] = gr[p].elem_base + gr[p].count;
+            hi[p] = on[p] ? end[p] : lo[p];
+            vhi[p] = kNone;
+        }
+        for (;;) {  // lower bounds of tgt in local[lo, hi), kLocPer at a time
+            bool any = false;
+#pragma unroll
+            for (uint32_t p = 0; p < kLocPer; ++p) any |= lo[p] < hi[p];
+            if (!__any(any)) break;
+            // some search is open, so the update has changes: every index below is one of them
+            uint32_t mid[kLocPer], v[kLocPer];
+#pragma unroll
+            for (uint32_t p = 0; p < kLocPer; ++p) {
+                mid[p] = lo[p] + ((hi[p] - lo[p]) >> 1);
+                v[p] = a.local[min(mid[p], a.n_changes - 1)];
+            }
+#pragma unroll
+            for (uint32_t p = 0; p < kLocPer; ++p) {
+                const bool open = lo[p] < hi[p], below = v[p] < tgt[p];
+                lo[p] = open && below ? mid[p] + 1 : lo[p];
+                vhi[p] = open && !below ? v[p] : vhi[p];  // local[hi] once hi has moved
+                hi[p] = open && !below ? mid[p] : hi[p];
             }
         }
-        if (on) {  // x.y, the count before the next slab, is kNone for a tensor's last slab
-            res[x.w] = lo;
-            has[x.w] = lo < end && (x.y == kNone || vhi < x.y);
-            atomicAdd(&before[x.w >> 8], lo - gbase);  // the group's changes before the slab
+#pragma unroll
+        for (uint32_t p = 0; p < kLocPer; ++p) {
+            if (on[p]) {
+                const uint32_t u = slot[p] >> 8, k = slot[p] & 255u;
+                ((uint32_t *)a.lb)[(uint64_t)(tau0 + u) * 256 + k] = lo[p];
+                if (lo[p] < end[p] && (nxt[p] == kNone || vhi[p] < nxt[p]))
+                    atomicOr(&hasw[4 * u + (k >> 6)], 1ULL << (k & 63));
+                atomicAdd(&before[u], lo[p] - gb[p]);  // the group's changes before the slab
+            }
         }
     }
     wave_fence();
-    for (uint32_t u = 0; u < kLocTiles; ++u) {
-        const uint32_t tau = blockIdx.x * kLocTiles + u;
-        if (tau >= tiles) break;
-        // the slab's records follow those of the slabs before it: of earlier tensors, then of its own
-        if (ln == 0) {
-            a.rstart[tau] = a.tchg[a.tile_tensor[tau]] + before[u];
+    if (ln == 0) {
+        for (uint32_t u = 0; u < kLocTiles; ++u) {
+            const uint32_t tau = tau0 + u;
+            if (tau >= tiles) break;
+            // the slab's records follow those of the slabs before it: of earlier tensors, then of its own
+            a.rstart[tau] = a.tchg[tt[u]] + before[u];
             if (tau + 1 == tiles) a.rstart[tiles] = a.tchg[a.n_tensors];
-        }
-        uint64_t w[4];  // bit ln of w[q]: exponent ln + 64 q has targets in this slab
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            ((uint32_t *)a.lb)[(uint64_t)tau * 256 + ln + 64 * q] = res[256 * u + ln + 64 * q];
-            w[q] = ballot(has[256 * u + ln + 64 * q] != 0);
-        }
-        if (ln == 0) {  // windows greedy from the lowest exponent with targets
+            const unsigned long long *w = &hasw[4 * u];  // windows greedy from the lowest exponent with targets
             auto first_at = [&](uint32_t from) -> uint32_t {  // lowest set bit at or past `from` (256: none)
                 for (uint32_t q = from >> 6; q < 4; ++q) {
-                    const uint64_t v = q == (from >> 6) ? w[q] & (~0ULL << (from & 63)) : w[q];
-                    if (v) return 64 * q + (uint32_t)__builtin_ctzll(v);
+                    const uint64_t x = q == (from >> 6) ? w[q] & (~0ULL << (from & 63)) : w[q];
+                    if (x) return 64 * q + (uint32_t)__builtin_ctzll(x);
                 }
                 return 256u;
             };

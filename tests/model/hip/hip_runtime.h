@@ -188,6 +188,8 @@ inline uint32_t simt_mbcnt_hi(uint32_t m, uint32_t acc) {
 #define __builtin_amdgcn_readlane(v, l) simt_readlane((v), (l))
 #define __builtin_amdgcn_readfirstlane(v) simt_readfirstlane((v))
 #define __builtin_amdgcn_fence(order, scope) simt_fence()
+// the emulator's memory operations complete when issued: a wait for them has nothing to wait for
+#define __builtin_amdgcn_s_waitcnt(imm) ((void)(imm))
 
 // Raw buffer loads: the hardware range check returns 0 for a load that does not lie wholly below
 // num_records bytes.
