@@ -487,17 +487,23 @@ def apply(weights: Mapping[str, torch.Tensor], u: Update, checksums: dict | None
     slab = int(_SLAB)
     hist_in, hist_out, bufs = [], [], []
     if keep:
+        # an entry is used for the same tensor object, unmodified since, with the same slab size and
+        # device, when the tensor's checksum is trusted too (one pass over the tensors)
+        fresh = []
         with _hist_lock:
             hg = _hist.get
-            found = [hg(id(a)) if c else None for a, c in zip(targets, has)]
-        # an entry is used for the same tensor object, unmodified since, with the same slab size and device
-        use = [e is not None and e[1] == v and e[3] == slab and e[0]() is a and e[4] == dev
-               for a, e, v in zip(targets, found, vers)]
-        bufs = [e[2] if u else None for e, u in zip(found, use)]
-        hist_in = [e[5] if u else 0 for e, u in zip(found, use)]
+            for i, (a, c, v) in enumerate(zip(targets, has, vers)):
+                e = hg(id(a)) if c else None
+                if e is not None and e[1] == v and e[3] == slab and e[4] == dev and e[0]() is a:
+                    bufs.append(e[2])
+                    hist_in.append(e[5])
+                else:
+                    bufs.append(None)
+                    hist_in.append(0)
+                    fresh.append(i)
         hist_out = list(hist_in)
         # tensors without usable counts: one allocation, sliced per tensor
-        fresh = [(i, L.crx_apply_hist_words(a.numel(), slab)) for i, (a, u) in enumerate(zip(targets, use)) if not u]
+        fresh = [(i, L.crx_apply_hist_words(targets[i].numel(), slab)) for i in fresh]
         if fresh:
             block = torch.empty(sum(w for _, w in fresh), dtype=torch.int32, device=dev)
             at, base = 0, block.data_ptr()

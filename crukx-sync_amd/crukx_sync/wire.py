@@ -159,6 +159,11 @@ for _n in NativeUpdate._FIELDS:
 del _n
 
 
+# The tensor names of the last update parsed, decoded: (their UTF-8 bytes, their ends, the list).  A run
+# sends the same tensors in every update, and decoding 339 names costs about 0.02 ms.  Replaced whole.
+_names_memo = None
+
+
 class ParsedUpdate(NativeUpdate):
     """An update parsed by the native library; fields are materialised on first access."""
 
@@ -194,11 +199,16 @@ class ParsedUpdate(NativeUpdate):
             ends, numels, chks = ((ctypes.c_uint64 * max(n, 1))() for _ in range(3))
             _native.raise_for(L.crx_update_headers(self._h, names, need.value, ctypes.byref(need), ends, numels,
                                                    chks), None)
-            raw = names.raw
-            out, start = [], 0
-            for i in range(n):
-                out.append(raw[start:ends[i]].decode("utf-8"))
-                start = ends[i]
+            raw, cut = names.raw, bytes(ends)
+            memo = _names_memo
+            if memo is not None and memo[0] == raw and memo[1] == cut:  # the same names as the last update
+                out = memo[2]
+            else:
+                out, start = [], 0
+                for i in range(n):
+                    out.append(raw[start:ends[i]].decode("utf-8"))
+                    start = ends[i]
+                globals()["_names_memo"] = (raw, cut, out)
             self._headers = (out, list(numels[:n]), list(chks[:n]))
         return self._headers
 

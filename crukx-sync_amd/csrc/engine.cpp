@@ -1258,8 +1258,9 @@ uint32_t apply_slab(int32_t slab_req) { return slab_size(slab_req); }
 struct ApplyShared {
     uint32_t *lim = nullptr, *off = nullptr, *syms = nullptr;
     uint32_t n_syms = 0, n_tables = 0;
-    uint64_t *pay = nullptr;
+    const uint64_t *pay = nullptr;  // the words holding the payload, from bit bit0 of the first
     uint64_t pay_words = 0;
+    uint32_t bit0 = 0;
     uint32_t *bb = nullptr;            // [blocks] bits of each block
     unsigned long long *boff = nullptr;  // [blocks + 1] first payload bit of each block
 };
@@ -1328,7 +1329,7 @@ PartCheck apply_part(const Update &u, const Layout &L, const ApplyPart &P, const
     hc.mark("apply_upload");
     Fork fork(s);
     DecodeArgs da{d_descs, sh.pay, sh.pay_words, sh.bb + P.b0, sh.boff + P.b0, B, d_groups, (uint32_t)G, bmap,
-                  sh.lim, sh.off, sh.syms, sh.n_syms, dz, blk_sum, bad, sh.n_tables};
+                  sh.lim, sh.off, sh.syms, sh.n_syms, dz, blk_sum, bad, sh.n_tables, sh.bit0};
     launch_decode(da, fork.aux);
     launch_scan_u64(blk_sum, B, blk_prefix, ar.get<unsigned long long>(scan_parts(B)), fork.aux);
 
@@ -1538,15 +1539,20 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
                               hipMemcpyDeviceToDevice, s));
     else
         HIP_OK(hipMemcpyAsync(sh.bb, u.block_table, 4 * B_all, hipMemcpyHostToDevice, s));
-    sh.pay_words = (u.payload_len + 7) / 8 + 2;
-    sh.pay = ar.get<uint64_t>(sh.pay_words);
-    // the copy fills whole words up to payload_len / 8; the rest (partial last word, two pad words) is zeroed
-    zero(sh.pay + u.payload_len / 8, sh.pay_words - u.payload_len / 8, s);
-    if (u.payload_len) {
-        if (payload_dev)
-            HIP_OK(hipMemcpyAsync(sh.pay, payload_dev, u.payload_len, hipMemcpyDeviceToDevice, s));
-        else
-            copy_from_host(reinterpret_cast<uint8_t *>(sh.pay), u.payload_host, u.payload_len, s);
+    if (payload_dev) {
+        // read in place: from the 8-byte aligned word holding the payload's first byte to the one holding
+        // its last (aligned words never cross a page, so these reads stay in the pages the payload is in)
+        const uintptr_t at = reinterpret_cast<uintptr_t>(payload_dev);
+        sh.pay = reinterpret_cast<const uint64_t *>(at & ~uintptr_t(7));
+        sh.bit0 = 8 * (uint32_t)(at & 7);
+        sh.pay_words = std::max<uint64_t>((u.payload_len + (at & 7) + 7) / 8, 1);
+    } else {
+        sh.pay_words = (u.payload_len + 7) / 8 + 2;
+        uint64_t *pay = ar.get<uint64_t>(sh.pay_words);
+        // the copy fills whole words up to payload_len / 8; the rest (partial last word, two pad words) is zeroed
+        zero(pay + u.payload_len / 8, sh.pay_words - u.payload_len / 8, s);
+        if (u.payload_len) copy_from_host(reinterpret_cast<uint8_t *>(pay), u.payload_host, u.payload_len, s);
+        sh.pay = pay;
     }
     sh.boff = ar.get<unsigned long long>(B_all + 1);
     launch_scan_u32(sh.bb, B_all, sh.boff, ar.get<unsigned long long>(scan_parts(B_all)), s);
@@ -1668,6 +1674,12 @@ int32_t crx_parse_prefix(const uint8_t *prefix, uint64_t prefix_len, uint64_t to
     *out = nullptr;
     *need = 0;
     try {
+        const uint64_t want = prefix_need(prefix, prefix_len, total_len);
+        if (want > prefix_len && prefix_len < total_len) {  // ask for more without an exception
+            *need = std::min(want, total_len);
+            if (err && errlen) std::snprintf(err, (size_t)errlen, "need %llu bytes", (unsigned long long)*need);
+            return CRX_INVALID;
+        }
         auto *h = new crx_update();
         try {
             parse(prefix, prefix_len, total_len, last_byte, h->u);

@@ -123,6 +123,74 @@ void put_varint(std::vector<uint8_t> &out, uint64_t v) {
     out.push_back((uint8_t)v);
 }
 
+uint64_t prefix_need(const uint8_t *d, uint64_t avail, uint64_t total) {
+    const uint64_t lim = std::min(avail, total);
+    uint64_t pos = 0;
+    bool out = false;  // the walk needs a byte past lim
+    auto byte = [&]() -> uint64_t {
+        if (pos >= lim) {
+            out = true;
+            return 0;
+        }
+        return d[pos++];
+    };
+    auto varint = [&]() -> uint64_t {
+        uint64_t v = 0;
+        for (int shift = 0; shift < 70 && !out; shift += 7) {
+            const uint64_t b = byte();
+            if (shift < 64) v |= (b & 0x7F) << shift;
+            if (!(b & 0x80)) return v;
+        }
+        return v;
+    };
+    auto skip = [&](uint64_t n) {
+        if (n > lim - std::min(lim, pos)) out = true;
+        else pos += n;
+    };
+    auto more = [&]() { return std::max(avail + 1, 2 * avail); };  // past the available bytes: at least this
+    // a prefix that is not an update of this version is left to parse, which rejects it
+    if (lim < 5 || std::memcmp(d, "CRXS", 4) != 0 || d[4] != kVersion) return avail;
+    skip(5);
+    const uint64_t n_tables = varint();
+    if (out) return more();
+    if (n_tables > 256) return avail;
+    for (uint64_t t = 0; t < n_tables; ++t) {
+        byte();
+        const uint64_t n_sym = varint();
+        if (out) return more();
+        if (n_sym > total) return avail;
+        for (uint64_t k = 0; k < n_sym && !out; ++k) {
+            varint();
+            byte();
+        }
+        if (out) return more();
+    }
+    const uint64_t n_tensors = varint();
+    if (out) return more();
+    if (n_tensors > total) return avail;
+    uint64_t blocks = 0;
+    for (uint64_t i = 0; i < n_tensors; ++i) {
+        skip(varint());  // name
+        varint();        // numel
+        skip(8);         // checksum
+        const uint64_t n_groups = varint();
+        if (out) return more();
+        if (n_groups > 256) return avail;
+        for (uint64_t g = 0; g < n_groups && !out; ++g) {
+            byte();
+            blocks = sat_add(blocks, n_blocks(varint()), total);
+            byte();
+        }
+        if (out) return more();
+    }
+    if (blocks > total / 4) return avail;
+    const uint64_t table_end = pos + 4 * blocks;
+    if (table_end + 1 > lim) return std::max(table_end + 10, avail + 1);  // the table and the payload length
+    pos = table_end;
+    varint();  // payload length
+    return out ? more() : pos;
+}
+
 // wire.py:126-212, check for check and in the same order.
 void parse(const uint8_t *data, uint64_t avail, uint64_t total, uint8_t last, Update &u) {
     Reader r{data, avail, total};

@@ -76,6 +76,14 @@ inline uint64_t n_blocks(uint64_t count) { return (count + kBlock - 1) / kBlock;
 // violation of the format's limits, NeedMore if the header or block table extends past `avail`.
 void parse(const uint8_t *data, uint64_t avail, uint64_t total, uint8_t last, Update &u);
 
+// The leading bytes that parse() reads of an update of `total` bytes (header, block table and payload
+// length), found by walking the same fields without checking them and without throwing: when the
+// first `avail` bytes do not hold them all, a number larger than `avail` (exact once the walk reaches
+// the block table); `avail` or less when they do, or when the walk cannot be followed (parse then
+// reports what it finds).  A first prefix that is too short then costs no exception (the process's
+// first C++ exception is slow to unwind: the unwinder first indexes every loaded library).
+uint64_t prefix_need(const uint8_t *data, uint64_t avail, uint64_t total);
+
 // LEB128 varint (wire.py:55-61); throws Invalid for values >= 2^63.
 void put_varint(std::vector<uint8_t> &out, uint64_t v);
 

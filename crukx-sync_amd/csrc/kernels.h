@@ -124,7 +124,9 @@ struct CodeArgs {
 
 struct DecodeArgs {
     const TensorDesc *descs;
-    const uint64_t *payload;        // big-endian byte stream, 8-byte aligned, zero padded
+    // the payload: a big-endian byte stream that starts bit0 bits into the 8-byte aligned word
+    // payload[0] and ends in payload[n_words - 1] (bits past its end are never decisive)
+    const uint64_t *payload;
     uint64_t n_words;
     const uint32_t *block_bits;
     const unsigned long long *block_off;
@@ -140,6 +142,7 @@ struct DecodeArgs {
     unsigned long long *blk_sum;    // [blocks] sum of (gap + 1) per block
     unsigned int *bad;
     uint32_t n_tables;              // tables: lim and off hold 17 entries each
+    uint32_t bit0;                  // first payload bit in payload[0] (0-56, a multiple of 8)
 };
 
 struct SelectArgs {

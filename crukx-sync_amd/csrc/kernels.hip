@@ -1211,7 +1211,7 @@ __device__ void decode_blocks(const DecodeArgs &a, const uint32_t *S_syms) {
     const uint64_t size = a.descs[gr.tensor].numel;
     const uint32_t rice = gr.rice;
     const uint64_t qmax = size >> rice;
-    uint64_t cur = a.block_off[b];
+    uint64_t cur = a.bit0 + a.block_off[b];
     const uint64_t end = cur + a.block_bits[b];
     bool bad = false;
     BitReader R;

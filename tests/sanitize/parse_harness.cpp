@@ -1,12 +1,14 @@
 // Runs the product's update parser (crukx-sync_amd/csrc/format.cpp) over a batch of inputs, each
-// parsed whole and as prefixes of several lengths, and prints one line per input.  Built with
+// parsed whole and as prefixes of several lengths (as crx_parse_prefix does: prefix_need first, parse
+// when the prefix holds what it needs), and prints one line per input.  Built with
 // AddressSanitizer and UndefinedBehaviorSanitizer by tests/test_parse_sanitized.py, which compares
 // the lines with the production library's crx_parse.
 //
 // Input file: repeated (u64 little-endian length, bytes).  Output line per input:
 //   <whole> | <prefix cut 0> | <cut 1> | <cut len/2> | <cut len-1>
-// where each outcome is "ok <tables> <tensors> <blocks> <changes> <payload offset> <payload len>",
-// "corrupt <message>", "invalid <message>" or "need <bytes>".
+// where each outcome is "ok <tables> <tensors> <blocks> <changes> <payload offset> <payload len>"
+// (the whole one followed by prefix_need of the whole input), "corrupt <message>", "invalid <message>"
+// or "need <bytes>".
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -35,6 +37,13 @@ std::string outcome(const uint8_t *data, uint64_t avail, uint64_t total, uint8_t
            std::to_string(u.payload_offset) + " " + std::to_string(u.payload_len);
 }
 
+// crx_parse_prefix's order: the walk first, asking for more without parsing
+std::string prefix_outcome(const uint8_t *data, uint64_t avail, uint64_t total, uint8_t last) {
+    const uint64_t want = crx::prefix_need(data, avail, total);
+    if (want > avail && avail < total) return "need " + std::to_string(std::min(want, total));
+    return outcome(data, avail, total, last);
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
@@ -57,11 +66,12 @@ int main(int argc, char **argv) {
         at += n;
         const uint8_t last = n ? in[n - 1] : 0;
         std::string line = outcome(in.get(), n, n, last);
+        if (line.rfind("ok ", 0) == 0) line += " " + std::to_string(crx::prefix_need(in.get(), n, n));
         for (uint64_t cut : {uint64_t(0), uint64_t(1), n / 2, n ? n - 1 : 0}) {
             if (cut > n) cut = n;
             std::unique_ptr<uint8_t[]> pre(new uint8_t[cut]);
             std::memcpy(pre.get(), in.get(), cut);
-            line += " | " + outcome(pre.get(), cut, n, last);
+            line += " | " + prefix_outcome(pre.get(), cut, n, last);
         }
         std::printf("%s\n", line.c_str());
     }
