@@ -1383,7 +1383,7 @@ PartCheck apply_part(const Update &u, const Layout &L, const ApplyPart &P, const
     unsigned int *ok = ar.get<unsigned int>(1);
     SelectArgs sa{d_descs, sd.tile_tensor, T, slab, hall, lb, d_gof, d_groups, local, rec, rstart, tchg, bad, more,
                   n_more, (uint32_t)std::min<uint64_t>(1024, (uint64_t)kSelMoreWindows * tiles), dz, sdelta, multi,
-                  done, (uint32_t)C, full};
+                  done, (uint32_t)C, blk_prefix, full};
     launch_locate(sa, tiles, s);
     // a dry pass marks every slab as one of several windows: the select pass then writes nothing, and
     // the verify pass takes every slab's checksum delta
@@ -1539,19 +1539,38 @@ void apply(const Update &u, const uint8_t *payload_dev, uint16_t *const *targets
                               hipMemcpyDeviceToDevice, s));
     else
         HIP_OK(hipMemcpyAsync(sh.bb, u.block_table, 4 * B_all, hipMemcpyHostToDevice, s));
-    if (payload_dev) {
-        // read in place: from the 8-byte aligned word holding the payload's first byte to the one holding
-        // its last (aligned words never cross a page, so these reads stay in the pages the payload is in)
-        const uintptr_t at = reinterpret_cast<uintptr_t>(payload_dev);
-        sh.pay = reinterpret_cast<const uint64_t *>(at & ~uintptr_t(7));
-        sh.bit0 = 8 * (uint32_t)(at & 7);
-        sh.pay_words = std::max<uint64_t>((u.payload_len + (at & 7) + 7) / 8, 1);
-    } else {
+    // A device-resident payload is read in place, in the 8-byte aligned words that hold it, when those
+    // words lie inside the allocation the update is in (the first one does: the update's header precedes
+    // the payload; the last one may reach past the update's end).  Otherwise, and from the host, it is
+    // copied into words of its own, zero-padded.
+    bool in_place = false;
+    if (payload_dev && u.payload_len) {
+        const uintptr_t at = reinterpret_cast<uintptr_t>(payload_dev), lead = at & 7;
+        const uint64_t words = (lead + u.payload_len + 7) / 8;
+        hipDeviceptr_t base = nullptr;
+        size_t size = 0;
+        if (hipMemGetAddressRange(&base, &size, reinterpret_cast<hipDeviceptr_t>(at)) == hipSuccess &&
+            at - lead >= reinterpret_cast<uintptr_t>(base) &&
+            at - lead + 8 * words <= reinterpret_cast<uintptr_t>(base) + size) {
+            in_place = true;
+            sh.pay = reinterpret_cast<const uint64_t *>(at - lead);
+            sh.bit0 = 8 * (uint32_t)lead;
+            sh.pay_words = words;
+        } else {
+            (void)hipGetLastError();  // an address the runtime does not know: copied instead
+        }
+    }
+    if (!in_place) {
         sh.pay_words = (u.payload_len + 7) / 8 + 2;
         uint64_t *pay = ar.get<uint64_t>(sh.pay_words);
         // the copy fills whole words up to payload_len / 8; the rest (partial last word, two pad words) is zeroed
         zero(pay + u.payload_len / 8, sh.pay_words - u.payload_len / 8, s);
-        if (u.payload_len) copy_from_host(reinterpret_cast<uint8_t *>(pay), u.payload_host, u.payload_len, s);
+        if (u.payload_len) {
+            if (payload_dev)
+                HIP_OK(hipMemcpyAsync(pay, payload_dev, u.payload_len, hipMemcpyDeviceToDevice, s));
+            else
+                copy_from_host(reinterpret_cast<uint8_t *>(pay), u.payload_host, u.payload_len, s);
+        }
         sh.pay = pay;
     }
     sh.boff = ar.get<unsigned long long>(B_all + 1);

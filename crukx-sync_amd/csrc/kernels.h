@@ -171,6 +171,7 @@ struct SelectArgs {
     uint8_t *multi;                 // [tiles] the slab has more than one window (k_locate)
     uint32_t *done;                 // [tiles] records written through by the select pass (zeroed by k_locate)
     uint32_t n_changes;
+    const unsigned long long *blk_prefix;  // [blocks + 1] sums of (gap + 1) over the blocks before each
     // [tiles] each slab's weighted sum for its tensor's checksum when the tensor is cold (no cached
     // checksum), else 0: completed by the slab's first window, which reads the weights before any
     // write (to the histogram pass's sum of the even rows, when that pass streamed the slab)

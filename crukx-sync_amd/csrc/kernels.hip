@@ -1368,7 +1368,7 @@ __global__ __launch_bounds__(256) void k_local_fix(BlockArgs a) {
 // and each lane runs kLocPer of the list's searches side by side (their loads issued together).  The
 // LDS footprint stays small (6 KiB) so that many wavefronts are resident.
 constexpr uint32_t kLocTiles = 4;  // slabs per wavefront
-constexpr uint32_t kLocPer = 4;    // searches per lane in flight
+constexpr uint32_t kLocPer = 2;    // searches per lane in flight
 __global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
     __shared__ uint32_t arg_g[kLocTiles * 256];          // the searches, packed: group
     __shared__ uint16_t arg_s[kLocTiles * 256];          // and slot = 256 u + exponent
@@ -1424,7 +1424,7 @@ __global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
         uint32_t lo[kLocPer], hi[kLocPer], end[kLocPer], vhi[kLocPer], gb[kLocPer], tgt[kLocPer], nxt[kLocPer],
             slot[kLocPer];
         bool on[kLocPer];
-        GroupDev gr[kLocPer];
+        uint32_t gcnt[kLocPer], gblk[kLocPer];  // the group's changes and first block
 #pragma unroll
         for (uint32_t p = 0; p < kLocPer; ++p) {  // the searches' bounds: every load issued before any use
             const uint32_t j = i0 + 64 * p + ln;
@@ -1432,18 +1432,80 @@ __global__ __launch_bounds__(64) void k_locate(SelectArgs a, uint32_t tiles) {
             const uint32_t jj = on[p] ? j : n_act - 1;
             slot[p] = arg_s[jj];
             const uint32_t u = slot[p] >> 8, k = slot[p] & 255u, tau = tau0 + u;
-            gr[p] = a.groups[arg_g[jj]];
+            const GroupDev *grp = &a.groups[arg_g[jj]];
+            gb[p] = grp->elem_base;
+            gcnt[p] = grp->count;
+            gblk[p] = grp->blk_base;
             tgt[p] = a.pre[(uint64_t)tau * 256 + k];
             // the count before the next slab (kNone for a tensor's last slab, whose row is read in its place)
             nxt[p] = a.pre[(uint64_t)(last_of[u] ? tau : tau + 1) * 256 + k];
         }
+        // Each search is first narrowed to one block of 256 changes.  Block j of a group holds the local
+        // indices [base_j, base_{j+1}), base_j = the decoder's block sums before it (blk_prefix), so the
+        // target lies in the last block with base_j <= target, and the first change at or past the target
+        // in that block: the block is estimated from the target's share of the group's range and checked
+        // with two loads (the blocks are bisected when the estimate misses), then bisected itself.
+        // (the group's local indices are below 2^32, so the block bases are taken mod 2^32)
+        uint32_t p0[kLocPer], span[kLocPer], nb[kLocPer], jlo[kLocPer], jhi[kLocPer];
 #pragma unroll
         for (uint32_t p = 0; p < kLocPer; ++p) {
             if (last_of[slot[p] >> 8]) nxt[p] = kNone;
-            lo[p] = gb[p] = gr[p].elem_base;
-            end[p] = gr[p].elem_base + gr[p].count;
-            hi[p] = on[p] ? end[p] : lo[p];
+            end[p] = gb[p] + gcnt[p];
             vhi[p] = kNone;
+            nb[p] = (gcnt[p] + 255u) / 256u;
+            p0[p] = (uint32_t)a.blk_prefix[gblk[p]];
+            span[p] = (uint32_t)a.blk_prefix[gblk[p] + nb[p]];
+        }
+        uint32_t e0[kLocPer], e1[kLocPer];
+#pragma unroll
+        for (uint32_t p = 0; p < kLocPer; ++p) {
+            span[p] -= p0[p];  // the group's range: its last change's local index + 1
+            const bool in = on[p] && tgt[p] < span[p];
+            const uint32_t je = in ? (uint32_t)min64((uint64_t)tgt[p] * nb[p] / span[p], nb[p] - 1) : 0u;
+            jlo[p] = je;
+            jhi[p] = in ? je + 1 : 0u;  // in: the block is in [jlo, jhi) once the estimate is checked
+            e0[p] = (uint32_t)a.blk_prefix[gblk[p] + je];
+            e1[p] = (uint32_t)a.blk_prefix[gblk[p] + je + 1];
+        }
+#pragma unroll
+        for (uint32_t p = 0; p < kLocPer; ++p) {
+            if (jhi[p]) {  // the estimate's block, or the side of it that holds the target
+                if (tgt[p] < e0[p] - p0[p]) {
+                    jhi[p] = jlo[p];
+                    jlo[p] = 0;
+                } else if (tgt[p] >= e1[p] - p0[p]) {
+                    jlo[p] = jlo[p] + 1;
+                    jhi[p] = nb[p];
+                }
+            }
+        }
+        for (;;) {  // the last block with base <= target, in [jlo, jhi) (base_jlo <= target)
+            bool any = false;
+#pragma unroll
+            for (uint32_t p = 0; p < kLocPer; ++p) any |= jhi[p] - jlo[p] > 1;
+            if (!__any(any)) break;
+            uint32_t mid[kLocPer], v[kLocPer];
+#pragma unroll
+            for (uint32_t p = 0; p < kLocPer; ++p) {
+                mid[p] = jlo[p] + ((jhi[p] - jlo[p]) >> 1);
+                v[p] = (uint32_t)a.blk_prefix[gblk[p] + mid[p]];
+            }
+#pragma unroll
+            for (uint32_t p = 0; p < kLocPer; ++p) {
+                if (jhi[p] - jlo[p] > 1) {
+                    if (v[p] - p0[p] <= tgt[p]) jlo[p] = mid[p];
+                    else jhi[p] = mid[p];
+                }
+            }
+        }
+#pragma unroll
+        for (uint32_t p = 0; p < kLocPer; ++p) {
+            if (jhi[p]) {  // the block's changes
+                lo[p] = gb[p] + 256u * jlo[p];
+                hi[p] = min(lo[p] + 256u, end[p]);
+            } else {  // no search, or every change of the group lies before the target
+                lo[p] = hi[p] = end[p];
+            }
         }
         for (;;) {  // lower bounds of tgt in local[lo, hi), kLocPer at a time
             bool any = false;

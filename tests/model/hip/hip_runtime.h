@@ -51,6 +51,7 @@ enum : int {
     hipErrorInvalidDevice = 101,
     hipErrorNotReady = 600,
 };
+typedef void *hipDeviceptr_t;
 typedef struct simt_stream *hipStream_t;
 typedef struct simt_event *hipEvent_t;
 enum hipMemcpyKind {
@@ -81,6 +82,13 @@ hipError_t hipHostFree(void *p);
 hipError_t hipMemcpyAsync(void *dst, const void *src, size_t bytes, hipMemcpyKind kind, hipStream_t s);
 hipError_t hipMemsetAsync(void *dst, int value, size_t bytes, hipStream_t s);
 hipError_t hipGetLastError();
+// the allocation holding an address: the model's memory is the host's, whose allocations it does not
+// track, so this answers that it does not know (callers then take their copying path)
+inline hipError_t hipMemGetAddressRange(hipDeviceptr_t *base, size_t *size, hipDeviceptr_t) {
+    *base = nullptr;
+    *size = 0;
+    return hipErrorInvalidValue;
+}
 hipError_t hipGetSymbolAddress(void **p, const void *symbol);
 const char *hipGetErrorString(hipError_t e);
 
