@@ -812,6 +812,7 @@ Ranked rank_changes(const Layout &L, uint32_t slab, hipStream_t s, Arena &ar, Ho
     R.full = ar.get<uint64_t>(tiles);
     R.sd = scan_buffers(ar, L, R.d_descs, ub.at<ScanChunk>(i_chunks), ub.at<uint32_t>(i_tcb), s);
     uint32_t *tot_all = ar.get<uint32_t>((uint64_t)T * 256), *tot_chg = ar.get<uint32_t>((uint64_t)T * 256);
+    uint32_t *csum_chg = ar.get<uint32_t>((uint64_t)R.sd.n_chunks * 256);  // the change counts' chunk sums
     R.d_groups = ar.get<GroupDev>((uint64_t)T * 256);
     R.gbase = ar.get<uint32_t>((uint64_t)T * 256);
     unsigned long long *gcnt = ar.get<unsigned long long>(2);
@@ -831,8 +832,8 @@ Ranked rank_changes(const Layout &L, uint32_t slab, hipStream_t s, Arena &ar, Ho
     unsigned int hovf1 = 0;
     unsigned long long gc[2];
     for (int pass = 0;; ++pass) {
-        launch_scan_tables(R.d_descs, R.hall, R.sd.chunks, R.sd.n_chunks, R.sd.tcb, T, R.sd.csum, tot_all, s);
-        launch_scan_tables(R.d_descs, R.hchg, R.sd.chunks, R.sd.n_chunks, R.sd.tcb, T, R.sd.csum, tot_chg, s);
+        const ScanTabs tabs{{R.hall, R.hchg}, {R.sd.csum, csum_chg}, {tot_all, tot_chg}};
+        launch_scan_tables(R.d_descs, tabs, 2, R.sd.chunks, R.sd.n_chunks, R.sd.tcb, T, s);
         launch_enc_groups(tot_chg, T, R.d_groups, R.gbase, gcnt, s);
         d2h(&hovf1, ovf, 1, s);
         d2h(gc, gcnt, 2, s);
@@ -1364,7 +1365,8 @@ PartCheck apply_part(const Update &u, const Layout &L, const ApplyPart &P, const
         ha.list = d_list;
         launch_hist(ha, (uint32_t)hist_list.size(), s);
     }
-    launch_scan_tables(d_descs, hall, sd.chunks, sd.n_chunks, sd.tcb, T, sd.csum, sizes, s);
+    const ScanTabs tabs{{hall, nullptr}, {sd.csum, nullptr}, {sizes, nullptr}};
+    launch_scan_tables(d_descs, tabs, 1, sd.chunks, sd.n_chunks, sd.tcb, T, s);
     fork.join();
     hc.mark("apply_pass_a");
 

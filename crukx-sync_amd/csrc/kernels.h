@@ -212,10 +212,15 @@ void launch_enc_rank(const EncRankArgs &a, uint32_t tiles, hipStream_t s);
 // Histograms of the listed slabs (all when a.list is null): n workgroups.
 void launch_hist(const HistArgs &a, uint32_t n, hipStream_t s);
 // Per-tensor exclusive scans over slabs of per-slab exponent tables, in place; slabs of tensors with
-// cached counts (descs: hist_in and not cold) are read from those counts.
-void launch_scan_tables(const TensorDesc *descs, uint32_t *h, const ScanChunk *chunks, uint32_t n_chunks,
-                        const uint32_t *tensor_chunk_begin, uint32_t n_tensors, uint32_t *csum, uint32_t *totals,
-                        hipStream_t s);
+// cached counts (descs: hist_in and not cold) are read from those counts.  n_tabs (1 or 2) tables of
+// the same layout are scanned by the same launches, each with its own chunk sums and totals.
+struct ScanTabs {
+    uint32_t *h[2];       // [tiles][256] tables, scanned in place
+    uint32_t *csum[2];    // [chunks][256] chunk sums of each
+    uint32_t *totals[2];  // [tensors][256] totals of each
+};
+void launch_scan_tables(const TensorDesc *descs, const ScanTabs &p, uint32_t n_tabs, const ScanChunk *chunks,
+                        uint32_t n_chunks, const uint32_t *tensor_chunk_begin, uint32_t n_tensors, hipStream_t s);
 void launch_enc_groups(const uint32_t *totals_chg, uint32_t n_tensors, GroupDev *groups, uint32_t *gbase,
                        unsigned long long *counters, hipStream_t s);
 void launch_place(const EncRankArgs &a, uint32_t tiles, const uint32_t *tile_tensor,

@@ -486,10 +486,14 @@ __device__ __forceinline__ const uint32_t *scan_src(const TensorDesc &td, const 
     return td.hist_in ? td.hist_in + (uint64_t)(t - td.tile_begin) * 256 : h + (uint64_t)t * 256;
 }
 
-__global__ __launch_bounds__(256) void k_scan_sum(const TensorDesc *descs, const uint32_t *h, const ScanChunk *ch,
-                                                  uint32_t *csum) {
-    const ScanChunk c = ch[blockIdx.x];
+// One or two tables are scanned by the same launches: workgroup i takes table i / n (n chunks or
+// tensors per table) and its chunk or tensor i mod n.
+__global__ __launch_bounds__(256) void k_scan_sum(const TensorDesc *descs, ScanTabs p, const ScanChunk *ch,
+                                                  uint32_t n_chunks) {
+    const uint32_t tab = blockIdx.x >= n_chunks, i = blockIdx.x - tab * n_chunks;
+    const ScanChunk c = ch[i];
     const TensorDesc td = descs[c.tensor];
+    const uint32_t *const h = p.h[tab];
     const uint32_t k = threadIdx.x;
     uint32_t s = 0;
     for (uint32_t t0 = c.tile_begin; t0 < c.tile_end; t0 += kScanBatch) {  // a batch of loads in flight
@@ -499,7 +503,7 @@ __global__ __launch_bounds__(256) void k_scan_sum(const TensorDesc *descs, const
 #pragma unroll
         for (uint32_t j = 0; j < kScanBatch; ++j) s += x[j];
     }
-    csum[(uint64_t)blockIdx.x * 256 + k] = s;
+    p.csum[tab][(uint64_t)i * 256 + k] = s;
 }
 
 // exclusive running sums of src column k over rows i0 .. i0 + n into dst (which may be src);
@@ -522,20 +526,23 @@ __device__ __forceinline__ uint32_t scan_column(Src src, Dst dst, uint32_t i0, u
     return run;
 }
 
-__global__ __launch_bounds__(256) void k_scan_mid(uint32_t *csum, const uint32_t *tcb, uint32_t *totals) {
-    const uint32_t t = blockIdx.x, k = threadIdx.x;
+__global__ __launch_bounds__(256) void k_scan_mid(ScanTabs p, const uint32_t *tcb, uint32_t n_tensors) {
+    const uint32_t tab = blockIdx.x >= n_tensors, t = blockIdx.x - tab * n_tensors, k = threadIdx.x;
+    uint32_t *const csum = p.csum[tab];
     auto row = [&](uint32_t i) { return csum + (uint64_t)i * 256; };
-    totals[(uint64_t)t * 256 + k] = scan_column(row, row, tcb[t], tcb[t + 1] - tcb[t], k, 0);
+    p.totals[tab][(uint64_t)t * 256 + k] = scan_column(row, row, tcb[t], tcb[t + 1] - tcb[t], k, 0);
 }
 
-__global__ __launch_bounds__(256) void k_scan_fin(const TensorDesc *descs, uint32_t *h, const ScanChunk *ch,
-                                                  const uint32_t *csum) {
-    const ScanChunk c = ch[blockIdx.x];
+__global__ __launch_bounds__(256) void k_scan_fin(const TensorDesc *descs, ScanTabs p, const ScanChunk *ch,
+                                                  uint32_t n_chunks) {
+    const uint32_t tab = blockIdx.x >= n_chunks, i = blockIdx.x - tab * n_chunks;
+    const ScanChunk c = ch[i];
     const TensorDesc td = descs[c.tensor];
+    uint32_t *const h = p.h[tab];
     const uint32_t k = threadIdx.x;
     auto src = [&](uint32_t t) { return scan_src(td, h, t); };
     auto dst = [&](uint32_t t) { return h + (uint64_t)t * 256; };
-    scan_column(src, dst, c.tile_begin, c.tile_end - c.tile_begin, k, csum[(uint64_t)blockIdx.x * 256 + k]);
+    scan_column(src, dst, c.tile_begin, c.tile_end - c.tile_begin, k, p.csum[tab][(uint64_t)i * 256 + k]);
 }
 
 // ================================================================== encode: groups and placement
@@ -2158,12 +2165,11 @@ void launch_enc_rank(const EncRankArgs &a, uint32_t tiles, hipStream_t s) {
 }
 void launch_hist(const HistArgs &a, uint32_t n, hipStream_t s) { CRX_LAUNCH("apply_hist", k_hist, n, 64, s, a); }
 
-void launch_scan_tables(const TensorDesc *descs, uint32_t *h, const ScanChunk *chunks, uint32_t n_chunks,
-                        const uint32_t *tensor_chunk_begin, uint32_t n_tensors, uint32_t *csum, uint32_t *totals,
-                        hipStream_t s) {
-    CRX_LAUNCH("scan_sum", k_scan_sum, n_chunks, 256, s, descs, h, chunks, csum);
-    CRX_LAUNCH("scan_mid", k_scan_mid, n_tensors, 256, s, csum, tensor_chunk_begin, totals);
-    CRX_LAUNCH("scan_fin", k_scan_fin, n_chunks, 256, s, descs, h, chunks, csum);
+void launch_scan_tables(const TensorDesc *descs, const ScanTabs &p, uint32_t n_tabs, const ScanChunk *chunks,
+                        uint32_t n_chunks, const uint32_t *tensor_chunk_begin, uint32_t n_tensors, hipStream_t s) {
+    CRX_LAUNCH("scan_sum", k_scan_sum, n_tabs * n_chunks, 256, s, descs, p, chunks, n_chunks);
+    CRX_LAUNCH("scan_mid", k_scan_mid, n_tabs * n_tensors, 256, s, p, tensor_chunk_begin, n_tensors);
+    CRX_LAUNCH("scan_fin", k_scan_fin, n_tabs * n_chunks, 256, s, descs, p, chunks, n_chunks);
 }
 
 void launch_enc_groups(const uint32_t *totals_chg, uint32_t n_tensors, GroupDev *groups, uint32_t *gbase,
