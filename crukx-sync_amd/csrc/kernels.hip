@@ -1616,25 +1616,14 @@ __device__ __forceinline__ uint32_t sel_count(const uint32_t *cnt, uint32_t c) {
     return s;
 }
 
-// The sparse list's windows write their slab's rows from the stream (kLines): the new bits of each
-// target, (new - old) mod 2^16, staged beside its rank, and every 128-byte half-row holding a target
-// stored whole from the row's registers.
-template <uint32_t CAP>
-constexpr bool kLines = CAP == kTgtCapSparse;
-
 template <uint32_t CAP>
 struct SelectLds {
     uint32_t cnt[(kWin + kSpare) * kSelCopies];  // running counts, kSelCopies copies (by lane)
     alignas(16) uint16_t list[CAP];                // slab ranks of the window's targets, per exponent in order
-    uint16_t delta[kLines<CAP> ? CAP : 1];          // kLines: each listed target's new bits - old bits
     union {
-        struct {
-            uint32_t slot[2 * kRow];  // streaming: in-row rank -> record high word; [kRow, 2 kRow): per lane
-            uint32_t patch[64];       // kLines: deltas of a row's targets taken one per lane, by element
-                                      // (lane l: element l low, l + 64 high); zero between rows
-        };
-        uint4 info[64];  // set-up, per lane (its window exponent; zero past kWin): {list begin, list end, change index - list
-                         // index, exponent count before the slab}
+        uint32_t slot[2 * kRow];  // streaming: in-row rank -> record high word; [kRow, 2 kRow): per lane
+        uint4 info[64];           // set-up, per lane (its window exponent; zero past kWin): {list begin, list end, change index - list
+                                  // index, exponent count before the slab}
     };
 };
 
@@ -1666,16 +1655,14 @@ __device__ __forceinline__ void stream_halves(const Slab &sl, const Rsrc &src, B
 
 template <uint32_t CAP, bool LDS_LIST, bool COLD>
 __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const TensorDesc &td, const Slab &sl, uint32_t kbase, SelectLds<CAP> &S,
-                            uint32_t nxt, uint32_t nd, uint32_t ci, const uint32_t cend, const uint32_t jofs, const uint32_t pre_k,
-                            uint32_t j, bool lines, uint64_t &fsum) {
-    // lane e, for window exponent e: nxt = slab rank of its next target (kFar: none left), nd = that
-    // target's new bits - old bits (LINES), ci = its change index, cend = the end of its changes, jofs =
-    // change index - list index (LDS list), pre_k = its count before the slab (HBM list).  j (uniform):
-    // the window's next record.  lines (uniform, LINES only): the rows are written from the stream.
+                            uint32_t nxt, uint32_t ci, const uint32_t cend, const uint32_t jofs, const uint32_t pre_k,
+                            uint32_t j, uint64_t &fsum) {
+    // lane e, for window exponent e: nxt = slab rank of its next target (kFar: none left), ci = that
+    // target's change index, cend = the end of its changes, jofs = change index - list index (LDS
+    // list), pre_k = its count before the slab (HBM list).  j (uniform): the window's next record.
     // COLD: the stream also sums the slab's weights for the tensor's checksum (codec.py:61-68) into
     // fsum, as it reads them before any write (the verdict's input when no checksum is cached): the odd
     // rows when the histogram pass streamed the slab (it summed the even ones), else every row.
-    constexpr bool LINES = LDS_LIST && kLines<CAP>;
     const uint32_t ln = lane();
     // Per 16-bit half, an element's key is (window index << 7) + (its lane's copy << 5): the counter's
     // byte offset << kCntShift, so one shift gives the address.  Exponents below the window wrap past
@@ -1689,11 +1676,6 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
         if (LDS_LIST) return S.list[min(c - jo, CAP - 1)];
         return a.local[c] - pr;
     };
-    // LINES: new bits - old bits of the target with change index c
-    auto tdelta = [&](uint32_t c, uint32_t jo) -> uint32_t {
-        if (LINES) return S.delta[min(c - jo, CAP - 1)];
-        return 0u;
-    };
     // Found targets become records, stored in the order found (rows in order) from record j on: the
     // change index c and the element's high word h = offset in the slab | bits << 16.  (Staging them
     // in LDS for one coalesced store per 64 measured slower than these sequential single stores: select
@@ -1701,15 +1683,6 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
     auto record = [&](uint32_t c, uint32_t h) -> unsigned long long {
         return (unsigned long long)c | ((unsigned long long)h << 32);
     };
-    // LINES: the slab's words for the row stores (the stream's own offsets), or a range of zero bytes,
-    // which drops every store: half-rows without targets, rows not wholly in the slab, and slabs not
-    // written from the stream
-    const Rsrc wr = slab_rsrc(td.frame, sl);
-    const Rsrc none = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(td.frame), (short)0, 0, 0x00020000);
-    if (LINES) {
-        S.patch[ln] = 0;
-        wave_fence();
-    }
 
     uint32_t prev = 0;  // exponent ln's count before the row
     WeightedSum cs;     // COLD: the checksum sum
@@ -1721,8 +1694,7 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
         u16x2 c = __builtin_elementwise_min(as16(o & 0x7F807F80u) - as16(kb), as16(sp));
         const uint32_t f = r * kRow + ln;  // the low element's offset; the high one's is f + 64
         uint32_t v = o;                    // COLD: the slab's own elements (zero outside it)
-        const bool full = row_full(sl, r);
-        if (!full) {
+        if (!row_full(sl, r)) {
             if (f < sl.f_lo || f >= sl.f_hi) {
                 c.x = as16(sp).x;
                 v &= 0xFFFF0000u;
@@ -1746,109 +1718,70 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
         const uint32_t s = sel_count(S.cnt, ln);  // exponent ln's count up to the row's end
         const uint32_t seen = prev;
         prev = s;
-        uint32_t dirty = 0;  // LINES (uniform): bit 0, the low half-row holds a target; bit 1, the high
-        uint32_t nw = o;     // LINES: the row's bits with its targets' new bits
-        // the row's targets: records, and (LINES) their new bits merged into nw
-        [&] {
-            uint64_t H = ballot(s > nxt);
-            if (!H) return;
-            wave_fence();
-            // window index << 7 of both elements (the copy term cleared)
-            const uint32_t kx = key & 0xFF80FF80u, c0 = kx & 0xFFFFu, c1 = kx >> 16;
-            // this lane's elements as records' high words: offset in the slab | bits << 16
-            const uint32_t w0 = (f - sl.f_lo) | (o << 16), w1 = (f + 64 - sl.f_lo) | (o & 0xFFFF0000u);
-            const uint32_t q = nxt - seen;  // in-row rank of the next target, for the exponents in H
-            const bool hit = s > nxt;       // this lane's exponent is in H
-            do {  // the next target of each exponent with targets in this row: exactly one element
-                const uint32_t k = (uint32_t)__builtin_ctzll(H), kk = k << 7;
-                const uint32_t qk = rdlane(q, k), ck = rdlane(ci, k);
-                const uint32_t dk = LINES ? rdlane(nd, k) : 0u;  // its new bits - old bits
-                const bool m0 = c0 == kk;
-                const uint64_t M0 = ballot(m0);
-                const uint32_t n0 = (uint32_t)__popcll(M0);  // exponent k's low elements in the row
-                if (qk < n0) {  // a low element: the one whose rank among them is qk
-                    if (m0 && mbcnt(M0) == qk) {
-                        a.rec[j] = record(ck, w0);
-                        if (LINES) nw = __builtin_bit_cast(uint32_t, as16(nw) + as16(dk));
-                    }
-                    dirty |= 1u;
-                } else {        // a high element: rank qk - n0 among the high ones
-                    const bool m1 = c1 == kk;
-                    const uint64_t M1 = ballot(m1);  // by every lane: a wave-wide vote
-                    if (m1 && mbcnt(M1) == qk - n0) {
-                        a.rec[j] = record(ck, w1);
-                        if (LINES) nw = __builtin_bit_cast(uint32_t, as16(nw) + as16(dk << 16));
-                    }
-                    dirty |= 2u;
-                }
-                ++j;
-                clear_bit(H, k);
-            } while (H);
-            if (hit) {  // every exponent that had one: its next target, lane-parallel
-                ++ci;
-                nxt = ci < cend ? target(ci, jofs, pre_k) : (uint32_t)kFar;
-                if (LINES) nd = tdelta(ci, jofs);
+        uint64_t H = ballot(s > nxt);
+        if (!H) return;
+        wave_fence();
+        // window index << 7 of both elements (the copy term cleared)
+        const uint32_t kx = key & 0xFF80FF80u, c0 = kx & 0xFFFFu, c1 = kx >> 16;
+        // this lane's elements as records' high words: offset in the slab | bits << 16
+        const uint32_t w0 = (f - sl.f_lo) | (o << 16), w1 = (f + 64 - sl.f_lo) | (o & 0xFFFF0000u);
+        const uint32_t q = nxt - seen;  // in-row rank of the next target, for the exponents in H
+        const bool hit = s > nxt;       // this lane's exponent is in H
+        do {  // the next target of each exponent with targets in this row: exactly one element
+            const uint32_t k = (uint32_t)__builtin_ctzll(H), kk = k << 7;
+            const uint32_t qk = rdlane(q, k), ck = rdlane(ci, k);
+            const bool m0 = c0 == kk;
+            const uint64_t M0 = ballot(m0);
+            const uint32_t n0 = (uint32_t)__popcll(M0);  // exponent k's low elements in the row
+            if (qk < n0) {  // a low element: the one whose rank among them is qk
+                if (m0 && mbcnt(M0) == qk) a.rec[j] = record(ck, w0);
+            } else {        // a high element: rank qk - n0 among the high ones
+                const bool m1 = c1 == kk;
+                const uint64_t M1 = ballot(m1);  // by every lane: a wave-wide vote
+                if (m1 && mbcnt(M1) == qk - n0) a.rec[j] = record(ck, w1);
             }
-            H = ballot(s > nxt);
-            if (!H) return;
-            // more targets of an exponent in this row (rare at low densities): publish its elements by
-            // in-row rank (other lanes write a slot of their own past the ranks) and take the rest one per
-            // lane; LINES: each taker posts its target's new bits at the element's place in the row patch
-            wave_fence();
-            do {
-                const uint32_t k = (uint32_t)__builtin_ctzll(H);
-                const uint32_t after = rdlane(s, k), seen_k = rdlane(seen, k), ke = rdlane(cend, k);
-                const uint32_t jo = LDS_LIST ? rdlane(jofs, k) : 0u, pr = LDS_LIST ? 0u : rdlane(pre_k, k);
-                uint32_t ck = rdlane(ci, k);
-                const bool m0 = c0 == (k << 7), m1 = c1 == (k << 7);
-                const uint64_t M0 = ballot(m0);
-                const uint32_t rr0 = mbcnt(M0), rr1 = (uint32_t)__popcll(M0) + mbcnt(ballot(m1));  // in-row ranks
-                S.slot[m0 ? rr0 : kRow + ln] = w0;
-                S.slot[m1 ? rr1 : kRow + ln] = w1;
-                wave_fence();
-                uint32_t n, tl;
-                do {  // one target per lane (64 more if all lanes take one); the takers are lanes 0 .. n-1
-                    const uint32_t c = ck + ln;
-                    tl = c < ke ? target(c, jo, pr) : (uint32_t)kFar;
-                    const bool take = c < ke && tl < after;  // never past the exponent's own targets
-                    n = (uint32_t)__popcll(ballot(take));
-                    if (take) {
-                        const uint32_t h = S.slot[tl - seen_k];
-                        a.rec[j + ln] = record(c, h);
-                        if (LINES) {  // the element's place in the row: (its offset in the slab + f_lo) mod 128
-                            const uint32_t e = ((h & 0xFFFFu) + sl.f_lo) & (kRow - 1);
-                            reinterpret_cast<uint16_t *>(S.patch)[2 * (e & 63u) + (e >> 6)] = (uint16_t)tdelta(c, jo);
-                        }
-                    }
-                    j += n;
-                    ck += n;
-                } while (n == 64);
-                const uint32_t tc = rdlane(tl, n);  // the first target not taken, or kFar
-                wave_fence();
-                if (ln == k) {
-                    nxt = tc;
-                    ci = ck;
-                    if (LINES) nd = tdelta(ck, jofs);
-                }
-                clear_bit(H, k);
-            } while (H);
-            if (LINES) {  // the posted new bits into the row, and the patch cleared for the next row
-                const uint32_t pt = S.patch[ln];
-                nw = __builtin_bit_cast(uint32_t, as16(nw) + as16(pt));
-                S.patch[ln] = 0;
-                if (ballot((pt & 0xFFFFu) != 0)) dirty |= 1u;
-                if (ballot(pt > 0xFFFFu)) dirty |= 2u;
-                wave_fence();
-            }
-        }();
-        if (LINES) {  // every row issues both stores (a fixed count keeps the loads' waits exact)
-            // (dirty is uniform: read from the first lane so that the resources are selected in scalar
-            // registers)
-            const uint32_t dm = (lines && full) ? __builtin_amdgcn_readfirstlane(dirty) : 0u;
-            const uint32_t rb = r * 256u;
-            __builtin_amdgcn_raw_buffer_store_b16((uint16_t)nw, (dm & 1u) ? wr : none, ln * 2u, rb, 0);
-            __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(nw >> 16), (dm & 2u) ? wr : none, ln * 2u, rb + 128u, 0);
+            ++j;
+            clear_bit(H, k);
+        } while (H);
+        if (hit) {  // every exponent that had one: its next target, lane-parallel
+            ++ci;
+            nxt = ci < cend ? target(ci, jofs, pre_k) : (uint32_t)kFar;
         }
+        H = ballot(s > nxt);
+        if (!H) return;
+        // more targets of an exponent in this row (rare at low densities): publish its elements by
+        // in-row rank (other lanes write a slot of their own past the ranks) and take the rest one per
+        // lane
+        wave_fence();
+        do {
+            const uint32_t k = (uint32_t)__builtin_ctzll(H);
+            const uint32_t after = rdlane(s, k), seen_k = rdlane(seen, k), ke = rdlane(cend, k);
+            const uint32_t jo = LDS_LIST ? rdlane(jofs, k) : 0u, pr = LDS_LIST ? 0u : rdlane(pre_k, k);
+            uint32_t ck = rdlane(ci, k);
+            const bool m0 = c0 == (k << 7), m1 = c1 == (k << 7);
+            const uint64_t M0 = ballot(m0);
+            const uint32_t rr0 = mbcnt(M0), rr1 = (uint32_t)__popcll(M0) + mbcnt(ballot(m1));  // in-row ranks
+            S.slot[m0 ? rr0 : kRow + ln] = w0;
+            S.slot[m1 ? rr1 : kRow + ln] = w1;
+            wave_fence();
+            uint32_t n, tl;
+            do {  // one target per lane (64 more if all lanes take one); the takers are lanes 0 .. n-1
+                const uint32_t c = ck + ln;
+                tl = c < ke ? target(c, jo, pr) : (uint32_t)kFar;
+                const bool take = c < ke && tl < after;  // never past the exponent's own targets
+                n = (uint32_t)__popcll(ballot(take));
+                if (take) a.rec[j + ln] = record(c, S.slot[tl - seen_k]);
+                j += n;
+                ck += n;
+            } while (n == 64);
+            const uint32_t tc = rdlane(tl, n);  // the first target not taken, or kFar
+            wave_fence();
+            if (ln == k) {
+                nxt = tc;
+                ci = ck;
+            }
+            clear_bit(H, k);
+        } while (H);
     });
     // every target of this window's exponents is found once its rank is passed: one still pending
     // lies past the slab's elements of its exponent (never so when the local indices were in range)
@@ -1864,13 +1797,10 @@ __device__ __forceinline__ uint32_t select_slab(const SelectArgs &a, const Tenso
 // back (they are in the records) if it does not verify, so a failed apply leaves the weights as they
 // were, as the reference's verify-then-write does (codec.py:703-707).  Writing here, while the other
 // waves of the chip are still streaming, takes the partial-sector writes off a pass of their own.
-// lines: the stream has already stored the rows lying wholly in the slab (whole 128-byte half-rows,
-// no read-modify-write in the memory system); only the targets of its first and last rows are stored
-// here.
 constexpr uint32_t kWritePer = 2;  // records per lane with their loads in flight together (registers: occupancy)
 
-__device__ void write_through(const SelectArgs &a, const TensorDesc &td, uint32_t tau, uint32_t lt, const Slab &sl,
-                              bool lines, uint32_t r0, uint32_t r1) {
+__device__ void write_through(const SelectArgs &a, const TensorDesc &td, uint32_t tau, uint32_t lt, uint32_t r0,
+                              uint32_t r1) {
     // this wave's record stores are complete, and its loads below see them
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -1901,8 +1831,7 @@ __device__ void write_through(const SelectArgs &a, const TensorDesc &td, uint32_
                 const uint32_t off = (uint32_t)(rc[u] >> 32) & 0xFFFFu, old = (uint32_t)(rc[u] >> 48);
                 const int32_t delta = (int32_t)(zz >> 1) ^ -(int32_t)(zz & 1);
                 const uint32_t nu = (uint32_t)((int32_t)old + delta) & 0xFFFF;
-                // lines: the stream stored the rows wholly in the slab; the others' targets are stored here
-                if (off < extent && !(lines && row_full(sl, (off + sl.f_lo) / kRow))) base[off] = (uint16_t)nu;
+                if (off < extent) base[off] = (uint16_t)nu;
                 d += (uint64_t)((int64_t)nu - (int64_t)old) * weight(first + off);
                 const uint32_t eo = (old >> 7) & 0xFF, en = (nu >> 7) & 0xFF;
                 if (eo != en && h) {  // the element moves between exponent counts of its slab
@@ -2045,27 +1974,13 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
                     const uint32_t x = x0 + 16 * ln + i;
                     if (x < total) S.list[x] = (uint16_t)(a.local[idx[i]] - sub[i]);
                 }
-                if (kLines<CAP>) {  // each target's new bits - old bits: (uint16) unzigzag(zz) (codec.py:698-700)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const uint32_t x = x0 + 16 * ln + i;
-                        if (x < total) {
-                            const uint32_t zz = (uint32_t)a.dz[idx[i]];
-                            S.delta[x] = (uint16_t)((int32_t)(zz >> 1) ^ -(int32_t)(zz & 1));
-                        }
-                    }
-                }
                 wave_fence();
             }
         }
         wave_fence();
         const uint4 inf = S.info[ln];  // lane ln: window exponent ln
         uint32_t first = (uint32_t)kFar;
-        uint32_t first_d = 0;  // its new bits - old bits (kLines)
-        if (inf.x < inf.y) {
-            first = in_lds ? S.list[inf.x] : a.local[inf.z + inf.x] - inf.w;
-            if (kLines<CAP> && in_lds) first_d = S.delta[inf.x];
-        }
+        if (inf.x < inf.y) first = in_lds ? S.list[inf.x] : a.local[inf.z + inf.x] - inf.w;
         wave_fence();
         for (uint32_t i = ln; i < (kWin + kSpare) * kSelCopies; i += 64) S.cnt[i] = 0;
         wave_fence();
@@ -2075,23 +1990,15 @@ __device__ __forceinline__ void select_window(const SelectArgs &a, uint32_t tau,
         const bool cold = ANYCOLD && kfirst == 256 && td.cold;
         uint64_t fsum = 0;
         uint32_t jend;
-        // a slab streamed once (its first window is its only one) is written from the stream where
-        // its list is in LDS (kLines), else by write_through alone
-        const bool single = kfirst == 256 && !a.multi[tau];
-        const bool lines = kLines<CAP> && __builtin_amdgcn_readfirstlane((uint32_t)(in_lds && single)) != 0u;  // uniform
         if (in_lds)
-            jend = cold ? select_slab<CAP, true, ANYCOLD>(a, td, sl, kbase, S, first, first_d, c_first, c_end, inf.z, inf.w, j,
-                                                          lines, fsum)
-                        : select_slab<CAP, true, false>(a, td, sl, kbase, S, first, first_d, c_first, c_end, inf.z, inf.w, j,
-                                                        lines, fsum);
+            jend = cold ? select_slab<CAP, true, ANYCOLD>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j, fsum)
+                        : select_slab<CAP, true, false>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j, fsum);
         else
-            jend = cold ? select_slab<CAP, false, ANYCOLD>(a, td, sl, kbase, S, first, 0u, c_first, c_end, inf.z, inf.w, j,
-                                                           false, fsum)
-                        : select_slab<CAP, false, false>(a, td, sl, kbase, S, first, 0u, c_first, c_end, inf.z, inf.w, j,
-                                                         false, fsum);
+            jend = cold ? select_slab<CAP, false, ANYCOLD>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j, fsum)
+                        : select_slab<CAP, false, false>(a, td, sl, kbase, S, first, c_first, c_end, inf.z, inf.w, j, fsum);
         if (kfirst == 256 && ln == 0) a.full[tau] = fsum + (cold && !td.hist_in ? a.full[tau] : 0);
-        // a slab streamed once: its checksum delta, exponent moves and the writes the stream left
-        if (single) write_through(a, td, tau, local_tile, sl, lines, j, jend);
+        // a slab streamed once (its first window is its only one) is written now
+        if (kfirst == 256 && !a.multi[tau]) write_through(a, td, tau, local_tile, j, jend);
     }
 }
 
