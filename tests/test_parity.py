@@ -140,6 +140,32 @@ def test_device_resident_bytes_and_apply(golden):
         assert torch.equal(w[k].cpu().view(torch.int16), new[k].view(torch.int16))
 
 
+def test_device_resident_update_at_every_byte_alignment_and_at_an_allocation_end():
+    """A device-resident update is applied wherever its bytes sit: the decoder reads the payload in
+    place from the 8-byte words around it (its first bit anywhere in a word), or from a padded copy
+    when the words past the payload's end lie outside the allocation (here: the update placed at the
+    very end of a tensor that has a device allocation of its own)."""
+    a, b = scenarios.rl_pair(300_000, seed=21)
+    upd = crukx_sync.encode_update_device({"w": a.cuda()}, {"w": b.cuda()})
+    n = upd.numel()
+    for shift in range(9):  # every offset of the payload within an aligned word, and one past
+        buf = torch.zeros(n + shift + 40, dtype=torch.uint8, device="cuda")
+        view = buf[shift:shift + n]
+        view.copy_(upd)
+        w = {"w": a.cuda()}
+        assert crukx_sync.apply_update(w, view).changed == int((a.view(torch.int16) != b.view(torch.int16)).sum())
+        assert torch.equal(w["w"].cpu().view(torch.int16), b.view(torch.int16)), shift
+    # large tensors get a device allocation of exactly their (rounded) size: the update's last byte is
+    # the allocation's last byte, so no aligned word past the payload may be read there
+    big = torch.empty(16 << 20, dtype=torch.uint8, device="cuda")
+    for cut in (0, 3, 5):
+        view = big[big.numel() - n - cut:big.numel() - cut]
+        view.copy_(upd)
+        w = {"w": a.cuda()}
+        crukx_sync.apply_update(w, view)
+        assert torch.equal(w["w"].cpu().view(torch.int16), b.view(torch.int16)), cut
+
+
 def test_device_resident_corruption_is_rejected():
     a, b = scenarios.rl_pair(20_000, seed=13)
     dev_upd = crukx_sync.encode_update_device({"w": a.cuda()}, {"w": b.cuda()})
