@@ -9,6 +9,7 @@
 // checks that every live lane of the wavefront reached the same point.
 #pragma once
 
+#include <sanitizer/allocator_interface.h>
 #include <sanitizer/asan_interface.h>
 
 #include <cstddef>
@@ -82,12 +83,19 @@ hipError_t hipHostFree(void *p);
 hipError_t hipMemcpyAsync(void *dst, const void *src, size_t bytes, hipMemcpyKind kind, hipStream_t s);
 hipError_t hipMemsetAsync(void *dst, int value, size_t bytes, hipStream_t s);
 hipError_t hipGetLastError();
-// the allocation holding an address: the model's memory is the host's, whose allocations it does not
-// track, so this answers that it does not know (callers then take their copying path)
-inline hipError_t hipMemGetAddressRange(hipDeviceptr_t *base, size_t *size, hipDeviceptr_t) {
-    *base = nullptr;
-    *size = 0;
-    return hipErrorInvalidValue;
+// the allocation holding an address: the model's memory is the host's, and the sanitizer's allocator
+// knows its blocks (an address outside every block: not known, as the runtime answers for memory it
+// did not allocate)
+inline hipError_t hipMemGetAddressRange(hipDeviceptr_t *base, size_t *size, hipDeviceptr_t p) {
+    const void *b = __sanitizer_get_allocated_begin(p);
+    if (!b) {
+        *base = nullptr;
+        *size = 0;
+        return hipErrorInvalidValue;
+    }
+    *base = const_cast<void *>(b);
+    *size = __sanitizer_get_allocated_size(b);
+    return hipSuccess;
 }
 hipError_t hipGetSymbolAddress(void **p, const void *symbol);
 const char *hipGetErrorString(hipError_t e);

@@ -225,6 +225,34 @@ def scenario_group_message() -> None:
     print(f"group message: {msgs}", flush=True)
 
 
+def scenario_device_offsets() -> None:
+    """A device-resident update applied from views at every byte offset within an 8-byte word (the
+    decoder then reads the payload in place, from the aligned words around it) and from the end of an
+    allocation of exactly its size (then from a padded copy, or in place when its last word ends
+    there): every access stays inside the update's allocation, and every apply is exact."""
+    import torch
+
+    import crukx_sync
+    import scenarios
+
+    a, b = scenarios.rl_pair(70_000, seed=21)
+    upd = crukx_sync.encode_update_device({"w": a}, {"w": b})
+    n = upd.numel()
+    views = []
+    for shift in range(9):
+        buf = torch.zeros(n + shift + 40, dtype=torch.uint8)
+        views.append(buf[shift:shift + n])
+    for cut in (0, 3, 5):
+        buf = torch.empty(n + cut, dtype=torch.uint8)  # the update at the very end of its allocation
+        views.append(buf[cut:])
+    for view in views:
+        view.copy_(upd)
+        w = {"w": a.clone()}
+        crukx_sync.apply_update(w, view)
+        assert torch.equal(w["w"].view(torch.int16), b.view(torch.int16))
+    print(f"device offsets: {len(views)} applies exact", flush=True)
+
+
 def scenario_parts() -> None:
     """The part-wise encode and apply (CRX_PART_ELEMENTS=60000: parts of one to three tensors) on the
     multi-tensor scenarios: the bytes equal the oracle's single-pass bytes (also with the sender's
@@ -280,7 +308,8 @@ def scenario_parts() -> None:
 
 
 SCENARIOS = {"parity": scenario_parity, "small4_flips": scenario_small4_flips, "rejected_early": scenario_rejected_early,
-             "group_message": scenario_group_message, "parts": scenario_parts}
+             "group_message": scenario_group_message, "parts": scenario_parts,
+             "device_offsets": scenario_device_offsets}
 
 if __name__ == "__main__":
     install()

@@ -62,6 +62,14 @@ def test_group_size_check_follows_the_slab_knob(model):
     assert "group has more changes than elements" in out
 
 
+def test_device_resident_update_read_in_place_at_any_offset(model):
+    """The decoder reads a device-resident payload in place from its aligned words when the update's
+    allocation covers them (the model's allocations are the sanitizer's, so a read past one is
+    reported), and from a copy when not."""
+    out = _run(model, "device_offsets")
+    assert "device offsets: 12 applies exact" in out
+
+
 def test_part_wise_encode_and_apply_match_the_oracle(model):
     """CRX_PART_ELEMENTS splits updates into parts of one to three tensors: the bytes are the oracle's
     single-pass bytes, chained applies with both caches are exact, and a corruption in the last part is
